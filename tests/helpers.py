@@ -1,0 +1,50 @@
+"""Tolerances and input builders shared by the parity tests.
+
+`assert_attention_close` keeps the reference's own tolerances
+(flash_attn_mps tests/reference.py:93-96): bf16 atol 2e-2 / rtol 5e-2, other
+dtypes atol 2e-3 / rtol 1e-2.  `assert_north_star` is the acceptance bar of
+this build for the benchmark configurations: max |out - oracle| <= 2e-3 for
+fp16, <= 1e-2 for bf16, and max |lse - oracle| <= 1e-4.
+"""
+import torch
+
+from oracle.attention import attention as attention_reference  # noqa: F401  (re-export)
+
+
+def assert_attention_close(actual, expected, dtype=torch.float16):
+    atol, rtol = (2e-2, 5e-2) if dtype == torch.bfloat16 else (2e-3, 1e-2)
+    torch.testing.assert_close(actual.detach().cpu().double(), expected.double(),
+                               atol=atol, rtol=rtol, check_dtype=False)
+
+
+NORTH_STAR_OUT_TOL = {torch.float16: 2e-3, torch.bfloat16: 1e-2, torch.float32: 1e-4}
+NORTH_STAR_LSE_TOL = 1e-4
+
+
+def max_abs(actual, expected, rows=None):
+    a = actual.detach().cpu().double()
+    e = expected.detach().cpu().double()
+    if rows is not None:
+        a, e = a[rows], e[rows]
+    finite = torch.isfinite(e)
+    both_inf = (~finite) & (a == e)
+    diff = torch.where(both_inf, torch.zeros_like(a), (a - e).abs())
+    return float(diff.max()) if diff.numel() else 0.0
+
+
+def assert_north_star(out, lse, ref_out, ref_lse, dtype, rows=None):
+    """rows: packed query indices checked (out rows / lse columns)."""
+    out_err = max_abs(out, ref_out, rows)
+    lse_a = lse.detach().cpu().double().transpose(0, 1)
+    lse_e = ref_lse.detach().cpu().double().transpose(0, 1)
+    lse_err = max_abs(lse_a, lse_e, rows)
+    assert out_err <= NORTH_STAR_OUT_TOL[dtype], f"max |out - oracle| = {out_err:.3e}"
+    assert lse_err <= NORTH_STAR_LSE_TOL, f"max |lse - oracle| = {lse_err:.3e}"
+    return out_err, lse_err
+
+
+def cu_from_lengths(lengths, device):
+    c = [0]
+    for n in lengths:
+        c.append(c[-1] + int(n))
+    return torch.tensor(c, dtype=torch.int32, device=device)

@@ -1,0 +1,62 @@
+"""C-ABI checks that need no GPU: libfa_gfx950.so loads, exports exactly the
+entry points declared in include/fa_gfx950.h, its argument structs have the
+sizes the ctypes mirrors assume, and invalid arguments are rejected before
+any HIP call."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from flash_attn_mps_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "fa_gfx950.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^(?:int|void|const char\*)\s+(fa_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_expected_entry_points():
+    names = declared_functions()
+    assert names == sorted(_lib.ENTRY_POINTS), names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_struct_sizes_match_c_layout():
+    lib = _lib.load()
+    sizes = (ctypes.c_int64 * 6)()
+    lib.fa_struct_sizes(sizes)
+    assert [ctypes.sizeof(s) for s in _lib.STRUCTS] == list(sizes)
+    assert lib.fa_abi_version() == _lib.ABI_VERSION
+
+
+@pytest.mark.parametrize("name,struct", [
+    ("fa_store_kvcache", _lib.StoreArgs), ("fa_append_kvcache", _lib.AppendArgs),
+    ("fa_rotary", _lib.RotaryArgs), ("fa_attn_fwd", _lib.AttnArgs),
+    ("fa_decode_fwd", _lib.AttnArgs), ("fa_prefill_fwd", _lib.AttnArgs),
+    ("fa_merge_pair", _lib.MergePairArgs), ("fa_merge_partials", _lib.MergePartialsArgs),
+])
+def test_null_arguments_are_rejected_before_launch(name, struct):
+    lib = _lib.load()
+    args = struct()   # all pointers NULL
+    if hasattr(args, "splits"):
+        args.splits = 1
+    rc = getattr(lib, name)(ctypes.byref(args), None)
+    assert rc == 1, rc          # FA_ERR_INVALID
+    assert lib.fa_last_error().decode().startswith(name)
+
+
+def test_supported_queries_reject_unsupported_combinations():
+    a = _lib.AttnArgs()
+    a.k_dtype = a.v_dtype = _lib.F32
+    a.head_dim_qk = a.head_dim_v = 100
+    a.heads_q = a.heads_k = 1
+    assert not _lib.supported("fa_decode_supported", a)
+    assert not _lib.supported("fa_prefill_supported", a)
