@@ -1,0 +1,299 @@
+"""Benchmark of the flash_attn_mps_amd hot path on one MI355X.
+
+Headline (`value`): bf16 causal varlen prefill TFLOP/s on BASELINE config 2
+(16 sequences, lengths U[256, 4096], Hq/Hkv = 16/8, d = 128, Qwen3-0.6B
+attention shape), one `flash_attn_varlen_func` call per step with Q/K/V
+resident in HBM.  Algorithmic FLOPs = sum over visible (query, key) pairs x
+Hq x 2 (Dqk + Dv), lower-right causal.
+
+Secondary lines (same JSON object, key "secondary"): paged bf16 decode
+(config 3, Llama-3-8B shape), paged FP8 decode with softcap + window
+(config 4, Gemma-2-9B shape), and the mixed chunked-prefill + decode DIFFKV
+call (config 5), each in algorithmic KV GB/s against 8 TB/s.
+
+Inputs are synthetic (seeded N(0,1)); lengths/tables come from
+torch.Generator().manual_seed(123 + cfg).  The CPU baseline times the fp32
+CPU oracle (tests' checker) on a bounded sample of config 2.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "flash-attn-mps_amd"))
+sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-secondary", action="store_true", help="only the headline prefill config")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--only", default="", help="comma list of configs to run (2,3,4,5)")
+    return p.parse_args()
+
+
+def cu_lengths(lengths, device):
+    import torch
+    c = torch.zeros(len(lengths) + 1, dtype=torch.int32)
+    c[1:] = torch.tensor(lengths, dtype=torch.int32).cumsum(0)
+    return c.to(device)
+
+
+def causal_pairs(q_lens, k_lens):
+    total = 0
+    for lq, lk in zip(q_lens, k_lens):
+        # rows i = 0..lq-1 see min(lk, lk - lq + i + 1) keys (lower-right)
+        first = lk - lq + 1
+        total += sum(max(0, min(lk, first + i)) for i in range(lq))
+    return total
+
+
+def time_calls(fn, steps, warmup):
+    """Warmup, then `steps` back-to-back calls bracketed by synchronize.
+    Returns (ms per step over the whole region, mean ms per call from per-call
+    events on the launching stream)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    region0 = torch.cuda.Event(enable_timing=True)
+    region1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    region0.record()
+    for i in range(steps):
+        starts[i].record()
+        fn()
+        ends[i].record()
+    region1.record()
+    torch.cuda.synchronize()
+    total = region0.elapsed_time(region1)
+    per_call = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
+    return total / steps, per_call[len(per_call) // 2]
+
+
+def config2(device, steps, warmup):
+    import torch
+    import flash_attn_mps_amd as fa
+    g = torch.Generator().manual_seed(123 + 2)
+    lengths = torch.randint(256, 4097, (16,), generator=g).tolist()
+    total = sum(lengths)
+    hq, hkv, d = 16, 8, 128
+    q = (torch.randn(total, hq, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
+    k = (torch.randn(total, hkv, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
+    v = (torch.randn(total, hkv, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
+    cu = cu_lengths(lengths, device)
+    maxlen = max(lengths)
+    out = torch.empty(total, hq, d, dtype=torch.bfloat16, device=device)
+
+    def step():
+        fa.flash_attn_varlen_func(q, k, v, cu, cu, maxlen, maxlen, causal=True, out=out)
+
+    ms, call_ms = time_calls(step, steps, warmup)
+    flops = causal_pairs(lengths, lengths) * hq * 2 * (d + d)
+    return dict(lengths=lengths, flops=flops, ms=ms, call_ms=call_ms,
+                tflops=flops / (ms * 1e-3) / 1e12, call_tflops=flops / (call_ms * 1e-3) / 1e12,
+                tensors=(q, k, v, cu))
+
+
+def paged_cache(ctx, page, hkv, d, dtype, device, gen_seed, scale=None, dv=None):
+    """K/V caches written by store_kvcache from a slot mapping whose block
+    table is a random permutation of a pool sized to the total tokens."""
+    import torch
+    import flash_attn_mps_amd as fa
+    g = torch.Generator().manual_seed(gen_seed)
+    dv = dv or d
+    pages_per = [(c + page - 1) // page for c in ctx]
+    pool = sum(pages_per)
+    perm = torch.randperm(pool, generator=g).to(torch.int32)
+    width = max(pages_per)
+    table = torch.zeros(len(ctx), width, dtype=torch.int32)
+    slots = []
+    start = 0
+    for b, (c, n) in enumerate(zip(ctx, pages_per)):
+        table[b, :n] = perm[start:start + n]
+        start += n
+        pos = torch.arange(c)
+        slots.append(table[b, pos // page] * page + pos % page)
+    slots = torch.cat(slots).to(torch.int32).to(device)
+    tokens = sum(ctx)
+    gdev = torch.Generator(device=device).manual_seed(gen_seed)
+    kx = torch.randn(tokens, hkv, d, generator=gdev, device=device, dtype=torch.float32).to(torch.bfloat16)
+    vx = torch.randn(tokens, hkv, dv, generator=gdev, device=device, dtype=torch.float32).to(torch.bfloat16)
+    kc = torch.empty(pool, page, hkv, d, dtype=dtype, device=device)
+    vc = torch.empty(pool, page, hkv, dv, dtype=dtype, device=device)
+    fa.store_kvcache(kx, vx, kc, vc, slots, k_scale=scale, v_scale=scale)
+    torch.cuda.synchronize()
+    del kx, vx
+    return kc, vc, table.to(device), slots
+
+
+def config3(device, steps, warmup):
+    import torch
+    import flash_attn_mps_amd as fa
+    g = torch.Generator().manual_seed(123 + 3)
+    ctx = torch.randint(512, 32769, (64,), generator=g).tolist()
+    hq, hkv, d, page = 32, 8, 128, 16
+    kc, vc, table, _ = paged_cache(ctx, page, hkv, d, torch.bfloat16, device, 123 + 3)
+    q = torch.randn(64, 1, hq, d, generator=g).to(torch.bfloat16).to(device)
+    lens = torch.tensor(ctx, dtype=torch.int32, device=device)
+
+    def step():
+        fa.flash_attn_with_kvcache(q, kc, vc, cache_seqlens=lens, block_table=table, causal=True)
+
+    ms, call_ms = time_calls(step, steps, warmup)
+    kv_bytes = sum(ctx) * hkv * 2 * d * 2
+    del kc, vc
+    return dict(kv_bytes=kv_bytes, ms=ms, call_ms=call_ms, gbs=kv_bytes / (ms * 1e-3) / 1e9,
+                call_gbs=kv_bytes / (call_ms * 1e-3) / 1e9)
+
+
+def config4(device, steps, warmup):
+    import torch
+    from flash_attn_mps_amd import vllm
+    g = torch.Generator().manual_seed(123 + 4)
+    ctx = torch.randint(1024, 8193, (128,), generator=g).tolist()
+    hq, hkv, d, page = 16, 8, 256, 16
+    scale = torch.empty(hkv).uniform_(0.01, 0.1, generator=g)
+    kc, vc, table, _ = paged_cache(ctx, page, hkv, d, torch.float8_e4m3fn, device, 123 + 4,
+                                   scale=scale.to(device))
+    q = torch.randn(128, hq, d, generator=g).to(torch.bfloat16).to(device)
+    cuq = torch.arange(129, dtype=torch.int32, device=device)
+    used = torch.tensor(ctx, dtype=torch.int32, device=device)
+    desc = scale.to(device).expand(128, hkv)
+    out = torch.empty(128, hq, d, dtype=torch.bfloat16, device=device)
+
+    def step():
+        vllm.flash_attn_varlen_func(q, kc, vc, 1, cuq, max(ctx), seqused_k=used, block_table=table,
+                                    causal=True, softcap=50.0, window_size=(4095, 0),
+                                    k_descale=desc, v_descale=desc, out=out)
+
+    ms, call_ms = time_calls(step, steps, warmup)
+    kv_bytes = sum(min(c, 4096) for c in ctx) * hkv * 2 * d * 1
+    del kc, vc
+    return dict(kv_bytes=kv_bytes, ms=ms, call_ms=call_ms, gbs=kv_bytes / (ms * 1e-3) / 1e9,
+                call_gbs=kv_bytes / (call_ms * 1e-3) / 1e9)
+
+
+def config5(device, steps, warmup):
+    import torch
+    from flash_attn_mps_amd import vllm
+    g = torch.Generator().manual_seed(123 + 5)
+    hq = hkv = 16
+    dqk, dv, page = 192, 128, 16
+    prefixes = torch.randint(0, 4097, (8,), generator=g).tolist()
+    dec_ctx = torch.randint(256, 16385, (120,), generator=g).tolist()
+    q_lens = [512] * 8 + [1] * 120
+    k_lens = [p + 512 for p in prefixes] + dec_ctx
+    kc, vc, table, _ = paged_cache(k_lens, page, hkv, dqk, torch.bfloat16, device, 123 + 5, dv=dv)
+    total_q = sum(q_lens)
+    q = torch.randn(total_q, hq, dqk, generator=g).to(torch.bfloat16).to(device)
+    sinks = torch.randn(hq, generator=g).to(device)
+    cuq = cu_lengths(q_lens, device)
+    used = torch.tensor(k_lens, dtype=torch.int32, device=device)
+    out = torch.empty(total_q, hq, dv, dtype=torch.bfloat16, device=device)
+
+    def step():
+        vllm.flash_attn_varlen_func(q, kc, vc, max(q_lens), cuq, max(k_lens), seqused_k=used,
+                                    block_table=table, causal=True, s_aux=sinks, out=out)
+
+    ms, call_ms = time_calls(step, steps, warmup)
+    dec_bytes = sum(dec_ctx) * hkv * (dqk + dv) * 2
+    chunk_bytes = sum(k_lens[:8]) * hkv * (dqk + dv) * 2
+    flops = causal_pairs(q_lens[:8], k_lens[:8]) * hq * 2 * (dqk + dv)
+    roof_ms = max(flops / (PEAK_BF16_TFLOPS * 1e12), (dec_bytes + chunk_bytes) / (PEAK_HBM_GBS * 1e9)) * 1e3
+    del kc, vc
+    return dict(kv_bytes=dec_bytes + chunk_bytes, flops=flops, ms=ms, call_ms=call_ms,
+                gbs=(dec_bytes + chunk_bytes) / (ms * 1e-3) / 1e9, roofline_ms=roof_ms,
+                frac=roof_ms / ms)
+
+
+def cpu_baseline(lengths, tensors):
+    """fp32 CPU oracle on the first sequences of config 2 (bounded sample)."""
+    import torch
+    from oracle.attention import attention as oracle_attention
+    q, k, v, _ = tensors
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    take = 2
+    sample = lengths[:take]
+    n = sum(sample)
+    qs, ks, vs = (t[:n].cpu() for t in (q, k, v))
+    cu = torch.zeros(take + 1, dtype=torch.int32)
+    cu[1:] = torch.tensor(sample).cumsum(0)
+    oracle_attention(qs, ks, vs, cu, cu, causal=True, dtype=torch.float32)   # warmup
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        oracle_attention(qs, ks, vs, cu, cu, causal=True, dtype=torch.float32)
+        times.append(time.perf_counter() - t0)
+    sec = sorted(times)[1]
+    flops = causal_pairs(sample, sample) * 16 * 2 * 256
+    return {"value": round(flops / sec / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"config 2 sequences 0-{take - 1} (lengths {sample}), fp32 oracle, median of 3"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one MI355X; --gpus must be 1 "
+                                   "(the kernels run on one GPU's share; see DESIGN.md for sharding)"}))
+        sys.exit(2)
+    import torch
+    device = torch.device("cuda", 0)
+    only = set(args.only.split(",")) if args.only else None
+    c2 = config2(device, args.steps, args.warmup)
+    line = {
+        "metric": "bf16 prefill TFLOP/s & paged-decode KV GB/s, % of MI355X roofline, 1 GPU",
+        "value": round(c2["tflops"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(c2["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded 0.5*N(0,1) Q/K/V, lengths from torch.Generator().manual_seed(125)",
+        "config": {"workload": "config 2: varlen causal prefill, 16 seqs L~U[256,4096], Hq/Hkv 16/8, d128 "
+                               "(Qwen3-0.6B attention)", "global_batch": 16, "seq_len": max(c2["lengths"]),
+                   "total_tokens": sum(c2["lengths"]), "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(c2["call_tflops"], 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(c2["call_tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "flops_per_launch": c2["flops"], "kernel_ms": round(c2["call_ms"], 4)},
+    }
+    secondary = {}
+    if not args.no_secondary:
+        for name, fn in (("3", config3), ("4", config4), ("5", config5)):
+            if only and name not in only:
+                continue
+            r = fn(device, args.steps, args.warmup)
+            entry = {"ms_per_step": round(r["ms"], 4), "kv_GBps": round(r["gbs"], 1)}
+            if name == "5":
+                entry.update(roofline_ms=round(r["roofline_ms"], 4), frac=round(r["frac"], 4),
+                             chunk_flops=r["flops"])
+            else:
+                entry.update(call_kv_GBps=round(r["call_gbs"], 1),
+                             frac_of_hbm=round(r["call_gbs"] / PEAK_HBM_GBS, 4), kv_bytes=r["kv_bytes"])
+            secondary["config" + name] = entry
+            torch.cuda.empty_cache()
+    line["secondary"] = secondary
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(c2["lengths"], c2["tensors"])
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,17 +1,426 @@
-// MFMA prefill entry points.  The gfx950 MFMA kernel is added in the next
-// change; until then every combination reports "not supported" and the
-// dispatcher runs the generic kernel.
+// MFMA FlashAttention prefill for gfx950 (bf16 / fp16, Dqk = Dv in {64, 128, 256}).
+//
+// Semantics follow the reference's fast path (flash_attn_mps/_attention.py:149-158,
+// flash_attn_mps/kernels/attention_fast.metal:103-597): packed or paged K/V, GQA,
+// lower-right causality, optional softcap, fp32 softmax and LSE.
+//
+// gfx950 design
+// * A workgroup is 4 waves; each wave owns NB x 32 query rows of one head, so a
+//   workgroup covers BM = 128 * NB rows.  K/V tiles of BN = 64 keys are staged
+//   in LDS (double buffered; the next tile's global loads are issued before the
+//   current tile's MFMAs).
+// * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16
+//   (A = K rows from LDS, B = Q^T held in registers for the whole kernel).  A
+//   lane then holds 32 keys of ONE query column, so the row max / row sum of
+//   the softmax are in-lane reductions plus one exchange with lane ^ 32.
+// * K rows are stored in LDS at row sigma(r) (bits 2 and 3 of r swapped) so
+//   that, in the score layout, every lane's 8 consecutive accumulator values
+//   are 8 consecutive keys.  Those 8 probabilities, rounded to bf16/fp16, are
+//   directly the B operand of O^T += V^T P^T; V is written transposed into LDS
+//   (V^T rows = head dims) so its A operand is one 16-byte LDS read.
+// * exp2 with softmax_scale*log2(e) folded into one FMA; the running max is
+//   only moved (and O rescaled) when a tile raises it by more than 2^8, which
+//   keeps probabilities <= 256 and skips almost all rescales.
+// * Workgroups are ordered heaviest query block first across all requests and
+//   heads (the causal triangle makes late query blocks the longest).
 #include "attn_common.h"
 
+namespace {
+
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+
+constexpr int PF_WAVES = 4;
+constexpr int PF_THREADS = 64 * PF_WAVES;
+constexpr int PF_BN = 64;          // keys per tile
+constexpr float PF_RESCALE = 8.0f; // log2 headroom before the running max moves
+
+template <typename T> FA_DEV f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c);
+template <> FA_DEV f32x16 mfma32<BF16T>(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <> FA_DEV f32x16 mfma32<F16T>(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// Two fp32 values -> one word of two 16-bit values (RNE).
+template <typename T> FA_DEV uint32_t pack2(float lo, float hi);
+template <> FA_DEV uint32_t pack2<BF16T>(float lo, float hi) {
+  bf16x2 v;
+  v[0] = (__bf16)lo;
+  v[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, v);
+}
+template <> FA_DEV uint32_t pack2<F16T>(float lo, float hi) {
+  f16x2 v;
+  v[0] = (_Float16)lo;
+  v[1] = (_Float16)hi;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Swap bits 2 and 3 of a row index (an involution).
+FA_DEV int sigma(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
+
+struct PrefillShape {
+  int n_qblocks;
+  int log2_page;   // paged K/V: page size = 1 << log2_page
+};
+
+template <typename T, int D, int NB, bool CAUSAL>
+__global__ __launch_bounds__(PF_THREADS, 1) void prefill_kernel(const fa_attn_args a, const PrefillShape shp) {
+  constexpr int BM = PF_WAVES * NB * 32;
+  constexpr int BN = PF_BN;
+  constexpr int KST = D / 16;                  // k-steps of the QK^T MFMA
+  constexpr int DB = D / 32;                   // 32-row blocks of O^T
+  constexpr int KLD = D + 8;                   // LDS row stride of K (elements)
+  constexpr int VLD = BN + 8;                  // LDS row stride of V^T
+  constexpr int KTILE = BN * KLD, VTILE = D * VLD;
+  constexpr int KCH = BN * D / 8 / PF_THREADS; // 16-byte K chunks per thread
+  constexpr int VUNITS = (BN / 4) * (D / 8);   // (4 keys x 8 dims) V units per tile
+  constexpr int VPT = (VUNITS + PF_THREADS - 1) / PF_THREADS;
+  static_assert(KCH >= 1 && BN * D / 8 % PF_THREADS == 0, "K staging shape");
+
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int64_t per_qb = a.batch * a.heads_q;
+  const int qb = shp.n_qblocks - 1 - (int)(blockIdx.x / per_qb);
+  const int64_t rem = blockIdx.x % per_qb;
+  const int64_t b = rem / a.heads_q;
+  const int h = (int)(rem - b * a.heads_q);
+  const RequestInfo r = load_request(a, b);
+  const int q0 = qb * BM;
+  if (q0 >= r.q_len) return;
+  const int kh = h / (int)(a.heads_q / a.heads_k);
+  const int off = r.k_len - r.q_len;   // absolute position of query row i is i + off
+  int kv_end = r.k_len;
+  if (CAUSAL) kv_end = min(kv_end, min(q0 + BM, r.q_len) - 1 + off + 1);
+  const int n_tiles = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
+
+  const T* __restrict__ Q = (const T*)nullptr;
+  (void)Q;
+  const uint16_t* qg = (const uint16_t*)a.q;
+  const uint16_t* kg = (const uint16_t*)a.k;
+  const uint16_t* vg = (const uint16_t*)a.v;
+
+  // Q^T operand for the whole kernel: lane holds Q[row][16kk + 8hh .. +8].
+  const int wq0 = q0 + wave * NB * 32;
+  u32x4 qop[NB][KST];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int row = wq0 + nb * 32 + l32;
+    const bool ok = row < r.q_len;
+    const uint16_t* qp = qg + ((int64_t)r.q_begin + row) * a.q_stride[0] + (int64_t)h * a.q_stride[1] + 8 * hh;
+#pragma unroll
+    for (int kk = 0; kk < KST; ++kk) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (ok) v = *(const u32x4*)(qp + 16 * kk);
+      qop[nb][kk] = v;
+    }
+  }
+
+  const bool paged = a.page_size != 0;
+  const int lp = shp.log2_page;
+  auto row_offset = [&](const int64_t* st, int key) -> int64_t {
+    if (paged) {
+      const int page = key >> lp;
+      const int64_t blk = a.block_table[b * a.bt_stride[0] + (int64_t)page * a.bt_stride[1]];
+      return blk * st[0] + (int64_t)(key - (page << lp)) * st[1] + (int64_t)kh * st[2];
+    }
+    return ((int64_t)r.k_base + key) * st[1] + (int64_t)kh * st[2];
+  };
+
+  u32x4 kreg[KCH];
+  u32x4 vreg[VPT][4];
+  auto load_tile = [&](int t0) {
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+      const int idx = tid + PF_THREADS * c;
+      const int row = idx / (D / 8), col8 = idx % (D / 8);
+      const int key = t0 + row;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (key < r.k_len) v = *(const u32x4*)(kg + row_offset(a.k_stride, key) + col8 * 8);
+      kreg[c] = v;
+    }
+#pragma unroll
+    for (int u = 0; u < VPT; ++u) {
+      const int uid = tid + PF_THREADS * u;
+      const int kgp = uid % (BN / 4), dc = uid / (BN / 4);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int key = t0 + 4 * kgp + rr;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (uid < VUNITS && key < r.k_len) v = *(const u32x4*)(vg + row_offset(a.v_stride, key) + dc * 8);
+        vreg[u][rr] = v;
+      }
+    }
+  };
+  auto store_tile = [&](int buf) {
+    uint16_t* kl = smem + buf * (KTILE + VTILE);
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+      const int idx = tid + PF_THREADS * c;
+      const int row = idx / (D / 8), col8 = idx % (D / 8);
+      *(u32x4*)(kl + sigma(row) * KLD + col8 * 8) = kreg[c];
+    }
+    uint16_t* vl = kl + KTILE;
+#pragma unroll
+    for (int u = 0; u < VPT; ++u) {
+      const int uid = tid + PF_THREADS * u;
+      if (uid >= VUNITS) continue;
+      const int kgp = uid % (BN / 4), dc = uid / (BN / 4);
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const uint32_t w0 = vreg[u][0][p], w1 = vreg[u][1][p], w2 = vreg[u][2][p], w3 = vreg[u][3][p];
+        uint2 even, odd;
+        even.x = (w0 & 0xffffu) | (w1 << 16);
+        even.y = (w2 & 0xffffu) | (w3 << 16);
+        odd.x = (w0 >> 16) | (w1 & 0xffff0000u);
+        odd.y = (w2 >> 16) | (w3 & 0xffff0000u);
+        *(uint2*)(vl + (8 * dc + 2 * p) * VLD + 4 * kgp) = even;
+        *(uint2*)(vl + (8 * dc + 2 * p + 1) * VLD + 4 * kgp) = odd;
+      }
+    }
+  };
+
+  const bool cap = a.softcap > 0.0f;
+  const float c_scale = a.softmax_scale * LOG2E;          // raw dot -> log2 units
+  const float cap_in = cap ? a.softmax_scale / a.softcap : 0.0f;
+  const float cap_out = a.softcap * LOG2E;
+
+  float m_run[NB], l_run[NB];
+  f32x16 o[DB][NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    m_run[nb] = -INFINITY;
+    l_run[nb] = 0.0f;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[db][nb][i] = 0.0f;
+  }
+
+  const bool wave_rows = wq0 < r.q_len;
+  const int wave_qabs_lo = wq0 + off;
+  const int wave_qabs_hi = min(wq0 + NB * 32, r.q_len) - 1 + off;
+
+  if (n_tiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (int j = 0; j < n_tiles; ++j) {
+    const int buf = j & 1;
+    const int t0 = j * BN;
+    if (j + 1 < n_tiles) load_tile(t0 + BN);
+    const bool active = wave_rows && (!CAUSAL || t0 <= wave_qabs_hi);
+    if (active) {
+      const uint16_t* kl = smem + buf * (KTILE + VTILE);
+      const uint16_t* vl = kl + KTILE;
+      f32x16 s[2][NB];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) s[kt][nb][i] = 0.0f;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const uint16_t* krow = kl + (32 * kt + l32) * KLD + 8 * hh;
+#pragma unroll
+        for (int kk = 0; kk < KST; ++kk) {
+          const u32x4 av = *(const u32x4*)(krow + 16 * kk);
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) s[kt][nb] = mfma32<T>(av, qop[nb][kk], s[kt][nb]);
+        }
+      }
+      const bool need_mask = (t0 + BN > r.k_len) || (CAUSAL && t0 + BN - 1 > wave_qabs_lo);
+      u32x4 pop[2][2][NB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        if (cap) {
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const float x = s[kt][nb][i] * cap_in;
+              const float e = fast_exp2(2.0f * LOG2E * x);
+              s[kt][nb][i] = cap_out * (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f));
+            }
+        }
+        if (need_mask) {
+          const int qabs = wq0 + nb * 32 + l32 + off;
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const int key = t0 + 32 * kt + 16 * (i >> 3) + 8 * hh + (i & 7);
+              const bool ok = key < r.k_len && (!CAUSAL || key <= qabs);
+              if (!ok) s[kt][nb][i] = -INFINITY;
+            }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kt][nb][i]);
+        mx = fmaxf(mx, shfl_xor_f(mx, 32));
+        const float cand = cap ? mx : mx * c_scale;
+        const bool need = cand > m_run[nb] + PF_RESCALE;
+        if (__any(need)) {
+          const float f = need ? fast_exp2(m_run[nb] - cand) : 1.0f;
+          if (need) m_run[nb] = cand;
+          l_run[nb] *= f;
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[db][nb][i] *= f;
+        }
+        const float mref = m_run[nb] == -INFINITY ? 0.0f : m_run[nb];
+        const float sc = cap ? 1.0f : c_scale;
+        float psum = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const float p = fast_exp2(fmaf(s[kt][nb][i], sc, -mref));
+            s[kt][nb][i] = p;
+            psum += p;
+          }
+        l_run[nb] += psum;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            u32x4 w;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) w[q] = pack2<T>(s[kt][nb][8 * c + 2 * q], s[kt][nb][8 * c + 2 * q + 1]);
+            pop[kt][c][nb] = w;
+          }
+      }
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int db = 0; db < DB; ++db) {
+            const u32x4 av = *(const u32x4*)(vl + (32 * db + l32) * VLD + 32 * kt + 16 * c + 8 * hh);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) o[db][nb] = mfma32<T>(av, pop[kt][c][nb], o[db][nb]);
+          }
+    }
+    if (j + 1 < n_tiles) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: O = O^T / l, LSE = m * ln2 + ln(l).
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const float lt = l_run[nb] + shfl_xor_f(l_run[nb], 32);
+    const int row = wq0 + nb * 32 + l32;
+    if (row < r.q_len) {
+      const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+      const int64_t tq = (int64_t)r.q_begin + row;
+      uint16_t* op = (uint16_t*)a.out + tq * a.out_stride[0] + (int64_t)h * a.out_stride[1] + 4 * hh;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          uint2 w;
+          w.x = pack2<T>(o[db][nb][4 * g] * inv, o[db][nb][4 * g + 1] * inv);
+          w.y = pack2<T>(o[db][nb][4 * g + 2] * inv, o[db][nb][4 * g + 3] * inv);
+          *(uint2*)(op + 32 * db + 8 * g) = w;
+        }
+      if (hh == 0)
+        a.lse[(int64_t)h * a.lse_stride[0] + tq * a.lse_stride[1]] =
+            lt > 0.0f ? m_run[nb] * LN2 + logf(lt) : -INFINITY;
+    }
+  }
+}
+
+template <int D> constexpr int nb_for() { return D <= 128 ? 2 : 1; }
+
+template <int D>
+constexpr size_t lds_bytes() {
+  return 2 * (size_t)(PF_BN * (D + 8) + D * (PF_BN + 8)) * sizeof(uint16_t);
+}
+
+using PrefillKernel = void (*)(fa_attn_args, PrefillShape);
+
+template <typename T, int D>
+PrefillKernel pick(bool causal) {
+  return causal ? prefill_kernel<T, D, nb_for<D>(), true> : prefill_kernel<T, D, nb_for<D>(), false>;
+}
+
+PrefillKernel select_prefill(const fa_attn_args& a, int* bm, size_t* lds) {
+  const int64_t d = a.head_dim_qk;
+  const bool bf = a.q_dtype == FA_BF16;
+  const bool causal = a.causal != 0;
+  switch (d) {
+    case 64: *bm = 128 * nb_for<64>(); *lds = lds_bytes<64>(); return bf ? pick<BF16T, 64>(causal) : pick<F16T, 64>(causal);
+    case 128: *bm = 128 * nb_for<128>(); *lds = lds_bytes<128>(); return bf ? pick<BF16T, 128>(causal) : pick<F16T, 128>(causal);
+    case 256: *bm = 128 * nb_for<256>(); *lds = lds_bytes<256>(); return bf ? pick<BF16T, 256>(causal) : pick<F16T, 256>(causal);
+    default: return nullptr;
+  }
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+bool prefill_ok(const fa_attn_args& a) {
+  if (!(a.q_dtype == a.k_dtype && a.k_dtype == a.v_dtype && a.v_dtype == a.out_dtype)) return false;
+  if (a.q_dtype != FA_BF16 && a.q_dtype != FA_F16) return false;
+  if (a.head_dim_qk != a.head_dim_v) return false;
+  if (a.head_dim_qk != 64 && a.head_dim_qk != 128 && a.head_dim_qk != 256) return false;
+  if (a.leftpad_k || a.alibi || a.sinks || a.q_descale || a.k_descale || a.v_descale) return false;
+  if (a.mask_kind != 0 || a.causal_by_batch || a.window_left != -1 || a.window_right != -1) return false;
+  if (a.num_splits != 1) return false;
+  if (a.q_stride[2] != 1 || a.k_stride[3] != 1 || a.v_stride[3] != 1 || a.out_stride[2] != 1) return false;
+  if (!aligned16(a.q) || !aligned16(a.k) || !aligned16(a.v) || ((uintptr_t)a.out & 7u)) return false;
+  for (int i = 0; i < 2; ++i)
+    if ((a.q_stride[i] * 2) % 16 || (a.out_stride[i] * 2) % 8) return false;
+  for (int i = a.page_size ? 0 : 1; i < 3; ++i)
+    if ((a.k_stride[i] * 2) % 16 || (a.v_stride[i] * 2) % 16) return false;
+  if (a.page_size) {
+    if (a.page_size < 16 || (a.page_size & (a.page_size - 1))) return false;
+  }
+  return true;
+}
+
+}  // namespace
+
 extern "C" int fa_prefill_supported(const fa_attn_args* a) {
-  (void)a;
-  return 0;
+  return a != nullptr && prefill_ok(*a);
 }
 
 extern "C" int fa_prefill_fwd(const fa_attn_args* a, void* stream) {
-  (void)stream;
   int rc = fa_validate_attn(a, "fa_prefill_fwd");
   if (rc) return rc;
-  fa_set_error("fa_prefill_fwd: combination not supported by the MFMA kernel");
-  return FA_ERR_UNSUPPORTED;
+  if (!prefill_ok(*a)) {
+    fa_set_error("fa_prefill_fwd: combination not supported by the MFMA kernel");
+    return FA_ERR_UNSUPPORTED;
+  }
+  if (a->total_q == 0) return FA_OK;
+  FA_REQUIRE(a->max_seqlen_q >= 1, "fa_prefill_fwd: max_seqlen_q must be positive");
+  int bm = 0;
+  size_t lds = 0;
+  const PrefillKernel kern = select_prefill(*a, &bm, &lds);
+  PrefillShape shp;
+  shp.n_qblocks = (int)fa_ceil_div(a->max_seqlen_q, bm);
+  shp.log2_page = 0;
+  if (a->page_size)
+    while ((1ll << shp.log2_page) < a->page_size) ++shp.log2_page;
+  const int64_t blocks = (int64_t)shp.n_qblocks * a->batch * a->heads_q;
+  FA_REQUIRE(blocks <= 0x7fffffffll, "fa_prefill_fwd: grid too large");
+  hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (err != hipSuccess) {
+    fa_set_error("fa_prefill_fwd: cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(err));
+    return FA_ERR_LAUNCH;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(PF_THREADS), lds, (hipStream_t)stream, *a, shp);
+  return fa_check_launch("fa_prefill_fwd");
 }

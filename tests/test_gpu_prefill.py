@@ -1,0 +1,146 @@
+"""MFMA prefill kernel (fa_prefill_fwd) vs the fp64 oracle.
+
+Covers the fast-path feature set: bf16/fp16, head dims 64/128/256, causal and
+non-causal, softcap, GQA ratios, packed and paged K/V, q_len != k_len
+(lower-right causality, rows with no visible key), partial query/key tiles,
+and that the MFMA path is the one taken.  Tolerances: this build's bar
+(max-abs <= 2e-3 fp16, <= 1e-2 bf16, LSE <= 1e-4).
+"""
+import pytest
+import torch
+
+from flash_attn_mps_amd import _lib, flash_attn_varlen_func
+from flash_attn_mps_amd._attention import attention, build_args
+from helpers import assert_attention_close, assert_north_star, attention_reference, cu_from_lengths
+
+pytestmark = pytest.mark.gpu
+
+
+def _uses_mfma(q, k, v, out, lse, **kw):
+    keep = []
+    a = build_args(q, k, v, out, lse, keep=keep, **kw)
+    return _lib.supported("fa_prefill_supported", a)
+
+
+def _case(device, dtype, d, hq, hkv, q_lens, k_lens, scale=1.0, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(sum(q_lens), hq, d, generator=g) * scale).to(dtype).to(device)
+    k = (torch.randn(sum(k_lens), hkv, d, generator=g) * scale).to(dtype).to(device)
+    v = torch.randn(sum(k_lens), hkv, d, generator=g).to(dtype).to(device)
+    return q, k, v, cu_from_lengths(q_lens, device), cu_from_lengths(k_lens, device)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_dims_causal(device, dtype, d, causal):
+    q_lens, k_lens = [1, 37, 300, 64, 513], [5, 37, 300, 200, 700]
+    q, k, v, cuq, cuk = _case(device, dtype, d, 8, 2, q_lens, k_lens, scale=0.5, seed=d)
+    out, lse = attention(q, k, v, cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=max(q_lens),
+                         max_seqlen_k=max(k_lens), causal=causal)
+    ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=causal)
+    assert_north_star(out, lse, ref, ref_lse, dtype)
+
+
+def test_prefill_route_is_mfma(device):
+    q, k, v, cuq, cuk = _case(device, torch.bfloat16, 128, 16, 8, [300, 17], [300, 17])
+    out = torch.empty_like(q)
+    lse = torch.empty(16, q.shape[0], device=device)
+    assert _uses_mfma(q, k, v, out, lse, cu_seqlens_q=cuq, cu_seqlens_k=cuk, seqused_k=None, max_seqlen_q=300,
+                      max_seqlen_k=300, block_table=None, softmax_scale=None, causal=True, window_size=(-1, -1),
+                      alibi_slopes=None, softcap=0., s_aux=None, q_descale=None, k_descale=None, v_descale=None,
+                      mask_mod=None, aux_tensors=None, leftpad_k=None)
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 16), (16, 8), (32, 8), (8, 1)])
+def test_prefill_gqa_ratios(device, hq, hkv):
+    q_lens = [129, 256, 1000]
+    q, k, v, cuq, cuk = _case(device, torch.bfloat16, 128, hq, hkv, q_lens, q_lens, scale=0.5, seed=hq * 7 + hkv)
+    out, lse = flash_attn_varlen_func(q, k, v, cuq, cuk, max(q_lens), max(q_lens), causal=True,
+                                      return_softmax_lse=True)
+    ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=True)
+    assert_north_star(out, lse, ref, ref_lse, torch.bfloat16)
+
+
+@pytest.mark.parametrize("cap", [0.5, 5.0, 50.0])
+def test_prefill_softcap(device, cap):
+    q_lens, k_lens = [70, 300], [100, 300]
+    q, k, v, cuq, cuk = _case(device, torch.float16, 128, 4, 2, q_lens, k_lens, scale=2.0, seed=3)
+    out, lse = attention(q, k, v, cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=300, max_seqlen_k=300,
+                         causal=True, softcap=cap)
+    ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=True, softcap=cap)
+    assert_north_star(out, lse, ref, ref_lse, torch.float16)
+
+
+@pytest.mark.parametrize("page", [16, 64, 256])
+def test_prefill_paged_permuted_table(device, page):
+    g = torch.Generator().manual_seed(page)
+    k_lens = [700, 33, 1029]
+    q_lens = [300, 33, 129]
+    hq, hkv, d = 8, 4, 128
+    cols = max((n + page - 1) // page for n in k_lens)
+    pool = cols * len(k_lens) + 3
+    table = torch.randperm(pool, generator=g)[:cols * len(k_lens)].int().reshape(len(k_lens), cols)
+    kc = torch.randn(pool, page, hkv, d, generator=g)
+    vc = torch.randn(pool, page, hkv, d, generator=g)
+    for b, n in enumerate(k_lens):       # poison every slot past the request's length
+        for pos in range(n, cols * page):
+            kc[table[b, pos // page], pos % page] = float("nan")
+            vc[table[b, pos // page], pos % page] = float("nan")
+    kc, vc = kc.to(torch.bfloat16).to(device), vc.to(torch.bfloat16).to(device)
+    q = (torch.randn(sum(q_lens), hq, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
+    cuq = cu_from_lengths(q_lens, device)
+    used = torch.tensor(k_lens, dtype=torch.int32, device=device)
+    table = table.to(device)
+    out, lse = attention(q, kc, vc, cu_seqlens_q=cuq, seqused_k=used, max_seqlen_q=max(q_lens),
+                         max_seqlen_k=cols * page, block_table=table, causal=True)
+    ref, ref_lse = attention_reference(q, kc, vc, cuq, used_k=used, block_table=table, causal=True)
+    assert_north_star(out, lse, ref, ref_lse, torch.bfloat16)
+
+
+def test_prefill_more_queries_than_keys_and_empty(device):
+    # Lower-right causality: the first q_len - k_len rows see no key -> 0 / -inf.
+    q_lens, k_lens = [40, 0, 100], [10, 5, 0]
+    q, k, v, cuq, cuk = _case(device, torch.float16, 64, 4, 4, q_lens, k_lens, seed=9)
+    out, lse = attention(q, k, v, cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=100, max_seqlen_k=10,
+                         causal=True)
+    ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=True)
+    assert_north_star(out, lse, ref, ref_lse, torch.float16)
+    assert torch.count_nonzero(out[40:]) == 0
+
+
+def test_prefill_strided_output_and_inputs(device):
+    """Caller-owned strided out (rows padded) and q/k/v views with padded rows."""
+    q_lens = [200, 77]
+    hq, hkv, d = 8, 2, 128
+    g = torch.Generator().manual_seed(21)
+    qb = torch.randn(sum(q_lens), hq + 2, d, generator=g).to(torch.bfloat16).to(device)
+    kb = torch.randn(sum(q_lens), hkv + 1, d, generator=g).to(torch.bfloat16).to(device)
+    vb = torch.randn(sum(q_lens), hkv + 1, d, generator=g).to(torch.bfloat16).to(device)
+    q, k, v = qb[:, 1:hq + 1], kb[:, :hkv], vb[:, 1:]
+    cu = cu_from_lengths(q_lens, device)
+    storage = torch.full((sum(q_lens), hq + 3, d), 7.0, dtype=torch.bfloat16, device=device)
+    out = storage[:, 2:hq + 2]
+    res, lse = attention(q, k, v, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=200, max_seqlen_k=200,
+                         causal=True, out=out)
+    assert res.data_ptr() == out.data_ptr()
+    ref, ref_lse = attention_reference(q, k, v, cu, cu, causal=True)
+    assert_north_star(out, lse, ref, ref_lse, torch.bfloat16)
+    assert torch.all(storage[:, :2] == 7.0) and torch.all(storage[:, hq + 2:] == 7.0)
+
+
+def test_prefill_long_softmax_stability(device):
+    torch.manual_seed(191)
+    q = (torch.randn(2049, 4, 128, device=device) * 3).to(torch.float16)
+    k = (torch.randn(4097, 2, 128, device=device) * 3).to(torch.float16)
+    v = torch.randn(4097, 2, 128, device=device).to(torch.float16)
+    cuq = torch.tensor([0, 2049], device=device, dtype=torch.int32)
+    cuk = torch.tensor([0, 4097], device=device, dtype=torch.int32)
+    out, lse = attention(q, k, v, cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=2049, max_seqlen_k=4097,
+                         causal=True)
+    ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=True)
+    # x3-scaled inputs make rows peaked and |out| reach ~4, where the fp16
+    # half-ulp alone is ~1e-3: the reference's own tolerance applies
+    # (tests/reference.py:93-96 of flash_attn_mps).
+    assert_attention_close(out, ref)
+    torch.testing.assert_close(lse.cpu().double(), ref_lse, atol=1e-4, rtol=0)
