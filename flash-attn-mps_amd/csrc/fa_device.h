@@ -145,6 +145,15 @@ FA_DEV float readlane_f(float x, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
 }
 
+// Wave-uniform read of memory that no kernel writes while it runs (block
+// tables, sequence metadata).  Reading through the constant address space
+// lets the compiler use a scalar load, which is tracked separately from the
+// vector-memory counter and so never forces a wait on in-flight K/V loads.
+FA_DEV int32_t load_invariant_i32(const int32_t* p, int64_t idx) {
+  typedef const __attribute__((address_space(4))) int32_t cint32;
+  return ((cint32*)p)[idx];
+}
+
 FA_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 FA_DEV float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 

@@ -36,8 +36,19 @@ typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
 
 constexpr int PF_WAVES = 4;
 constexpr int PF_THREADS = 64 * PF_WAVES;
-constexpr int PF_BN = 64;          // keys per tile
 constexpr float PF_RESCALE = 8.0f; // log2 headroom before the running max moves
+
+// Tile shape for head dims <= 128: NB 32-row query blocks per wave, KT
+// 32-key blocks per K/V tile, MINB workgroups per CU in the launch bounds.
+#ifndef FA_PF_NB
+#define FA_PF_NB 1
+#endif
+#ifndef FA_PF_KT
+#define FA_PF_KT 2
+#endif
+#ifndef FA_PF_MINB
+#define FA_PF_MINB 2
+#endif
 
 template <typename T> FA_DEV f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c);
 template <> FA_DEV f32x16 mfma32<BF16T>(u32x4 a, u32x4 b, f32x16 c) {
@@ -70,10 +81,10 @@ struct PrefillShape {
   int log2_page;   // paged K/V: page size = 1 << log2_page
 };
 
-template <typename T, int D, int NB, bool CAUSAL>
-__global__ __launch_bounds__(PF_THREADS, 1) void prefill_kernel(const fa_attn_args a, const PrefillShape shp) {
+template <typename T, int D, int NB, int KT, int MINB, bool CAUSAL>
+__global__ __launch_bounds__(PF_THREADS, MINB) void prefill_kernel(const fa_attn_args a, const PrefillShape shp) {
   constexpr int BM = PF_WAVES * NB * 32;
-  constexpr int BN = PF_BN;
+  constexpr int BN = 32 * KT;
   constexpr int KST = D / 16;                  // k-steps of the QK^T MFMA
   constexpr int DB = D / 32;                   // 32-row blocks of O^T
   constexpr int KLD = D + 8;                   // LDS row stride of K (elements)
@@ -108,7 +119,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void prefill_kernel(const fa_attn_ar
   const uint16_t* vg = (const uint16_t*)a.v;
 
   // Q^T operand for the whole kernel: lane holds Q[row][16kk + 8hh .. +8].
-  const int wq0 = q0 + wave * NB * 32;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);   // wave index as a scalar
+  const int wq0 = q0 + wave_u * NB * 32;
   u32x4 qop[NB][KST];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
@@ -122,9 +134,15 @@ __global__ __launch_bounds__(PF_THREADS, 1) void prefill_kernel(const fa_attn_ar
       qop[nb][kk] = v;
     }
   }
+  // Complete the Q loads here: otherwise the loop header cannot prove them
+  // done and every iteration would wait for all in-flight K/V loads before
+  // its first MFMA (s_waitcnt vmcnt(0); expcnt/lgkmcnt left unconstrained).
+  __builtin_amdgcn_s_waitcnt(0x0F70);
 
   const bool paged = a.page_size != 0;
   const int lp = shp.log2_page;
+  // Storage offset (elements) of key `key`; used per lane only when a wave's
+  // rows can span two 16-key groups (D = 64).
   auto row_offset = [&](const int64_t* st, int key) -> int64_t {
     if (paged) {
       const int page = key >> lp;
@@ -134,45 +152,101 @@ __global__ __launch_bounds__(PF_THREADS, 1) void prefill_kernel(const fa_attn_ar
     return ((int64_t)r.k_base + key) * st[1] + (int64_t)kh * st[2];
   };
 
+  // Staging layout.  K: 16-byte chunk c of a thread covers row r0 + lane/(D/8)
+  // (r0 uniform per wave) and columns 8*(lane % (D/8)).  V: unit u of a thread
+  // covers 4 keys x 8 dims with the dims fastest across lanes (coalesced
+  // global reads).  For D >= 128 every wave's rows of a chunk/unit lie inside
+  // one 16-key group, whose storage base is wave-uniform (one scalar block
+  // table read per group and tile); lanes add a 32-bit offset computed once.
+  constexpr int KROWS_W = 64 / (D / 8);
+  constexpr int VROWS_W = 4 * 64 / (D / 8);
+  constexpr bool UNIFORM = VROWS_W <= 16;
+  int kgrp[KCH], koff[KCH], kst[KCH];
+#pragma unroll
+  for (int c = 0; c < KCH; ++c) {
+    const int r0 = (64 * wave_u + PF_THREADS * c) / (D / 8);
+    const int row = r0 + lane / (D / 8), col8 = lane % (D / 8);
+    kgrp[c] = r0 & ~15;
+    koff[c] = 2 * ((row - kgrp[c]) * (int)a.k_stride[1] + col8 * 8);   // bytes
+    kst[c] = sigma(row) * KLD + col8 * 8;
+  }
+  int vgrp[VPT], voff[VPT][4], vst[VPT];
+  bool vunit[VPT];
+#pragma unroll
+  for (int u = 0; u < VPT; ++u) {
+    const int uid0 = 64 * wave_u + PF_THREADS * u;
+    const int uid = uid0 + lane;
+    const int kgp = uid / (D / 8), dc = uid % (D / 8);
+    vunit[u] = uid < VUNITS;
+    vgrp[u] = (4 * (uid0 / (D / 8))) & ~15;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) voff[u][rr] = 2 * ((4 * kgp + rr - vgrp[u]) * (int)a.v_stride[1] + dc * 8);
+    // V^T element (dim, key) lives at dim*VLD + 8*((key/8) ^ ((dim/8) & 7)) + key%8.
+    vst[u] = 8 * dc * VLD + 8 * ((kgp >> 1) ^ (dc & 7)) + 4 * (kgp & 1);
+  }
+  auto group_base = [&](const int64_t* st, int key0) -> int64_t {
+    if (paged) {
+      const int64_t blk = load_invariant_i32(a.block_table, b * a.bt_stride[0] + (int64_t)(key0 >> lp) * a.bt_stride[1]);
+      return blk * st[0] + (int64_t)(key0 & ((1 << lp) - 1)) * st[1] + (int64_t)kh * st[2];
+    }
+    return ((int64_t)r.k_base + key0) * st[1] + (int64_t)kh * st[2];
+  };
+
+  // K/V tiles are read with buffer loads.  Each 16-key group gets a scalar
+  // resource descriptor whose base is the group's first row and whose size
+  // ends with the last valid key of the request, so rows past the keys read
+  // as zero in hardware; lane offsets are loop-invariant registers.
   u32x4 kreg[KCH];
   u32x4 vreg[VPT][4];
+  uint32_t vmask = ~0u;
+  const int64_t safe_v = UNIFORM ? 0 : group_base(a.v_stride, 0);
+  auto group_rsrc = [&](const uint16_t* base, const int64_t* st, int key0, int row_elems) {
+    const int nvalid = min(max(r.k_len - key0, 0), 16);
+    const uint16_t* gptr = nvalid > 0 ? base + group_base(st, key0) : base;
+    const int bytes = nvalid > 0 ? 2 * ((nvalid - 1) * (int)st[1] + row_elems) : 0;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)gptr, (short)0, bytes, 0x00020000);
+  };
   auto load_tile = [&](int t0) {
 #pragma unroll
     for (int c = 0; c < KCH; ++c) {
-      const int idx = tid + PF_THREADS * c;
-      const int row = idx / (D / 8), col8 = idx % (D / 8);
-      const int key = t0 + row;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (key < r.k_len) v = *(const u32x4*)(kg + row_offset(a.k_stride, key) + col8 * 8);
-      kreg[c] = v;
+      const auto rsrc = group_rsrc(kg, a.k_stride, t0 + kgrp[c], D);
+      kreg[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, koff[c], 0, 0));
     }
 #pragma unroll
     for (int u = 0; u < VPT; ++u) {
-      const int uid = tid + PF_THREADS * u;
-      const int kgp = uid % (BN / 4), dc = uid / (BN / 4);
+      if (UNIFORM) {
+        const auto rsrc = group_rsrc(vg, a.v_stride, t0 + vgrp[u], D);
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int key = t0 + 4 * kgp + rr;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (uid < VUNITS && key < r.k_len) v = *(const u32x4*)(vg + row_offset(a.v_stride, key) + dc * 8);
-        vreg[u][rr] = v;
+        for (int rr = 0; rr < 4; ++rr)
+          vreg[u][rr] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff[u][rr], 0, 0));
+      } else {
+        // D = 64: a wave's V rows span two 16-key groups; per-lane addresses.
+        const int uid = 64 * wave_u + PF_THREADS * u + lane;
+        const int kgp = uid / (D / 8), dc = uid % (D / 8);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int key = t0 + 4 * kgp + rr;
+          const bool ok = vunit[u] && key < r.k_len;
+          vreg[u][rr] = *(const u32x4*)(vg + (ok ? row_offset(a.v_stride, key) : safe_v) + dc * 8);
+          vmask = ok ? (vmask | (1u << (4 * u + rr))) : (vmask & ~(1u << (4 * u + rr)));
+        }
       }
     }
   };
   auto store_tile = [&](int buf) {
+    const u32x4 zero = {0u, 0u, 0u, 0u};
     uint16_t* kl = smem + buf * (KTILE + VTILE);
 #pragma unroll
-    for (int c = 0; c < KCH; ++c) {
-      const int idx = tid + PF_THREADS * c;
-      const int row = idx / (D / 8), col8 = idx % (D / 8);
-      *(u32x4*)(kl + sigma(row) * KLD + col8 * 8) = kreg[c];
-    }
+    for (int c = 0; c < KCH; ++c) *(u32x4*)(kl + kst[c]) = kreg[c];
     uint16_t* vl = kl + KTILE;
 #pragma unroll
     for (int u = 0; u < VPT; ++u) {
-      const int uid = tid + PF_THREADS * u;
-      if (uid >= VUNITS) continue;
-      const int kgp = uid % (BN / 4), dc = uid / (BN / 4);
+      if (!vunit[u]) continue;
+      if (!UNIFORM) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          if (!((vmask >> (4 * u + rr)) & 1)) vreg[u][rr] = zero;
+      }
 #pragma unroll
       for (int p = 0; p < 4; ++p) {
         const uint32_t w0 = vreg[u][0][p], w1 = vreg[u][1][p], w2 = vreg[u][2][p], w3 = vreg[u][3][p];
@@ -181,11 +255,12 @@ __global__ __launch_bounds__(PF_THREADS, 1) void prefill_kernel(const fa_attn_ar
         even.y = (w2 & 0xffffu) | (w3 << 16);
         odd.x = (w0 >> 16) | (w1 & 0xffff0000u);
         odd.y = (w2 >> 16) | (w3 & 0xffff0000u);
-        *(uint2*)(vl + (8 * dc + 2 * p) * VLD + 4 * kgp) = even;
-        *(uint2*)(vl + (8 * dc + 2 * p + 1) * VLD + 4 * kgp) = odd;
+        *(uint2*)(vl + vst[u] + (2 * p) * VLD) = even;
+        *(uint2*)(vl + vst[u] + (2 * p + 1) * VLD) = odd;
       }
     }
   };
+  (void)KROWS_W;
 
   const bool cap = a.softcap > 0.0f;
   const float c_scale = a.softmax_scale * LOG2E;          // raw dot -> log2 units
@@ -222,30 +297,29 @@ __global__ __launch_bounds__(PF_THREADS, 1) void prefill_kernel(const fa_attn_ar
     if (active) {
       const uint16_t* kl = smem + buf * (KTILE + VTILE);
       const uint16_t* vl = kl + KTILE;
-      f32x16 s[2][NB];
+      f32x16 s[KT][NB];
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+      for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
           for (int i = 0; i < 16; ++i) s[kt][nb][i] = 0.0f;
+      const uint16_t* krow = kl + l32 * KLD + 8 * hh;
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        const uint16_t* krow = kl + (32 * kt + l32) * KLD + 8 * hh;
+      for (int kk = 0; kk < KST; ++kk)
 #pragma unroll
-        for (int kk = 0; kk < KST; ++kk) {
-          const u32x4 av = *(const u32x4*)(krow + 16 * kk);
+        for (int kt = 0; kt < KT; ++kt) {
+          const u32x4 av = *(const u32x4*)(krow + 32 * kt * KLD + 16 * kk);
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) s[kt][nb] = mfma32<T>(av, qop[nb][kk], s[kt][nb]);
         }
-      }
       const bool need_mask = (t0 + BN > r.k_len) || (CAUSAL && t0 + BN - 1 > wave_qabs_lo);
-      u32x4 pop[2][2][NB];
+      u32x4 pop[KT][2][NB];
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
         if (cap) {
 #pragma unroll
-          for (int kt = 0; kt < 2; ++kt)
+          for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
               const float x = s[kt][nb][i] * cap_in;
@@ -256,7 +330,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void prefill_kernel(const fa_attn_ar
         if (need_mask) {
           const int qabs = wq0 + nb * 32 + l32 + off;
 #pragma unroll
-          for (int kt = 0; kt < 2; ++kt)
+          for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
               const int key = t0 + 32 * kt + 16 * (i >> 3) + 8 * hh + (i & 7);
@@ -266,7 +340,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void prefill_kernel(const fa_attn_ar
         }
         float mx = -INFINITY;
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+        for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
           for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kt][nb][i]);
         mx = fmaxf(mx, shfl_xor_f(mx, 32));
@@ -285,7 +359,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void prefill_kernel(const fa_attn_ar
         const float sc = cap ? 1.0f : c_scale;
         float psum = 0.0f;
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+        for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const float p = fast_exp2(fmaf(s[kt][nb][i], sc, -mref));
@@ -294,7 +368,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void prefill_kernel(const fa_attn_ar
           }
         l_run[nb] += psum;
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+        for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
           for (int c = 0; c < 2; ++c) {
             u32x4 w;
@@ -304,12 +378,14 @@ __global__ __launch_bounds__(PF_THREADS, 1) void prefill_kernel(const fa_attn_ar
           }
       }
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+      for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
           for (int db = 0; db < DB; ++db) {
-            const u32x4 av = *(const u32x4*)(vl + (32 * db + l32) * VLD + 32 * kt + 16 * c + 8 * hh);
+            const int dim = 32 * db + l32;
+            const int chunk = (4 * kt + 2 * c + hh) ^ ((dim >> 3) & 7);
+            const u32x4 av = *(const u32x4*)(vl + dim * VLD + 8 * chunk);
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) o[db][nb] = mfma32<T>(av, pop[kt][c][nb], o[db][nb]);
           }
@@ -343,18 +419,21 @@ __global__ __launch_bounds__(PF_THREADS, 1) void prefill_kernel(const fa_attn_ar
   }
 }
 
-template <int D> constexpr int nb_for() { return D <= 128 ? 2 : 1; }
+template <int D> constexpr int nb_for() { return D <= 128 ? FA_PF_NB : 1; }
+template <int D> constexpr int kt_for() { return D <= 128 ? FA_PF_KT : 2; }
+template <int D> constexpr int minb_for() { return D <= 128 ? FA_PF_MINB : 1; }
 
 template <int D>
 constexpr size_t lds_bytes() {
-  return 2 * (size_t)(PF_BN * (D + 8) + D * (PF_BN + 8)) * sizeof(uint16_t);
+  return 2 * (size_t)(32 * kt_for<D>() * (D + 8) + D * (32 * kt_for<D>() + 8)) * sizeof(uint16_t);
 }
 
 using PrefillKernel = void (*)(fa_attn_args, PrefillShape);
 
 template <typename T, int D>
 PrefillKernel pick(bool causal) {
-  return causal ? prefill_kernel<T, D, nb_for<D>(), true> : prefill_kernel<T, D, nb_for<D>(), false>;
+  constexpr int NB = nb_for<D>(), KT = kt_for<D>(), MB = minb_for<D>();
+  return causal ? prefill_kernel<T, D, NB, KT, MB, true> : prefill_kernel<T, D, NB, KT, MB, false>;
 }
 
 PrefillKernel select_prefill(const fa_attn_args& a, int* bm, size_t* lds) {
