@@ -21,8 +21,10 @@
 // * exp2 with softmax_scale*log2(e) folded into one FMA; the running max is
 //   only moved (and O rescaled) when a tile raises it by more than 2^8, which
 //   keeps probabilities <= 256 and skips almost all rescales.
-// * Workgroups are ordered heaviest query block first across all requests and
-//   heads (the causal triangle makes late query blocks the longest).
+// * Work is ordered per XCD: each XCD runs whole (request, KV head) pairs one
+//   after another, query blocks heaviest-first within a pair (the causal
+//   triangle makes late blocks the longest), so resident workgroups share K/V
+//   in their XCD's L2.  K/V tiles are read with bounded buffer loads.
 #include "attn_common.h"
 
 namespace {
@@ -98,11 +100,20 @@ __global__ __launch_bounds__(PF_THREADS, MINB) void prefill_kernel(const fa_attn
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-  const int64_t per_qb = a.batch * a.heads_q;
-  const int qb = shp.n_qblocks - 1 - (int)(blockIdx.x / per_qb);
-  const int64_t rem = blockIdx.x % per_qb;
-  const int64_t b = rem / a.heads_q;
-  const int h = (int)(rem - b * a.heads_q);
+  // Work order.  Workgroups are dispatched round-robin over the 8 XCDs
+  // (XCD = blockIdx % 8), each with its own L2.  XCD x takes the (request,
+  // KV head) pairs p = x, x + 8, ... one after another, and within a pair the
+  // query blocks of its G query heads heaviest-first, so the workgroups
+  // resident on an XCD at any time share one pair's K/V in that XCD's L2.
+  const int G = (int)(a.heads_q / a.heads_k);
+  const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
+  const int per_pair = shp.n_qblocks * G;
+  const int64_t pair = (int64_t)(slot / per_pair) * 8 + xcd;
+  if (pair >= a.batch * a.heads_k) return;
+  const int rem = slot % per_pair;
+  const int qb = shp.n_qblocks - 1 - rem / G;
+  const int64_t b = pair / a.heads_k;
+  const int h = (int)(pair % a.heads_k) * G + rem % G;
   const RequestInfo r = load_request(a, b);
   const int q0 = qb * BM;
   if (q0 >= r.q_len) return;
@@ -181,8 +192,11 @@ __global__ __launch_bounds__(PF_THREADS, MINB) void prefill_kernel(const fa_attn
     vgrp[u] = (4 * (uid0 / (D / 8))) & ~15;
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) voff[u][rr] = 2 * ((4 * kgp + rr - vgrp[u]) * (int)a.v_stride[1] + dc * 8);
-    // V^T element (dim, key) lives at dim*VLD + 8*((key/8) ^ ((dim/8) & 7)) + key%8.
-    vst[u] = 8 * dc * VLD + 8 * ((kgp >> 1) ^ (dc & 7)) + 4 * (kgp & 1);
+    // V^T element (dim, key) lives at dim*VLD + 8*((key/8) ^ ((dim/16) & 7)) + key%8:
+    // with 64 LDS banks, 32 lanes writing 8 bytes (dims 8*dc + d, two key
+    // groups) and 16 lanes reading 16 bytes (16 consecutive dims) both hit
+    // distinct banks.
+    vst[u] = 8 * dc * VLD + 8 * ((kgp >> 1) ^ ((dc >> 1) & 7)) + 4 * (kgp & 1);
   }
   auto group_base = [&](const int64_t* st, int key0) -> int64_t {
     if (paged) {
@@ -200,22 +214,33 @@ __global__ __launch_bounds__(PF_THREADS, MINB) void prefill_kernel(const fa_attn
   u32x4 vreg[VPT][4];
   uint32_t vmask = ~0u;
   const int64_t safe_v = UNIFORM ? 0 : group_base(a.v_stride, 0);
-  auto group_rsrc = [&](const uint16_t* base, const int64_t* st, int key0, int row_elems) {
+  // Packed K/V: running address of each group's first key for the current
+  // tile, advanced by one tile per load (no per-tile 64-bit products).
+  const uint16_t* kcur[KCH];
+  const uint16_t* vcur[VPT];
+#pragma unroll
+  for (int c = 0; c < KCH; ++c) kcur[c] = kg + ((int64_t)r.k_base + kgrp[c]) * a.k_stride[1] + (int64_t)kh * a.k_stride[2];
+#pragma unroll
+  for (int u = 0; u < VPT; ++u) vcur[u] = vg + ((int64_t)r.k_base + vgrp[u]) * a.v_stride[1] + (int64_t)kh * a.v_stride[2];
+  const int64_t kstep = (int64_t)BN * a.k_stride[1], vstep = (int64_t)BN * a.v_stride[1];
+  auto group_rsrc = [&](const uint16_t* base, const uint16_t* packed_ptr, const int64_t* st, int key0, int row_elems) {
     const int nvalid = min(max(r.k_len - key0, 0), 16);
-    const uint16_t* gptr = nvalid > 0 ? base + group_base(st, key0) : base;
+    const uint16_t* gptr = paged ? (nvalid > 0 ? base + group_base(st, key0) : base) : packed_ptr;
     const int bytes = nvalid > 0 ? 2 * ((nvalid - 1) * (int)st[1] + row_elems) : 0;
     return __builtin_amdgcn_make_buffer_rsrc((void*)gptr, (short)0, bytes, 0x00020000);
   };
   auto load_tile = [&](int t0) {
 #pragma unroll
     for (int c = 0; c < KCH; ++c) {
-      const auto rsrc = group_rsrc(kg, a.k_stride, t0 + kgrp[c], D);
+      const auto rsrc = group_rsrc(kg, kcur[c], a.k_stride, t0 + kgrp[c], D);
+      kcur[c] += kstep;
       kreg[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, koff[c], 0, 0));
     }
 #pragma unroll
     for (int u = 0; u < VPT; ++u) {
       if (UNIFORM) {
-        const auto rsrc = group_rsrc(vg, a.v_stride, t0 + vgrp[u], D);
+        const auto rsrc = group_rsrc(vg, vcur[u], a.v_stride, t0 + vgrp[u], D);
+        vcur[u] += vstep;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr)
           vreg[u][rr] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff[u][rr], 0, 0));
@@ -384,7 +409,7 @@ __global__ __launch_bounds__(PF_THREADS, MINB) void prefill_kernel(const fa_attn
 #pragma unroll
           for (int db = 0; db < DB; ++db) {
             const int dim = 32 * db + l32;
-            const int chunk = (4 * kt + 2 * c + hh) ^ ((dim >> 3) & 7);
+            const int chunk = (4 * kt + 2 * c + hh) ^ ((dim >> 4) & 7);
             const u32x4 av = *(const u32x4*)(vl + dim * VLD + 8 * chunk);
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) o[db][nb] = mfma32<T>(av, pop[kt][c][nb], o[db][nb]);
@@ -493,7 +518,8 @@ extern "C" int fa_prefill_fwd(const fa_attn_args* a, void* stream) {
   shp.log2_page = 0;
   if (a->page_size)
     while ((1ll << shp.log2_page) < a->page_size) ++shp.log2_page;
-  const int64_t blocks = (int64_t)shp.n_qblocks * a->batch * a->heads_q;
+  const int64_t pairs = a->batch * a->heads_k;
+  const int64_t blocks = fa_ceil_div(pairs, 8) * 8 * shp.n_qblocks * (a->heads_q / a->heads_k);
   FA_REQUIRE(blocks <= 0x7fffffffll, "fa_prefill_fwd: grid too large");
   hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (err != hipSuccess) {
