@@ -1,14 +1,18 @@
-// MFMA FlashAttention prefill for gfx950 (bf16 / fp16, Dqk = Dv in {64, 128, 256}).
+// MFMA FlashAttention prefill for gfx950 (bf16 / fp16).
 //
 // Semantics follow the reference's fast path (flash_attn_mps/_attention.py:149-158,
-// flash_attn_mps/kernels/attention_fast.metal:103-597): packed or paged K/V, GQA,
-// lower-right causality, optional softcap, fp32 softmax and LSE.
+// flash_attn_mps/kernels/attention_fast.metal:103-597) plus the DIFFKV head
+// dims and attention sinks of its tiled path (flash_attn_mps/kernels/
+// attention.metal:60-181): packed or paged K/V, GQA, lower-right causality,
+// optional softcap, a per-head sink logit that joins the softmax
+// denominator only, fp32 softmax and natural-log LSE.  Head dims (Dqk, Dv)
+// in {(64,64), (128,128), (256,256), (192,128)}.
 //
 // gfx950 design
-// * A workgroup is 4 waves; each wave owns NB x 32 query rows of one head, so a
-//   workgroup covers BM = 128 * NB rows.  K/V tiles of BN = 64 keys are staged
-//   in LDS (double buffered; the next tile's global loads are issued before the
-//   current tile's MFMAs).
+// * A workgroup is W waves; each wave owns NB x 32 query rows of one head.
+//   K/V tiles of BN = 32*KT keys are staged in LDS, double buffered; the
+//   next tile's global loads are issued before the current tile's MFMAs and
+//   only waited for when that tile is written to LDS.
 // * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16
 //   (A = K rows from LDS, B = Q^T held in registers for the whole kernel).  A
 //   lane then holds 32 keys of ONE query column, so the row max / row sum of
@@ -17,14 +21,19 @@
 //   that, in the score layout, every lane's 8 consecutive accumulator values
 //   are 8 consecutive keys.  Those 8 probabilities, rounded to bf16/fp16, are
 //   directly the B operand of O^T += V^T P^T; V is written transposed into LDS
-//   (V^T rows = head dims) so its A operand is one 16-byte LDS read.
+//   (V^T rows = head dims, 16-byte key chunks XOR-swizzled) so its A operand
+//   is one 16-byte LDS read.
+// * K/V tiles are read with buffer loads: each 16-key group gets a scalar
+//   resource descriptor whose base is the group's first row and whose size
+//   ends at the request's last key, so rows past the keys read as zero in
+//   hardware and lane offsets are loop-invariant registers.
 // * exp2 with softmax_scale*log2(e) folded into one FMA; the running max is
 //   only moved (and O rescaled) when a tile raises it by more than 2^8, which
 //   keeps probabilities <= 256 and skips almost all rescales.
 // * Work is ordered per XCD: each XCD runs whole (request, KV head) pairs one
 //   after another, query blocks heaviest-first within a pair (the causal
 //   triangle makes late blocks the longest), so resident workgroups share K/V
-//   in their XCD's L2.  K/V tiles are read with bounded buffer loads.
+//   in their XCD's L2.
 #include "attn_common.h"
 
 namespace {
@@ -36,21 +45,7 @@ typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
 
-constexpr int PF_WAVES = 4;
-constexpr int PF_THREADS = 64 * PF_WAVES;
-constexpr float PF_RESCALE = 8.0f; // log2 headroom before the running max moves
-
-// Tile shape for head dims <= 128: NB 32-row query blocks per wave, KT
-// 32-key blocks per K/V tile, MINB workgroups per CU in the launch bounds.
-#ifndef FA_PF_NB
-#define FA_PF_NB 1
-#endif
-#ifndef FA_PF_KT
-#define FA_PF_KT 2
-#endif
-#ifndef FA_PF_MINB
-#define FA_PF_MINB 2
-#endif
+constexpr float PF_RESCALE = 8.0f;  // log2 headroom before the running max moves
 
 template <typename T> FA_DEV f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c);
 template <> FA_DEV f32x16 mfma32<BF16T>(u32x4 a, u32x4 b, f32x16 c) {
@@ -83,23 +78,59 @@ struct PrefillShape {
   int log2_page;   // paged K/V: page size = 1 << log2_page
 };
 
-template <typename T, int D, int NB, int KT, int MINB, bool CAUSAL>
-__global__ __launch_bounds__(PF_THREADS, MINB) void prefill_kernel(const fa_attn_args a, const PrefillShape shp) {
-  constexpr int BM = PF_WAVES * NB * 32;
+// True when every wave's rows of every V unit stay inside one 16-key group
+// (K chunks always do for the supported head dims), so group storage bases
+// are wave-uniform.
+constexpr bool groups_uniform(int dq, int dv, int threads) {
+  const int kcpr = dq / 8, vcpr = dv / 8;
+  for (int c = 0; c * threads < 64 * kcpr; ++c)
+    for (int w = 0; w * 64 < threads; ++w) {
+      const int s = 64 * w + threads * c, e = s + 63;
+      if ((s / kcpr) / 16 != (e / kcpr) / 16) return false;
+    }
+  for (int u = 0; u * threads < 16 * vcpr; ++u)
+    for (int w = 0; w * 64 < threads; ++w) {
+      const int s = 64 * w + threads * u;
+      if (s >= 16 * vcpr) continue;
+      const int e = s + 63 < 16 * vcpr - 1 ? s + 63 : 16 * vcpr - 1;
+      if ((4 * (s / vcpr)) / 16 != (4 * (e / vcpr) + 3) / 16) return false;
+    }
+  return true;
+}
+
+constexpr bool k_groups_uniform(int dq, int threads) {
+  const int kcpr = dq / 8;
+  for (int c = 0; c * threads < 64 * kcpr; ++c)
+    for (int w = 0; w * 64 < threads; ++w) {
+      const int s = 64 * w + threads * c, e = s + 63;
+      if ((s / kcpr) / 16 != (e / kcpr) / 16) return false;
+    }
+  return true;
+}
+
+template <typename T, int DQ, int DV, int NB, int KT, int W, int MINB, bool CAUSAL>
+__global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_args a, const PrefillShape shp) {
+  constexpr int THREADS = 64 * W;
+  constexpr int BM = W * NB * 32;
   constexpr int BN = 32 * KT;
-  constexpr int KST = D / 16;                  // k-steps of the QK^T MFMA
-  constexpr int DB = D / 32;                   // 32-row blocks of O^T
-  constexpr int KLD = D + 8;                   // LDS row stride of K (elements)
+  constexpr int KST = DQ / 16;                 // k-steps of the QK^T MFMA
+  constexpr int DB = DV / 32;                  // 32-row blocks of O^T
+  constexpr int KLD = DQ + 8;                  // LDS row stride of K (elements)
   constexpr int VLD = BN + 8;                  // LDS row stride of V^T
-  constexpr int KTILE = BN * KLD, VTILE = D * VLD;
-  constexpr int KCH = BN * D / 8 / PF_THREADS; // 16-byte K chunks per thread
-  constexpr int VUNITS = (BN / 4) * (D / 8);   // (4 keys x 8 dims) V units per tile
-  constexpr int VPT = (VUNITS + PF_THREADS - 1) / PF_THREADS;
-  static_assert(KCH >= 1 && BN * D / 8 % PF_THREADS == 0, "K staging shape");
+  constexpr int KTILE = BN * KLD, VTILE = DV * VLD;
+  constexpr int KCPR = DQ / 8, VCPR = DV / 8;  // 16-byte chunks per K / V row
+  constexpr int KCH = BN * KCPR / THREADS;     // K chunks per thread
+  constexpr int VUNITS = (BN / 4) * VCPR;      // (4 keys x 8 dims) V units per tile
+  constexpr int VPT = (VUNITS + THREADS - 1) / THREADS;
+  constexpr bool UNIFORM_V = groups_uniform(DQ, DV, THREADS);
+  static_assert(KCH >= 1 && BN * KCPR % THREADS == 0, "K staging shape");
+  static_assert(k_groups_uniform(DQ, THREADS), "K chunks must stay inside 16-key groups");
+  static_assert(BN == 64, "the V^T swizzle assumes 8 key chunks per row");
 
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int wave_u = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index as a scalar
   // Work order.  Workgroups are dispatched round-robin over the 8 XCDs
   // (XCD = blockIdx % 8), each with its own L2.  XCD x takes the (request,
   // KV head) pairs p = x, x + 8, ... one after another, and within a pair the
@@ -113,24 +144,22 @@ __global__ __launch_bounds__(PF_THREADS, MINB) void prefill_kernel(const fa_attn
   const int rem = slot % per_pair;
   const int qb = shp.n_qblocks - 1 - rem / G;
   const int64_t b = pair / a.heads_k;
-  const int h = (int)(pair % a.heads_k) * G + rem % G;
+  const int kh = (int)(pair % a.heads_k);
+  const int h = kh * G + rem % G;
   const RequestInfo r = load_request(a, b);
+  if ((a.flags & FA_FLAG_SKIP_SINGLE_QUERY) && r.q_len == 1) return;   // the decode kernel owns it
   const int q0 = qb * BM;
   if (q0 >= r.q_len) return;
-  const int kh = h / (int)(a.heads_q / a.heads_k);
   const int off = r.k_len - r.q_len;   // absolute position of query row i is i + off
   int kv_end = r.k_len;
   if (CAUSAL) kv_end = min(kv_end, min(q0 + BM, r.q_len) - 1 + off + 1);
   const int n_tiles = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
 
-  const T* __restrict__ Q = (const T*)nullptr;
-  (void)Q;
   const uint16_t* qg = (const uint16_t*)a.q;
   const uint16_t* kg = (const uint16_t*)a.k;
   const uint16_t* vg = (const uint16_t*)a.v;
 
   // Q^T operand for the whole kernel: lane holds Q[row][16kk + 8hh .. +8].
-  const int wave_u = __builtin_amdgcn_readfirstlane(wave);   // wave index as a scalar
   const int wq0 = q0 + wave_u * NB * 32;
   u32x4 qop[NB][KST];
 #pragma unroll
@@ -152,8 +181,8 @@ __global__ __launch_bounds__(PF_THREADS, MINB) void prefill_kernel(const fa_attn
 
   const bool paged = a.page_size != 0;
   const int lp = shp.log2_page;
-  // Storage offset (elements) of key `key`; used per lane only when a wave's
-  // rows can span two 16-key groups (D = 64).
+  // Storage offset (elements) of key `key`; per lane only for V layouts whose
+  // wave rows can span two 16-key groups (Dv = 64).
   auto row_offset = [&](const int64_t* st, int key) -> int64_t {
     if (paged) {
       const int page = key >> lp;
@@ -162,42 +191,6 @@ __global__ __launch_bounds__(PF_THREADS, MINB) void prefill_kernel(const fa_attn
     }
     return ((int64_t)r.k_base + key) * st[1] + (int64_t)kh * st[2];
   };
-
-  // Staging layout.  K: 16-byte chunk c of a thread covers row r0 + lane/(D/8)
-  // (r0 uniform per wave) and columns 8*(lane % (D/8)).  V: unit u of a thread
-  // covers 4 keys x 8 dims with the dims fastest across lanes (coalesced
-  // global reads).  For D >= 128 every wave's rows of a chunk/unit lie inside
-  // one 16-key group, whose storage base is wave-uniform (one scalar block
-  // table read per group and tile); lanes add a 32-bit offset computed once.
-  constexpr int KROWS_W = 64 / (D / 8);
-  constexpr int VROWS_W = 4 * 64 / (D / 8);
-  constexpr bool UNIFORM = VROWS_W <= 16;
-  int kgrp[KCH], koff[KCH], kst[KCH];
-#pragma unroll
-  for (int c = 0; c < KCH; ++c) {
-    const int r0 = (64 * wave_u + PF_THREADS * c) / (D / 8);
-    const int row = r0 + lane / (D / 8), col8 = lane % (D / 8);
-    kgrp[c] = r0 & ~15;
-    koff[c] = 2 * ((row - kgrp[c]) * (int)a.k_stride[1] + col8 * 8);   // bytes
-    kst[c] = sigma(row) * KLD + col8 * 8;
-  }
-  int vgrp[VPT], voff[VPT][4], vst[VPT];
-  bool vunit[VPT];
-#pragma unroll
-  for (int u = 0; u < VPT; ++u) {
-    const int uid0 = 64 * wave_u + PF_THREADS * u;
-    const int uid = uid0 + lane;
-    const int kgp = uid / (D / 8), dc = uid % (D / 8);
-    vunit[u] = uid < VUNITS;
-    vgrp[u] = (4 * (uid0 / (D / 8))) & ~15;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) voff[u][rr] = 2 * ((4 * kgp + rr - vgrp[u]) * (int)a.v_stride[1] + dc * 8);
-    // V^T element (dim, key) lives at dim*VLD + 8*((key/8) ^ ((dim/16) & 7)) + key%8:
-    // with 64 LDS banks, 32 lanes writing 8 bytes (dims 8*dc + d, two key
-    // groups) and 16 lanes reading 16 bytes (16 consecutive dims) both hit
-    // distinct banks.
-    vst[u] = 8 * dc * VLD + 8 * ((kgp >> 1) ^ ((dc >> 1) & 7)) + 4 * (kgp & 1);
-  }
   auto group_base = [&](const int64_t* st, int key0) -> int64_t {
     if (paged) {
       const int64_t blk = load_invariant_i32(a.block_table, b * a.bt_stride[0] + (int64_t)(key0 >> lp) * a.bt_stride[1]);
@@ -206,14 +199,35 @@ __global__ __launch_bounds__(PF_THREADS, MINB) void prefill_kernel(const fa_attn
     return ((int64_t)r.k_base + key0) * st[1] + (int64_t)kh * st[2];
   };
 
-  // K/V tiles are read with buffer loads.  Each 16-key group gets a scalar
-  // resource descriptor whose base is the group's first row and whose size
-  // ends with the last valid key of the request, so rows past the keys read
-  // as zero in hardware; lane offsets are loop-invariant registers.
-  u32x4 kreg[KCH];
-  u32x4 vreg[VPT][4];
-  uint32_t vmask = ~0u;
-  const int64_t safe_v = UNIFORM ? 0 : group_base(a.v_stride, 0);
+  // Staging layout.  K: chunk c of a thread is 16 bytes of row idx / KCPR at
+  // column 8 * (idx % KCPR), idx = 64 * wave + THREADS * c + lane, stored at
+  // LDS row sigma(row).  V: unit u of a thread covers 4 keys x 8 dims with
+  // the dims fastest across lanes (coalesced global reads).
+  int kgrp[KCH], koff[KCH], kst[KCH];
+#pragma unroll
+  for (int c = 0; c < KCH; ++c) {
+    const int idx0 = 64 * wave_u + THREADS * c;
+    const int idx = idx0 + lane;
+    const int row = idx / KCPR, col = idx % KCPR;
+    kgrp[c] = (idx0 / KCPR) & ~15;
+    koff[c] = 2 * ((row - kgrp[c]) * (int)a.k_stride[1] + col * 8);   // bytes
+    kst[c] = sigma(row) * KLD + col * 8;
+  }
+  int vgrp[VPT], voff[VPT][4], vst[VPT];
+  bool vunit[VPT];
+#pragma unroll
+  for (int u = 0; u < VPT; ++u) {
+    const int uid0 = 64 * wave_u + THREADS * u;
+    const int uid = uid0 + lane;
+    const int kgp = uid / VCPR, dc = uid % VCPR;
+    vunit[u] = uid < VUNITS;
+    vgrp[u] = (4 * (uid0 / VCPR)) & ~15;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) voff[u][rr] = 2 * ((4 * kgp + rr - vgrp[u]) * (int)a.v_stride[1] + dc * 8);
+    // V^T element (dim, key) lives at dim*VLD + 8*((key/8) ^ ((dim/16) & 7)) + key%8.
+    vst[u] = 8 * dc * VLD + 8 * ((kgp >> 1) ^ ((dc >> 1) & 7)) + 4 * (kgp & 1);
+  }
+
   // Packed K/V: running address of each group's first key for the current
   // tile, advanced by one tile per load (no per-tile 64-bit products).
   const uint16_t* kcur[KCH];
@@ -229,25 +243,29 @@ __global__ __launch_bounds__(PF_THREADS, MINB) void prefill_kernel(const fa_attn
     const int bytes = nvalid > 0 ? 2 * ((nvalid - 1) * (int)st[1] + row_elems) : 0;
     return __builtin_amdgcn_make_buffer_rsrc((void*)gptr, (short)0, bytes, 0x00020000);
   };
+
+  u32x4 kreg[KCH];
+  u32x4 vreg[VPT][4];
+  uint32_t vmask = ~0u;
+  const int64_t safe_v = UNIFORM_V ? 0 : group_base(a.v_stride, 0);
   auto load_tile = [&](int t0) {
 #pragma unroll
     for (int c = 0; c < KCH; ++c) {
-      const auto rsrc = group_rsrc(kg, kcur[c], a.k_stride, t0 + kgrp[c], D);
+      const auto rsrc = group_rsrc(kg, kcur[c], a.k_stride, t0 + kgrp[c], DQ);
       kcur[c] += kstep;
       kreg[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, koff[c], 0, 0));
     }
 #pragma unroll
     for (int u = 0; u < VPT; ++u) {
-      if (UNIFORM) {
-        const auto rsrc = group_rsrc(vg, vcur[u], a.v_stride, t0 + vgrp[u], D);
+      if (UNIFORM_V) {
+        const auto rsrc = group_rsrc(vg, vcur[u], a.v_stride, t0 + vgrp[u], DV);
         vcur[u] += vstep;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr)
           vreg[u][rr] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff[u][rr], 0, 0));
       } else {
-        // D = 64: a wave's V rows span two 16-key groups; per-lane addresses.
-        const int uid = 64 * wave_u + PF_THREADS * u + lane;
-        const int kgp = uid / (D / 8), dc = uid % (D / 8);
+        const int uid = 64 * wave_u + THREADS * u + lane;
+        const int kgp = uid / VCPR, dc = uid % VCPR;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int key = t0 + 4 * kgp + rr;
@@ -267,7 +285,7 @@ __global__ __launch_bounds__(PF_THREADS, MINB) void prefill_kernel(const fa_attn
 #pragma unroll
     for (int u = 0; u < VPT; ++u) {
       if (!vunit[u]) continue;
-      if (!UNIFORM) {
+      if (!UNIFORM_V) {
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr)
           if (!((vmask >> (4 * u + rr)) & 1)) vreg[u][rr] = zero;
@@ -285,19 +303,20 @@ __global__ __launch_bounds__(PF_THREADS, MINB) void prefill_kernel(const fa_attn
       }
     }
   };
-  (void)KROWS_W;
 
   const bool cap = a.softcap > 0.0f;
   const float c_scale = a.softmax_scale * LOG2E;          // raw dot -> log2 units
   const float cap_in = cap ? a.softmax_scale / a.softcap : 0.0f;
   const float cap_out = a.softcap * LOG2E;
+  // A sink logit seeds the running state (max = sink, sum = 1) of every row.
+  const float sink2 = a.sinks ? a.sinks[(int64_t)h * a.sink_stride] * LOG2E : -INFINITY;
 
   float m_run[NB], l_run[NB];
   f32x16 o[DB][NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    m_run[nb] = -INFINITY;
-    l_run[nb] = 0.0f;
+    m_run[nb] = sink2;
+    l_run[nb] = (a.sinks && hh == 0) ? 1.0f : 0.0f;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -444,33 +463,54 @@ __global__ __launch_bounds__(PF_THREADS, MINB) void prefill_kernel(const fa_attn
   }
 }
 
-template <int D> constexpr int nb_for() { return D <= 128 ? FA_PF_NB : 1; }
-template <int D> constexpr int kt_for() { return D <= 128 ? FA_PF_KT : 2; }
-template <int D> constexpr int minb_for() { return D <= 128 ? FA_PF_MINB : 1; }
+// Tile shape per head-dim pair: NB query blocks per wave, W waves per
+// workgroup, MINB workgroups per CU.  Two waves per SIMD either as two
+// 4-wave workgroups (when LDS holds two double-buffered tile pairs) or as
+// one 8-wave workgroup sharing its tiles.
+template <int DQ, int DV> struct PrefillTile;
+template <> struct PrefillTile<64, 64> { static constexpr int NB = 1, W = 4, MINB = 2; };
+template <> struct PrefillTile<128, 128> { static constexpr int NB = 1, W = 4, MINB = 2; };
+template <> struct PrefillTile<192, 128> { static constexpr int NB = 1, W = 8, MINB = 1; };
+template <> struct PrefillTile<256, 256> { static constexpr int NB = 1, W = 4, MINB = 1; };
 
-template <int D>
+template <int DQ, int DV>
 constexpr size_t lds_bytes() {
-  return 2 * (size_t)(32 * kt_for<D>() * (D + 8) + D * (32 * kt_for<D>() + 8)) * sizeof(uint16_t);
+  return 2 * (size_t)(64 * (DQ + 8) + DV * (64 + 8)) * sizeof(uint16_t);
 }
 
 using PrefillKernel = void (*)(fa_attn_args, PrefillShape);
 
-template <typename T, int D>
-PrefillKernel pick(bool causal) {
-  constexpr int NB = nb_for<D>(), KT = kt_for<D>(), MB = minb_for<D>();
-  return causal ? prefill_kernel<T, D, NB, KT, MB, true> : prefill_kernel<T, D, NB, KT, MB, false>;
+struct PrefillChoice {
+  PrefillKernel kern;
+  int bm, threads;
+  size_t lds;
+};
+
+template <typename T, int DQ, int DV>
+PrefillChoice pick(bool causal) {
+  using S = PrefillTile<DQ, DV>;
+  PrefillChoice c;
+  c.kern = causal ? prefill_kernel<T, DQ, DV, S::NB, 2, S::W, S::MINB, true>
+                  : prefill_kernel<T, DQ, DV, S::NB, 2, S::W, S::MINB, false>;
+  c.bm = 32 * S::NB * S::W;
+  c.threads = 64 * S::W;
+  c.lds = lds_bytes<DQ, DV>();
+  return c;
 }
 
-PrefillKernel select_prefill(const fa_attn_args& a, int* bm, size_t* lds) {
-  const int64_t d = a.head_dim_qk;
-  const bool bf = a.q_dtype == FA_BF16;
+template <typename T>
+PrefillChoice pick_dims(int64_t dq, int64_t dv, bool causal) {
+  if (dq == 64 && dv == 64) return pick<T, 64, 64>(causal);
+  if (dq == 128 && dv == 128) return pick<T, 128, 128>(causal);
+  if (dq == 192 && dv == 128) return pick<T, 192, 128>(causal);
+  if (dq == 256 && dv == 256) return pick<T, 256, 256>(causal);
+  return PrefillChoice{nullptr, 0, 0, 0};
+}
+
+PrefillChoice select_prefill(const fa_attn_args& a) {
   const bool causal = a.causal != 0;
-  switch (d) {
-    case 64: *bm = 128 * nb_for<64>(); *lds = lds_bytes<64>(); return bf ? pick<BF16T, 64>(causal) : pick<F16T, 64>(causal);
-    case 128: *bm = 128 * nb_for<128>(); *lds = lds_bytes<128>(); return bf ? pick<BF16T, 128>(causal) : pick<F16T, 128>(causal);
-    case 256: *bm = 128 * nb_for<256>(); *lds = lds_bytes<256>(); return bf ? pick<BF16T, 256>(causal) : pick<F16T, 256>(causal);
-    default: return nullptr;
-  }
+  return a.q_dtype == FA_BF16 ? pick_dims<BF16T>(a.head_dim_qk, a.head_dim_v, causal)
+                              : pick_dims<F16T>(a.head_dim_qk, a.head_dim_v, causal);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -478,9 +518,9 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 bool prefill_ok(const fa_attn_args& a) {
   if (!(a.q_dtype == a.k_dtype && a.k_dtype == a.v_dtype && a.v_dtype == a.out_dtype)) return false;
   if (a.q_dtype != FA_BF16 && a.q_dtype != FA_F16) return false;
-  if (a.head_dim_qk != a.head_dim_v) return false;
-  if (a.head_dim_qk != 64 && a.head_dim_qk != 128 && a.head_dim_qk != 256) return false;
-  if (a.leftpad_k || a.alibi || a.sinks || a.q_descale || a.k_descale || a.v_descale) return false;
+  const int64_t dq = a.head_dim_qk, dv = a.head_dim_v;
+  if (!((dq == dv && (dq == 64 || dq == 128 || dq == 256)) || (dq == 192 && dv == 128))) return false;
+  if (a.leftpad_k || a.alibi || a.q_descale || a.k_descale || a.v_descale) return false;
   if (a.mask_kind != 0 || a.causal_by_batch || a.window_left != -1 || a.window_right != -1) return false;
   if (a.num_splits != 1) return false;
   if (a.q_stride[2] != 1 || a.k_stride[3] != 1 || a.v_stride[3] != 1 || a.out_stride[2] != 1) return false;
@@ -489,6 +529,10 @@ bool prefill_ok(const fa_attn_args& a) {
     if ((a.q_stride[i] * 2) % 16 || (a.out_stride[i] * 2) % 8) return false;
   for (int i = a.page_size ? 0 : 1; i < 3; ++i)
     if ((a.k_stride[i] * 2) % 16 || (a.v_stride[i] * 2) % 16) return false;
+  // Group-bounded buffer loads need non-overlapping rows and 16-row groups
+  // that span less than 2 GiB.
+  if (a.k_stride[1] < dq || a.v_stride[1] < dv) return false;
+  if (16 * a.k_stride[1] * 2 >= 0x7fffffffll || 16 * a.v_stride[1] * 2 >= 0x7fffffffll) return false;
   if (a.page_size) {
     if (a.page_size < 16 || (a.page_size & (a.page_size - 1))) return false;
   }
@@ -510,22 +554,20 @@ extern "C" int fa_prefill_fwd(const fa_attn_args* a, void* stream) {
   }
   if (a->total_q == 0) return FA_OK;
   FA_REQUIRE(a->max_seqlen_q >= 1, "fa_prefill_fwd: max_seqlen_q must be positive");
-  int bm = 0;
-  size_t lds = 0;
-  const PrefillKernel kern = select_prefill(*a, &bm, &lds);
+  const PrefillChoice ch = select_prefill(*a);
   PrefillShape shp;
-  shp.n_qblocks = (int)fa_ceil_div(a->max_seqlen_q, bm);
+  shp.n_qblocks = (int)fa_ceil_div(a->max_seqlen_q, ch.bm);
   shp.log2_page = 0;
   if (a->page_size)
     while ((1ll << shp.log2_page) < a->page_size) ++shp.log2_page;
   const int64_t pairs = a->batch * a->heads_k;
   const int64_t blocks = fa_ceil_div(pairs, 8) * 8 * shp.n_qblocks * (a->heads_q / a->heads_k);
   FA_REQUIRE(blocks <= 0x7fffffffll, "fa_prefill_fwd: grid too large");
-  hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  hipError_t err = hipFuncSetAttribute((const void*)ch.kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ch.lds);
   if (err != hipSuccess) {
-    fa_set_error("fa_prefill_fwd: cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(err));
+    fa_set_error("fa_prefill_fwd: cannot reserve %zu bytes of LDS: %s", ch.lds, hipGetErrorString(err));
     return FA_ERR_LAUNCH;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(PF_THREADS), lds, (hipStream_t)stream, *a, shp);
+  hipLaunchKernelGGL(ch.kern, dim3((unsigned)blocks), dim3(ch.threads), ch.lds, (hipStream_t)stream, *a, shp);
   return fa_check_launch("fa_prefill_fwd");
 }

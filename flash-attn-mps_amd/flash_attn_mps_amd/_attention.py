@@ -8,6 +8,9 @@ shapes, dtypes, strides, feature flags and the caller's maximum lengths:
    -> split-KV decode (``_decode.decode_attention``; _attention.py:134-147);
 2. bf16/fp16 with the feature set compiled into the MFMA prefill kernel
    -> fa_prefill_fwd (the reference's `fast` route, _attention.py:149-158);
+   in a batch of several requests, the single-query ones go to the split-KV
+   decode kernel first and fa_prefill_fwd skips them
+   (FA_FLAG_SKIP_SINGLE_QUERY);
 3. everything else -> fa_attn_fwd, the generic kernel, with the reference's
    split rule: deterministic -> 1, else num_splits, else
    min(32, ceil(max_k / 256)) when the row is decode-like or d > 256
@@ -118,9 +121,29 @@ def _fast_candidate(q, k, v, out, num_splits, deterministic, causal, window_size
             and q.dtype in (torch.float16, torch.bfloat16)
             and not isinstance(causal, torch.Tensor)
             and tuple(window_size) == (-1, -1)
-            and alibi_slopes is None and s_aux is None
+            and alibi_slopes is None
             and q_descale is None and k_descale is None and v_descale is None
             and mask_mod is None and leftpad_k is None)
+
+
+def _decode_rows(args, batch, heads, kvheads, dq, dv, max_seqlen_k, device, keep):
+    """Launch the split-KV decode kernel on the single-query requests of a
+    mixed batch (it skips every other request); True if it ran."""
+    if not _lib.supported("fa_decode_supported", args):
+        return False
+    from ._decode import decode_group_tile, split_plan
+    groups = heads // decode_group_tile(heads, kvheads, dq, dv)
+    splits, span = split_plan(batch, groups, max_seqlen_k, 0)
+    args.num_splits, args.split_span = splits, span
+    if splits > 1:
+        partial = torch.empty((batch, heads, splits, dv), dtype=torch.float32, device=device)
+        partial_lse = torch.empty((batch, heads, splits), dtype=torch.float32, device=device)
+        keep += [partial, partial_lse]
+        args.partial_out, args.partial_lse = partial.data_ptr(), partial_lse.data_ptr()
+    _lib.call("fa_decode_fwd", args, device)
+    args.num_splits, args.split_span = 1, 0
+    args.partial_out = args.partial_lse = None
+    return True
 
 
 def attention(q, k, v, *, cu_seqlens_q, cu_seqlens_k=None, seqused_k=None, max_seqlen_q,
@@ -188,6 +211,11 @@ def attention(q, k, v, *, cu_seqlens_q, cu_seqlens_k=None, seqused_k=None, max_s
     if (_fast_candidate(q, k, v, out, num_splits, deterministic, causal, window_size, alibi_slopes,
                         s_aux, q_descale, k_descale, v_descale, mask_mod, leftpad_k)
             and _lib.supported("fa_prefill_supported", args)):
+        # Mixed batches (chunked prefill + decode): single-query requests run
+        # on the split-KV decode kernel and the MFMA kernel skips them, since a
+        # 128-row query tile would spend one workgroup per head on each.
+        if batch > 1 and _decode_rows(args, batch, heads, kh, dq, dv, max_seqlen_k, q.device, keep):
+            args.flags |= _lib.FLAG_SKIP_SINGLE_QUERY
         _lib.call("fa_prefill_fwd", args, q.device)
         return out, lse
     vector = deterministic or max_seqlen_q == 1 or max(dq, dv) > 256

@@ -82,7 +82,8 @@ class AttnArgs(ctypes.Structure):
                 ("k_descale", _p), ("k_descale_stride", _arr(_i64, 2)),
                 ("v_descale", _p), ("v_descale_stride", _arr(_i64, 2)),
                 ("num_splits", _i32), ("split_span", _i32),
-                ("partial_out", _p), ("partial_lse", _p)]
+                ("partial_out", _p), ("partial_lse", _p),
+                ("flags", _i32), ("_pad1", _i32)]
 
 
 class MergePairArgs(ctypes.Structure):
@@ -121,7 +122,8 @@ ENTRY_POINTS = {
     "fa_merge_partials": (MergePartialsArgs, ctypes.c_int),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
+FLAG_SKIP_SINGLE_QUERY = 1
 _lib = None
 
 

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 1
+#define FA_ABI_VERSION 2
 
 /* Element types of attention/cache tensors. */
 enum fa_dtype { FA_F16 = 0, FA_BF16 = 1, FA_F32 = 2, FA_E4M3 = 3 };
@@ -160,7 +160,14 @@ typedef struct fa_attn_args {
   int32_t split_span;                /* decode: keys per split (multiple of 128) */
   float* partial_out;                /* workspace, see fa_*_workspace_floats */
   float* partial_lse;
+
+  int32_t flags;                     /* FA_FLAG_* bits */
+  int32_t _pad1;
 } fa_attn_args;
+
+/* fa_attn_args.flags: fa_prefill_fwd leaves requests with exactly one query
+ * row untouched (a caller routes those to fa_decode_fwd in the same batch). */
+#define FA_FLAG_SKIP_SINGLE_QUERY 1
 
 /* Two-state merge (out may alias a or b, out_lse may alias a_lse). */
 typedef struct fa_merge_pair_args {

@@ -9,9 +9,10 @@ and that the MFMA path is the one taken.  Tolerances: this build's bar
 import pytest
 import torch
 
-from flash_attn_mps_amd import _lib, flash_attn_varlen_func
+from flash_attn_mps_amd import _lib, flash_attn_varlen_func, vllm
 from flash_attn_mps_amd._attention import attention, build_args
-from helpers import assert_attention_close, assert_north_star, attention_reference, cu_from_lengths
+from helpers import (assert_attention_close, assert_north_star, assert_reference_tol, attention_reference,
+                     cu_from_lengths)
 
 pytestmark = pytest.mark.gpu
 
@@ -144,3 +145,77 @@ def test_prefill_long_softmax_stability(device):
     # (tests/reference.py:93-96 of flash_attn_mps).
     assert_attention_close(out, ref)
     torch.testing.assert_close(lse.cpu().double(), ref_lse, atol=1e-4, rtol=0)
+
+
+def _case_dims(device, dtype, dq, dv, hq, hkv, q_lens, k_lens, scale=0.5, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(sum(q_lens), hq, dq, generator=g) * scale).to(dtype).to(device)
+    k = (torch.randn(sum(k_lens), hkv, dq, generator=g) * scale).to(dtype).to(device)
+    v = torch.randn(sum(k_lens), hkv, dv, generator=g).to(dtype).to(device)
+    return q, k, v, cu_from_lengths(q_lens, device), cu_from_lengths(k_lens, device)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 2)])
+def test_prefill_diffkv_192_128(device, dtype, causal, hq, hkv):
+    """DIFFKV head dims (Dqk 192, Dv 128) on the MFMA kernel."""
+    q_lens, k_lens = [3, 129, 300, 64], [3, 200, 300, 1000]
+    q, k, v, cuq, cuk = _case_dims(device, dtype, 192, 128, hq, hkv, q_lens, k_lens, seed=hq + 2 * causal)
+    out = torch.empty(q.shape[0], hq, 128, dtype=dtype, device=device)
+    lse = torch.empty(hq, q.shape[0], device=device)
+    kw = dict(cu_seqlens_q=cuq, cu_seqlens_k=cuk, seqused_k=None, max_seqlen_q=300, max_seqlen_k=1000,
+              block_table=None, softmax_scale=None, causal=causal, window_size=(-1, -1), alibi_slopes=None,
+              softcap=0., s_aux=None, q_descale=None, k_descale=None, v_descale=None, mask_mod=None,
+              aux_tensors=None, leftpad_k=None)
+    assert _uses_mfma(q, k, v, out, lse, **kw)
+    out, lse = attention(q, k, v, cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=300, max_seqlen_k=1000,
+                         causal=causal)
+    assert out.shape == (q.shape[0], hq, 128)
+    ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=causal)
+    assert_north_star(out, lse, ref, ref_lse, dtype)
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_prefill_sinks(device, d):
+    """Per-head sink logits join the denominator only (rows with no key: lse = sink)."""
+    q_lens, k_lens = [50, 130, 7], [10, 130, 0]
+    q, k, v, cuq, cuk = _case(device, torch.bfloat16, d, 8, 4, q_lens, k_lens, seed=31 + d)
+    sinks = torch.randn(8, generator=torch.Generator().manual_seed(d)).mul(3).to(device)
+    out, lse = attention(q, k, v, cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=130, max_seqlen_k=130,
+                         causal=True, s_aux=sinks)
+    ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=True, sinks=sinks.cpu())
+    assert_reference_tol(out, lse, ref, ref_lse, torch.bfloat16)
+    # rows of the second request that see >= 32 keys meet the 1e-2 bar
+    assert_north_star(out, lse, ref, ref_lse, torch.bfloat16, rows=torch.arange(50 + 31, 180))
+
+
+@pytest.mark.parametrize("dq,dv", [(128, 128), (192, 128), (64, 64)])
+def test_mixed_batch_routes_single_queries_to_decode(device, dq, dv):
+    """Chunked prefill + decode in one paged call: q_len == 1 requests run on
+    the decode kernel, the rest on the MFMA kernel (which skips them)."""
+    g = torch.Generator().manual_seed(dq + dv)
+    page, hq, hkv = 16, 8, 2
+    q_lens = [1, 300, 1, 1, 77, 1, 2]
+    k_lens = [900, 700, 1, 4000, 77, 33, 2]
+    cols = max((n + page - 1) // page for n in k_lens)
+    pool = cols * len(k_lens)
+    table = torch.randperm(pool, generator=g).int().reshape(len(k_lens), cols)
+    kc = torch.randn(pool, page, hkv, dq, generator=g).to(torch.bfloat16).to(device)
+    vc = torch.randn(pool, page, hkv, dv, generator=g).to(torch.bfloat16).to(device)
+    q = (torch.randn(sum(q_lens), hq, dq, generator=g) * 0.5).to(torch.bfloat16).to(device)
+    sinks = torch.randn(hq, generator=g).to(device)
+    cuq = cu_from_lengths(q_lens, device)
+    used = torch.tensor(k_lens, dtype=torch.int32, device=device)
+    out, lse = vllm.flash_attn_varlen_func(q, kc, vc, max(q_lens), cuq, cols * page, seqused_k=used,
+                                           block_table=table.to(device), causal=True, s_aux=sinks,
+                                           return_softmax_lse=True)
+    ref, ref_lse = attention_reference(q, kc, vc, cuq, used_k=used, block_table=table, causal=True,
+                                       sinks=sinks.cpu())
+    assert_reference_tol(out, lse, ref, ref_lse, torch.bfloat16)
+    # rows that see >= 32 keys meet the 1e-2 bar (row i of a request sees k - q + i + 1 keys)
+    many, start = [], 0
+    for n, m in zip(q_lens, k_lens):
+        many += [start + i for i in range(n) if m - n + i + 1 >= 32]
+        start += n
+    assert_north_star(out, lse, ref, ref_lse, torch.bfloat16, rows=torch.tensor(many))
