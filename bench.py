@@ -39,6 +39,9 @@ def parse():
     p.add_argument("--no-secondary", action="store_true", help="only the headline prefill config")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--only", default="", help="comma list of configs to run (2,3,4,5)")
+    p.add_argument("--copy-probe", action="store_true",
+                   help="first run a known-size copy kernel (reads and writes 1 GiB) that calibrates "
+                        "rocprofv3 FETCH_SIZE / WRITE_SIZE")
     return p.parse_args()
 
 
@@ -81,6 +84,33 @@ def time_calls(fn, steps, warmup):
     total = region0.elapsed_time(region1)
     per_call = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
     return total / steps, per_call[len(per_call) // 2]
+
+
+def copy_probe(device):
+    """torch.neg over 2^28 fp32 values: 1 GiB read + 1 GiB written per launch,
+    three launches.  Under rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE give
+    the factor from counter KiB to bytes moved."""
+    import torch
+    x = torch.ones(1 << 28, dtype=torch.float32, device=device)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        torch.neg(x, out=y)
+    torch.cuda.synchronize()
+    del x, y
+    torch.cuda.empty_cache()
+
+
+def measured_traffic():
+    """HBM bytes per launch of the prefill kernel on config 2, from the
+    committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes (scaled by the copy
+    probe), or None when that summary is absent."""
+    path = ROOT / "profiles" / "prefill_config2_traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
 
 
 def config2(device, steps, warmup):
@@ -253,6 +283,8 @@ def main():
     import torch
     device = torch.device("cuda", 0)
     only = set(args.only.split(",")) if args.only else None
+    if args.copy_probe:
+        copy_probe(device)
     c2 = config2(device, args.steps, args.warmup)
     line = {
         "metric": "bf16 prefill TFLOP/s & paged-decode KV GB/s, % of MI355X roofline, 1 GPU",
@@ -271,7 +303,8 @@ def main():
                                "(Qwen3-0.6B attention)", "global_batch": 16, "seq_len": max(c2["lengths"]),
                    "total_tokens": sum(c2["lengths"]), "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(c2["call_tflops"], 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(c2["call_tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(c2["call_tflops"] / PEAK_BF16_TFLOPS, 4),
+                     "traffic": measured_traffic(),
                      "flops_per_launch": c2["flops"], "kernel_ms": round(c2["call_ms"], 4)},
     }
     secondary = {}
