@@ -209,7 +209,10 @@ int fa_decode_supported(const fa_attn_args* args);
 int fa_decode_fwd(const fa_attn_args* args, void* stream);
 
 /* MFMA prefill (bf16/fp16).  fa_prefill_supported() says whether the
- * argument combination is compiled in. */
+ * argument combination is compiled in.  With FA_FLAG_SKIP_SINGLE_QUERY in
+ * args->flags, requests with one query row are left untouched for
+ * fa_decode_fwd (no reference counterpart: the reference runs such rows
+ * through its prefill tile, flash_attn_mps/_attention.py:149-158). */
 int fa_prefill_supported(const fa_attn_args* args);
 int fa_prefill_fwd(const fa_attn_args* args, void* stream);
 
