@@ -3,34 +3,51 @@
 // Semantics follow flash_attn_mps/_decode.py:40-99 and
 // flash_attn_mps/kernels/attention_decode.metal:18-207: one query per request,
 // keys [vis_begin, len) with vis_begin = len - window_left - 1 under a left
-// window, q pre-scaled by softmax_scale * q_descale * k_descale, softcap on the
-// scaled score, the sink seeding (max, sum) = (sink, 1) of split 0 only, the
-// output multiplied by v_descale, fp32 partial states merged by log-sum-exp.
+// window, scores scaled by softmax_scale * q_descale * k_descale, softcap on
+// the scaled score, the sink seeding (max, sum) = (sink, 1) of split 0 only,
+// the output multiplied by v_descale, fp32 partial states merged by
+// log-sum-exp.
 //
 // gfx950 layout.  A workgroup (4 waves) owns one (request, group of GT query
 // heads sharing a KV head, split of `span` keys).  Every 16-lane row of a wave
-// owns one key at a time and spreads its head dimension over the 16 lanes,
-// so each lane moves D/16 contiguous elements per key with 4..16-byte loads:
-// a 256-byte bf16/FP8 head row is one fully coalesced 16-lane access.  A wave
-// step covers 32 key positions (4 rows x 8 positions; 8 consecutive positions
-// share one page when P % 8 == 0; 4 positions for 512-byte K+V row pairs)
-// and issues all of its K and V loads before any arithmetic, which keeps
-// 8-16 KiB per wave in flight for the HBM stream.
-// Scores are reduced across the 16 lanes with DPP; each row keeps its own
-// online-softmax state, combined across rows with lane shuffles and across
-// waves through LDS at the end.  Math is exp2-based with log2(e) folded into q.
+// owns NT consecutive key positions per step and spreads the head dimension
+// over its 16 lanes, so a 256-byte K or V head row is one coalesced 16-lane
+// access of 16-byte loads.  A wave step covers 4 rows x NT positions; the
+// wave's next step is STEP * 4 positions further (the 4 waves interleave).
+// * The K/V loads of step t+1 are issued before step t is computed (two
+//   register buffers), so every wave keeps one step of K/V in flight while
+//   it does arithmetic.
+// * Block-table entries for 64 steps are loaded once per wave into lanes
+//   (lane 4u + row holds the page of step u's row) and handed to the rows
+//   with ds_bpermute: no dependent table load inside the loop.
+// * Loads are unconditional: positions outside the split clamp to the row's
+//   first/last valid position (rows with none read the split's first key),
+//   and their scores are masked to -inf, so V is finite and p = 0.
+// * Q.K runs on packed pairs with v_dot2_f32_bf16 / v_dot2_f32_f16 (FP8 K
+//   converts exactly to the query's 16-bit type with v_cvt_scalef32_pk_*);
+//   the softmax scale is applied to the reduced score.  P.V is fp32 FMA.
+// * exp2 online softmax per row whose running max moves only when a step
+//   raises it by more than 2^8 (probabilities stay <= 256); rows combine
+//   with lane shuffles and waves through LDS at the end.
 #include "attn_common.h"
 
 namespace {
 
 constexpr int DEC_THREADS = 256;
 constexpr int DEC_PAGE_ALIGN = 8;   // paged K/V needs P % 8 == 0
+#ifndef FA_DEC_MINB
+#define FA_DEC_MINB 2
+#endif
+constexpr float DEC_RESCALE = 8.0f;
 
-// Positions per 16-lane row per step: 8, or 4 when a K+V row pair is wide
-// enough that 8 of each in flight would exceed the register budget.
+typedef __attribute__((ext_vector_type(2))) __bf16 dec_bf16x2;
+typedef __attribute__((ext_vector_type(2))) _Float16 dec_f16x2;
+
+// Positions per 16-lane row per step: 4, or 2 for K+V row pairs of 64 bytes
+// per lane or more (keeps two register buffers within budget).
 template <int KB, int VB>
 struct DecodeRows {
-  static constexpr int value = (KB + VB) / 4 * 8 > 96 ? 4 : 8;
+  static constexpr int value = KB + VB >= 64 ? 2 : 4;
 };
 
 template <int BYTES>
@@ -69,40 +86,77 @@ FA_DEV void words_to_f32(const uint32_t* w, float* f) {
       f[2 * i] = f16_bits_to_f32(w[i] & 0xffffu);
       f[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
     }
-  } else if constexpr (T::id == FA_E4M3) {
+  } else {
+    static_assert(T::id == FA_E4M3, "V element type");
 #pragma unroll
     for (int i = 0; i < N / 4; ++i) {
       const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], false);
       const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], true);
       f[4 * i] = lo[0]; f[4 * i + 1] = lo[1]; f[4 * i + 2] = hi[0]; f[4 * i + 3] = hi[1];
     }
-  } else {
-#pragma unroll
-    for (int i = 0; i < N; ++i) f[i] = __uint_as_float(w[i]);
   }
+}
+
+// c + a.lo * b.lo + a.hi * b.hi on packed 16-bit pairs, fp32 result.
+template <typename CT> FA_DEV float dot2(uint32_t a, uint32_t b, float c);
+template <> FA_DEV float dot2<BF16T>(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(dec_bf16x2, a), __builtin_bit_cast(dec_bf16x2, b), c, false);
+}
+template <> FA_DEV float dot2<F16T>(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(dec_f16x2, a), __builtin_bit_cast(dec_f16x2, b), c, false);
+}
+
+// K row words -> EK/2 packed pairs of the compute type (FP8 widens exactly).
+template <typename CT, typename KT, int EK>
+FA_DEV void k_pairs(const uint32_t* w, uint32_t* p) {
+  if constexpr (KT::id == FA_E4M3) {
+#pragma unroll
+    for (int i = 0; i < EK / 4; ++i) {
+      if constexpr (CT::id == FA_BF16) {
+        p[2 * i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[i], 1.0f, false));
+        p[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[i], 1.0f, true));
+      } else {
+        p[2 * i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[i], 1.0f, false));
+        p[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[i], 1.0f, true));
+      }
+    }
+  } else {
+    static_assert(KT::id == CT::id, "16-bit K must match the compute type");
+#pragma unroll
+    for (int i = 0; i < EK / 2; ++i) p[i] = w[i];
+  }
+}
+
+template <typename CT>
+FA_DEV uint32_t pack_pair_bits(float lo, float hi) {
+  if constexpr (CT::id == FA_BF16) return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+  else return (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
 }
 
 FA_DEV int decode_vis_begin(const fa_attn_args& a, int k_len) {
   return a.window_left >= 0 ? max(0, k_len - a.window_left - 1) : 0;
 }
 
-template <typename KT, typename VT, int D, int DV, int GT>
-__global__ __launch_bounds__(DEC_THREADS, 2) void decode_kernel(const fa_attn_args a, const int span) {
+template <typename CT, typename KT, typename VT, int D, int DV, int GT, bool CAP>
+__global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const fa_attn_args a, const int span) {
   constexpr int EK = D / 16, EV = DV / 16;
   constexpr int KB = EK * KT::bytes, VB = EV * VT::bytes;
-  constexpr int DEC_NT = DecodeRows<KB, VB>::value;
-  constexpr int STEP = 4 * DEC_NT;   // positions per wave step
-  static_assert(D % 16 == 0 && DV % 16 == 0 && KB % 4 == 0 && VB % 4 == 0, "decode tile shape");
+  constexpr int NT = DecodeRows<KB, VB>::value;
+  constexpr int STEP = 4 * NT;          // positions of one wave step
+  constexpr int WSTRIDE = 4 * STEP;     // positions between a wave's consecutive steps
+  static_assert(EK % 4 == 0 && EV % 4 == 0 && KB % 4 == 0 && VB % 4 == 0, "decode tile shape");
   __shared__ float sm_m[4][GT], sm_l[4][GT];
   __shared__ float sm_acc[4][GT][DV];
 
-  const int split = blockIdx.x;
+  // Head groups are the fastest grid dimension: the workgroups of one
+  // (request, split) run together and read whole token rows of the same pages.
+  const int split = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, rg = lane >> 4, l16 = lane & 15;
   const RequestInfo r = load_request(a, b);
   if (r.q_len != 1) return;
   const int group = (int)(a.heads_q / a.heads_k);
-  const int h0 = blockIdx.y * GT;
+  const int h0 = blockIdx.x * GT;
   const int kh = h0 / group;
   const int vis_begin = decode_vis_begin(a, r.k_len);
   const int begin = vis_begin + split * span;
@@ -111,18 +165,25 @@ __global__ __launch_bounds__(DEC_THREADS, 2) void decode_kernel(const fa_attn_ar
   const int64_t tq = r.q_begin;
   const int S = a.num_splits;
 
-  const bool cap = a.softcap > 0.0f;
-  const float qscale = a.softmax_scale * descale_of(a.q_descale, a.q_descale_stride, b, kh) *
-                       descale_of(a.k_descale, a.k_descale_stride, b, kh) * (cap ? 1.0f : LOG2E);
+  const float sscale = a.softmax_scale * descale_of(a.q_descale, a.q_descale_stride, b, kh) *
+                       descale_of(a.k_descale, a.k_descale_stride, b, kh) * (CAP ? 1.0f : LOG2E);
+  const float cap_in = CAP ? 2.0f * LOG2E / a.softcap : 0.0f, cap_out = a.softcap * LOG2E;
   const float vscale = descale_of(a.v_descale, a.v_descale_stride, b, kh);
 
-  float q[GT][EK];
+  // Query pairs of this lane's dims (l16 * EK ..), unscaled, in the compute type.
+  uint32_t qp[GT][EK / 2];
 #pragma unroll
-  for (int g = 0; g < GT; ++g)
+  for (int g = 0; g < GT; ++g) {
+    const int64_t q0 = tq * a.q_stride[0] + (int64_t)(h0 + g) * a.q_stride[1];
+    if (a.q_stride[2] == 1) {
+      load_words<EK * 2>((const char*)a.q + (q0 + l16 * EK) * 2, qp[g]);
+    } else {
 #pragma unroll
-    for (int e = 0; e < EK; ++e)
-      q[g][e] = load_any(a.q, tq * a.q_stride[0] + (int64_t)(h0 + g) * a.q_stride[1] + (int64_t)(l16 * EK + e) * a.q_stride[2],
-                         a.q_dtype) * qscale;
+      for (int j = 0; j < EK / 2; ++j)
+        qp[g][j] = pack_pair_bits<CT>(load_elem<CT>(a.q, q0 + (int64_t)(l16 * EK + 2 * j) * a.q_stride[2]),
+                                      load_elem<CT>(a.q, q0 + (int64_t)(l16 * EK + 2 * j + 1) * a.q_stride[2]));
+    }
+  }
 
   float m[GT], l[GT], acc[GT][EV];
   const bool seed = a.sinks && split == 0 && wave == 0 && rg == 0;
@@ -134,96 +195,184 @@ __global__ __launch_bounds__(DEC_THREADS, 2) void decode_kernel(const fa_attn_ar
     for (int e = 0; e < EV; ++e) acc[g][e] = 0.0f;
   }
 
-  const int64_t base = (int64_t)r.k_base + r.left;   // storage position of key 0
-  const int64_t plo = base + begin, phi = base + end;
-  const char* kc = (const char*)a.k;
-  const char* vc = (const char*)a.v;
-  const int64_t P = a.page_size;
+  // Storage positions [plo, phi) of this split (packed rows or paged slots).
+  const int plo = r.k_base + r.left + begin, phi = r.k_base + r.left + end;
+  const int P = (int)a.page_size;
+  const int sb0 = (plo & ~(STEP - 1)) + STEP * wave;
+  const int nsteps = (begin < end && sb0 < phi) ? (phi - 1 - sb0) / WSTRIDE + 1 : 0;
 
-  for (int64_t sb = (plo & ~(int64_t)(STEP - 1)) + STEP * wave; sb < phi; sb += 4 * STEP) {
-    const int64_t rpos = sb + DEC_NT * rg;
-    int64_t koff = 0, voff = 0;
-    if (rpos + DEC_NT > plo && rpos < phi) {
-      if (P) {
-        const int64_t page = rpos / P;
-        const int64_t blk = a.block_table[b * a.bt_stride[0] + page * a.bt_stride[1]];
-        const int64_t in = rpos - page * P;
-        koff = blk * a.k_stride[0] + in * a.k_stride[1] + (int64_t)kh * a.k_stride[2];
-        voff = blk * a.v_stride[0] + in * a.v_stride[1] + (int64_t)kh * a.v_stride[2];
-      } else {
-        koff = rpos * a.k_stride[1] + (int64_t)kh * a.k_stride[2];
-        voff = rpos * a.v_stride[1] + (int64_t)kh * a.v_stride[2];
-      }
+  // Byte addressing.  Row r of page blk of KV head kh, dims from l16 * E:
+  // base + blk * page_stride + r * row_stride + kh * head_stride + l16 * E * bytes.
+  const uint32_t kpage_b = (uint32_t)(a.k_stride[0] * KT::bytes), vpage_b = (uint32_t)(a.v_stride[0] * VT::bytes);
+  const uint32_t krow_b = (uint32_t)(a.k_stride[1] * KT::bytes), vrow_b = (uint32_t)(a.v_stride[1] * VT::bytes);
+  const char* kbase = (const char*)a.k + (int64_t)kh * a.k_stride[2] * KT::bytes + l16 * KB;
+  const char* vbase = (const char*)a.v + (int64_t)kh * a.v_stride[2] * VT::bytes + l16 * VB;
+
+  // Address of the split's first key: the read target of rows with no valid position.
+  const char* ksafe = kbase;
+  const char* vsafe = vbase;
+  if (nsteps > 0) {
+    if (P) {
+      const uint32_t blk = (uint32_t)load_invariant_i32(a.block_table, b * a.bt_stride[0] + (int64_t)(plo / P) * a.bt_stride[1]);
+      ksafe += (uint64_t)blk * kpage_b + (uint64_t)(plo % P) * krow_b;
+      vsafe += (uint64_t)blk * vpage_b + (uint64_t)(plo % P) * vrow_b;
+    } else {
+      ksafe += (uint64_t)plo * krow_b;
+      vsafe += (uint64_t)plo * vrow_b;
     }
-    uint32_t kw[DEC_NT][KB / 4], vw[DEC_NT][VB / 4];
-    bool ok[DEC_NT];
+  }
+
+  // Block-table window: tab[c] of lane 4u + row holds the page of that row at
+  // step t0 + 16c + u (0 for rows outside the split).
+  int tab[4] = {0, 0, 0, 0};
+  auto load_tab = [&](int t0) {
 #pragma unroll
-    for (int i = 0; i < DEC_NT; ++i) {
-      ok[i] = rpos + i >= plo && rpos + i < phi;
-      if (ok[i]) {
-        load_words<KB>(kc + (koff + i * a.k_stride[1] + l16 * EK) * KT::bytes, kw[i]);
-      } else {
-#pragma unroll
-        for (int w = 0; w < KB / 4; ++w) kw[i][w] = 0u;
-      }
+    for (int c = 0; c < 4; ++c) {
+      const int tt = t0 + 16 * c + (lane >> 2);
+      const int rp = sb0 + WSTRIDE * tt + NT * (lane & 3);
+      const bool ok = tt < nsteps && rp + NT > plo && rp < phi;
+      tab[c] = ok ? a.block_table[b * a.bt_stride[0] + (int64_t)(rp / P) * a.bt_stride[1]] : 0;
     }
-#pragma unroll
-    for (int i = 0; i < DEC_NT; ++i) {
-      if (ok[i]) {
-        load_words<VB>(vc + (voff + i * a.v_stride[1] + l16 * EV) * VT::bytes, vw[i]);
-      } else {
-#pragma unroll
-        for (int w = 0; w < VB / 4; ++w) vw[i][w] = 0u;
-      }
+  };
+
+  // Row state advanced once per issued step: paged -> row index inside the
+  // page (and its byte offsets); packed -> byte offsets of the row itself.
+  const int rp0 = sb0 + NT * rg;
+  int inr = P ? rp0 % P : 0;
+  const int wrap = P ? WSTRIDE % P : 0;
+  uint64_t kin = P ? (uint64_t)inr * krow_b : (uint64_t)rp0 * krow_b;
+  uint64_t vin = P ? (uint64_t)inr * vrow_b : (uint64_t)rp0 * vrow_b;
+  const uint64_t kstep_packed = (uint64_t)WSTRIDE * krow_b, vstep_packed = (uint64_t)WSTRIDE * vrow_b;
+
+  auto issue = [&](int t, uint32_t (&kw)[NT][KB / 4], uint32_t (&vw)[NT][VB / 4]) {
+    const int sbt = sb0 + WSTRIDE * t;
+    const bool full = sbt >= plo && sbt + STEP <= phi;   // every position of the wave step is in the split
+    const char* krow = kbase + kin;
+    const char* vrow = vbase + vin;
+    if (P) {
+      const int u = t & 63, c = u >> 4;
+      const int e = c == 0 ? tab[0] : c == 1 ? tab[1] : c == 2 ? tab[2] : tab[3];
+      const uint32_t blk = (uint32_t)__builtin_amdgcn_ds_bpermute((((u & 15) << 2) + rg) << 2, e);
+      krow += (uint64_t)blk * kpage_b;
+      vrow += (uint64_t)blk * vpage_b;
     }
-    float s[GT][DEC_NT];
+    if (full) {
 #pragma unroll
-    for (int i = 0; i < DEC_NT; ++i) {
-      float kf[EK];
-      words_to_f32<KT, EK>(kw[i], kf);
+      for (int i = 0; i < NT; ++i) load_words<KB>(krow + i * krow_b, kw[i]);
+#pragma unroll
+      for (int i = 0; i < NT; ++i) load_words<VB>(vrow + i * vrow_b, vw[i]);
+    } else {
+      const int rp = rp0 + WSTRIDE * t;
+      const bool row_ok = rp + NT > plo && rp < phi;
+      const int lo_i = row_ok ? max(plo - rp, 0) : 0;
+      const int hi_i = row_ok ? min(phi - rp, NT) - 1 : 0;
+      if (!row_ok) {
+        krow = ksafe;
+        vrow = vsafe;
+      }
+#pragma unroll
+      for (int i = 0; i < NT; ++i) load_words<KB>(krow + min(max(i, lo_i), hi_i) * krow_b, kw[i]);
+#pragma unroll
+      for (int i = 0; i < NT; ++i) load_words<VB>(vrow + min(max(i, lo_i), hi_i) * vrow_b, vw[i]);
+    }
+    if (P) {
+      inr += wrap;
+      kin += (uint64_t)wrap * krow_b;
+      vin += (uint64_t)wrap * vrow_b;
+      if (inr >= P) {
+        inr -= P;
+        kin -= (uint64_t)P * krow_b;
+        vin -= (uint64_t)P * vrow_b;
+      }
+    } else {
+      kin += kstep_packed;
+      vin += vstep_packed;
+    }
+  };
+
+  auto compute = [&](int t, const uint32_t (&kw)[NT][KB / 4], const uint32_t (&vw)[NT][VB / 4]) {
+    const int sbt = sb0 + WSTRIDE * t;
+    const bool full = sbt >= plo && sbt + STEP <= phi;
+    const int rp = rp0 + WSTRIDE * t;
+    float s[GT][NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+      uint32_t kp[EK / 2];
+      k_pairs<CT, KT, EK>(kw[i], kp);
 #pragma unroll
       for (int g = 0; g < GT; ++g) {
         float dot = 0.0f;
 #pragma unroll
-        for (int e = 0; e < EK; ++e) dot = fmaf(q[g][e], kf[e], dot);
+        for (int j = 0; j < EK / 2; ++j) dot = dot2<CT>(qp[g][j], kp[j], dot);
         s[g][i] = dot;
       }
     }
 #pragma unroll
     for (int g = 0; g < GT; ++g)
 #pragma unroll
-      for (int i = 0; i < DEC_NT; ++i) {
-        float v = row16_sum(s[g][i]);
-        if (cap) v = a.softcap * tanhf(v / a.softcap) * LOG2E;
-        s[g][i] = ok[i] ? v : -INFINITY;
+      for (int i = 0; i < NT; ++i) {
+        float v = row16_sum(s[g][i]) * sscale;
+        if constexpr (CAP) v = cap_out * (1.0f - 2.0f * __builtin_amdgcn_rcpf(fast_exp2(v * cap_in) + 1.0f));
+        s[g][i] = v;
       }
+    if (!full) {
+#pragma unroll
+      for (int i = 0; i < NT; ++i) {
+        const bool ok = rp + i >= plo && rp + i < phi;
+#pragma unroll
+        for (int g = 0; g < GT; ++g) s[g][i] = ok ? s[g][i] : -INFINITY;
+      }
+    }
 #pragma unroll
     for (int g = 0; g < GT; ++g) {
       float mx = s[g][0];
 #pragma unroll
-      for (int i = 1; i < DEC_NT; ++i) mx = fmaxf(mx, s[g][i]);
-      const float m_new = fmaxf(m[g], mx);
-      const float ref = m_new == -INFINITY ? 0.0f : m_new;
-      const float f = fast_exp2(m[g] - ref);
+      for (int i = 1; i < NT; ++i) mx = fmaxf(mx, s[g][i]);
+      const bool need = mx > m[g] + DEC_RESCALE;
+      if (__builtin_expect(__any(need), 0)) {
+        const float f = need ? fast_exp2(m[g] - mx) : 1.0f;
+        if (need) m[g] = mx;
+        l[g] *= f;
+#pragma unroll
+        for (int e = 0; e < EV; ++e) acc[g][e] *= f;
+      }
+      const float ref = m[g] == -INFINITY ? 0.0f : m[g];
       float sum = 0.0f;
 #pragma unroll
-      for (int i = 0; i < DEC_NT; ++i) {
+      for (int i = 0; i < NT; ++i) {
         s[g][i] = fast_exp2(s[g][i] - ref);
         sum += s[g][i];
       }
-      l[g] = l[g] * f + sum;
-      m[g] = m_new;
-#pragma unroll
-      for (int e = 0; e < EV; ++e) acc[g][e] *= f;
+      l[g] += sum;
     }
 #pragma unroll
-    for (int i = 0; i < DEC_NT; ++i) {
+    for (int i = 0; i < NT; ++i) {
       float vf[EV];
       words_to_f32<VT, EV>(vw[i], vf);
 #pragma unroll
       for (int g = 0; g < GT; ++g)
 #pragma unroll
         for (int e = 0; e < EV; ++e) acc[g][e] = fmaf(s[g][i], vf[e], acc[g][e]);
+    }
+  };
+
+  if (nsteps > 0) {
+    uint32_t kwa[NT][KB / 4], vwa[NT][VB / 4], kwb[NT][KB / 4], vwb[NT][VB / 4];
+    if (P) load_tab(0);
+    issue(0, kwa, vwa);
+    for (int t = 0;; t += 2) {
+      if (t + 1 < nsteps) {
+        if (P && ((t + 1) & 63) == 0) load_tab(t + 1);
+        issue(t + 1, kwb, vwb);
+      }
+      compute(t, kwa, vwa);
+      if (t + 1 >= nsteps) break;
+      if (t + 2 < nsteps) {
+        if (P && ((t + 2) & 63) == 0) load_tab(t + 2);
+        issue(t + 2, kwa, vwa);
+      }
+      compute(t + 1, kwb, vwb);
+      if (t + 2 >= nsteps) break;
     }
   }
 
@@ -285,6 +434,11 @@ __global__ __launch_bounds__(DEC_THREADS, 2) void decode_kernel(const fa_attn_ar
 
 // One wavefront merges the valid splits of one (request, head) row into the
 // caller's output.  Splits past the request's last key were never written.
+// Split weights exp(lse_s - max) are computed once, 64 splits at a time (split
+// s0 + j on lane j), and broadcast with readlane; every lane accumulates the
+// dims lane, lane + 64, ... so each partial row is one coalesced read.
+constexpr int MERGE_DIMS = 256 / 64;   // dims per lane: the decode kernels cover Dv <= 256
+
 __global__ __launch_bounds__(256) void decode_merge_kernel(const fa_attn_args a, const int span) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + wave;
@@ -293,49 +447,70 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const fa_attn_args a,
   const RequestInfo r = load_request(a, b);
   if (r.q_len != 1) return;
   const int S = a.num_splits;
+  const int DV = (int)a.head_dim_v;
   const int n = r.k_len - decode_vis_begin(a, r.k_len);
   const int nv = n > 0 ? min(S, (n + span - 1) / span) : 1;
   const float* plse = a.partial_lse + row * S;
-  const float* po = a.partial_out + row * S * a.head_dim_v;
+  const float* po = a.partial_out + row * S * DV;
   float peak = -INFINITY;
   for (int s = lane; s < nv; s += 64) peak = fmaxf(peak, plse[s]);
   peak = wave_max(peak);
   const float ref = peak == -INFINITY ? 0.0f : peak;
+  float acc[MERGE_DIMS];
+#pragma unroll
+  for (int k = 0; k < MERGE_DIMS; ++k) acc[k] = 0.0f;
   float denom = 0.0f;
-  for (int s = lane; s < nv; s += 64) denom += expf(plse[s] - ref);
+  for (int s0 = 0; s0 < nv; s0 += 64) {
+    const float w = s0 + lane < nv ? expf(plse[s0 + lane] - ref) : 0.0f;
+    denom += w;
+    const int cnt = min(64, nv - s0);
+    for (int j = 0; j < cnt; ++j) {
+      const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
+      if (ws > 0.0f) {   // zero-weight splits are never read
+        const float* src = po + (int64_t)(s0 + j) * DV;
+#pragma unroll
+        for (int k = 0; k < MERGE_DIMS; ++k)
+          if (lane + 64 * k < DV) acc[k] = fmaf(ws, src[lane + 64 * k], acc[k]);
+      }
+    }
+  }
   denom = wave_sum(denom);
   const int64_t tq = r.q_begin;
-  for (int d = lane; d < a.head_dim_v; d += 64) {
-    float v = 0.0f;
-    for (int s = 0; s < nv; ++s) {
-      const float w = expf(plse[s] - ref);
-      if (w > 0.0f) v = fmaf(w, po[(int64_t)s * a.head_dim_v + d], v);
-    }
-    store_any(a.out, tq * a.out_stride[0] + h * a.out_stride[1] + (int64_t)d * a.out_stride[2], a.out_dtype,
-              denom > 0.0f ? v / denom : 0.0f);
+  const float inv = denom > 0.0f ? 1.0f / denom : 0.0f;
+#pragma unroll
+  for (int k = 0; k < MERGE_DIMS; ++k) {
+    const int d = lane + 64 * k;
+    if (d < DV)
+      store_any(a.out, tq * a.out_stride[0] + h * a.out_stride[1] + (int64_t)d * a.out_stride[2], a.out_dtype,
+                acc[k] * inv);
   }
   if (lane == 0) a.lse[h * a.lse_stride[0] + tq * a.lse_stride[1]] = denom > 0.0f ? peak + logf(denom) : -INFINITY;
 }
 
 using DecodeKernel = void (*)(fa_attn_args, int);
 
-template <typename KT, typename VT, int D, int DV>
+template <typename CT, typename KT, typename VT, int D, int DV, bool CAP>
 DecodeKernel pick_group(int gt) {
   switch (gt) {
-    case 4: if constexpr (4 * (D + DV) <= 64 * 16) return decode_kernel<KT, VT, D, DV, 4>; else return nullptr;
-    case 2: if constexpr (2 * (D + DV) <= 64 * 16) return decode_kernel<KT, VT, D, DV, 2>; else return nullptr;
-    case 1: return decode_kernel<KT, VT, D, DV, 1>;
+    case 4: if constexpr (4 * (D + DV) <= 64 * 16) return decode_kernel<CT, KT, VT, D, DV, 4, CAP>; else return nullptr;
+    case 2: if constexpr (2 * (D + DV) <= 64 * 16) return decode_kernel<CT, KT, VT, D, DV, 2, CAP>; else return nullptr;
+    case 1: return decode_kernel<CT, KT, VT, D, DV, 1, CAP>;
     default: return nullptr;
   }
 }
 
-template <typename KT, typename VT>
-DecodeKernel pick_dims(int64_t d, int64_t dv, int gt) {
-  if (d == 64 && dv == 64) return pick_group<KT, VT, 64, 64>(gt);
-  if (d == 128 && dv == 128) return pick_group<KT, VT, 128, 128>(gt);
-  if (d == 192 && dv == 128) return pick_group<KT, VT, 192, 128>(gt);
-  if (d == 256 && dv == 256) return pick_group<KT, VT, 256, 256>(gt);
+template <typename CT, typename KT, typename VT, bool CAP>
+DecodeKernel pick_dims_cap(int64_t d, int64_t dv, int gt) {
+  if (d == 64 && dv == 64) return pick_group<CT, KT, VT, 64, 64, CAP>(gt);
+  if (d == 128 && dv == 128) return pick_group<CT, KT, VT, 128, 128, CAP>(gt);
+  if (d == 192 && dv == 128) return pick_group<CT, KT, VT, 192, 128, CAP>(gt);
+  if (d == 256 && dv == 256) return pick_group<CT, KT, VT, 256, 256, CAP>(gt);
   return nullptr;
+}
+
+template <typename CT, typename KT, typename VT>
+DecodeKernel pick_dims(int64_t d, int64_t dv, int gt, bool cap) {
+  return cap ? pick_dims_cap<CT, KT, VT, true>(d, dv, gt) : pick_dims_cap<CT, KT, VT, false>(d, dv, gt);
 }
 
 int elem_size(int dt) { return dt == FA_F32 ? 4 : dt == FA_E4M3 ? 1 : 2; }
@@ -362,17 +537,29 @@ DecodeKernel select_decode(const fa_attn_args& a, int* gt_out) {
   if (a.k_dtype != a.v_dtype) return nullptr;
   if (a.mask_kind != 0 || a.alibi) return nullptr;
   if (a.page_size && a.page_size % DEC_PAGE_ALIGN) return nullptr;
+  // Page and row strides are 32-bit byte counts in the kernel's addressing.
+  for (int i = 0; i < 3; ++i)
+    if (a.k_stride[i] < 0 || a.v_stride[i] < 0 || a.k_stride[i] * elem_size(a.k_dtype) >= (1ll << 32) ||
+        a.v_stride[i] * elem_size(a.v_dtype) >= (1ll << 32))
+      return nullptr;
   if (a.k_stride[3] != 1 || a.v_stride[3] != 1) return nullptr;
   const int esz = elem_size(a.k_dtype);
   if ((a.head_dim_qk / 16) * esz % 4 || (a.head_dim_v / 16) * esz % 4) return nullptr;
   if (!chunk_aligned(a.k, a.k_stride, 3, esz, (int)(a.head_dim_qk / 16) * esz)) return nullptr;
   if (!chunk_aligned(a.v, a.v_stride, 3, esz, (int)(a.head_dim_v / 16) * esz)) return nullptr;
+  // Q.K runs on 16-bit pairs of the query's type: 16-bit K must match it,
+  // FP8 K widens exactly to either.
+  if (a.q_dtype != FA_BF16 && a.q_dtype != FA_F16) return nullptr;
+  if (a.q_stride[2] == 1 && !chunk_aligned(a.q, a.q_stride, 2, 2, (int)(a.head_dim_qk / 16) * 2)) return nullptr;
   const int gt = decode_group_tile(a);
   *gt_out = gt;
+  const bool qbf = a.q_dtype == FA_BF16, cap = a.softcap > 0.0f;
+  const int64_t dq = a.head_dim_qk, dv = a.head_dim_v;
   switch (a.k_dtype) {
-    case FA_BF16: return pick_dims<BF16T, BF16T>(a.head_dim_qk, a.head_dim_v, gt);
-    case FA_F16: return pick_dims<F16T, F16T>(a.head_dim_qk, a.head_dim_v, gt);
-    case FA_E4M3: return pick_dims<E4M3T, E4M3T>(a.head_dim_qk, a.head_dim_v, gt);
+    case FA_BF16: return qbf ? pick_dims<BF16T, BF16T, BF16T>(dq, dv, gt, cap) : nullptr;
+    case FA_F16: return qbf ? nullptr : pick_dims<F16T, F16T, F16T>(dq, dv, gt, cap);
+    case FA_E4M3:
+      return qbf ? pick_dims<BF16T, E4M3T, E4M3T>(dq, dv, gt, cap) : pick_dims<F16T, E4M3T, E4M3T>(dq, dv, gt, cap);
     default: return nullptr;
   }
 }
@@ -399,9 +586,9 @@ extern "C" int fa_decode_fwd(const fa_attn_args* a, void* stream) {
   FA_REQUIRE(a->num_splits == 1 || (a->partial_out && a->partial_lse), "fa_decode_fwd: splits need partial buffers");
   FA_REQUIRE(a->batch <= 65535, "fa_decode_fwd: batch exceeds the grid limit");
   const int64_t head_groups = a->heads_q / gt;
-  FA_REQUIRE(head_groups <= 65535, "fa_decode_fwd: too many heads");
+  FA_REQUIRE(a->num_splits <= 65535, "fa_decode_fwd: too many splits");
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid((unsigned)a->num_splits, (unsigned)head_groups, (unsigned)a->batch);
+  const dim3 grid((unsigned)head_groups, (unsigned)a->num_splits, (unsigned)a->batch);
   hipLaunchKernelGGL(kern, grid, dim3(DEC_THREADS), 0, s, *a, (int)a->split_span);
   rc = fa_check_launch("fa_decode_fwd");
   if (rc || a->num_splits == 1) return rc;

@@ -3,7 +3,7 @@
 Counterpart of flash_attn_mps/_decode.py:40-99.  The split plan uses only
 host-known sizes: the effective maximum key count (clipped by a left window,
 _decode.py:63) and the number of (request, head-group) work units.  A split
-covers `span` keys; the default span starts at 512 keys and halves (down to
+covers `span` keys; the default span starts at 2048 keys and halves (down to
 128) until the grid holds at least 2048 workgroups, so small batches still
 fill the 256 compute units.  An explicit num_splits is honoured.
 """
@@ -13,6 +13,8 @@ from . import _lib
 from ._attention import build_args
 
 _MIN_WORKGROUPS = 2048
+_START_SPAN = 2048
+_MIN_SPAN = 128
 
 
 def _round_up(x, m):
@@ -26,8 +28,8 @@ def split_plan(batch, head_groups, effective_max, num_splits):
     if num_splits:
         span = max(32, _round_up(-(-effective_max // num_splits), 32))
         return max(1, min(num_splits, -(-effective_max // span))), span
-    span = 512
-    while span > 128 and batch * head_groups * -(-effective_max // span) < _MIN_WORKGROUPS:
+    span = _START_SPAN
+    while span > _MIN_SPAN and batch * head_groups * -(-effective_max // span) < _MIN_WORKGROUPS:
         span //= 2
     return -(-effective_max // span), span
 
