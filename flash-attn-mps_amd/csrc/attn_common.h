@@ -17,15 +17,17 @@ struct RequestInfo {
   bool causal;
 };
 
+// The metadata is read-only for the whole launch, so it is read through the
+// scalar cache (uniform values stay in SGPRs for every caller with a uniform b).
 FA_DEV RequestInfo load_request(const fa_attn_args& a, int64_t b) {
   RequestInfo r;
-  r.q_begin = a.cu_seqlens_q[b * a.cu_q_stride];
-  r.q_len = a.cu_seqlens_q[(b + 1) * a.cu_q_stride] - r.q_begin;
-  const int kcu = a.cu_seqlens_k ? a.cu_seqlens_k[b * a.cu_k_stride] : 0;
+  r.q_begin = load_invariant_i32(a.cu_seqlens_q, b * a.cu_q_stride);
+  r.q_len = load_invariant_i32(a.cu_seqlens_q, (b + 1) * a.cu_q_stride) - r.q_begin;
+  const int kcu = a.cu_seqlens_k ? load_invariant_i32(a.cu_seqlens_k, b * a.cu_k_stride) : 0;
   r.k_base = a.page_size ? 0 : kcu;
-  r.k_len = a.seqused_k ? a.seqused_k[b * a.used_k_stride]
-                        : a.cu_seqlens_k[(b + 1) * a.cu_k_stride] - kcu;
-  r.left = a.leftpad_k ? a.leftpad_k[b * a.leftpad_stride] : 0;
+  r.k_len = a.seqused_k ? load_invariant_i32(a.seqused_k, b * a.used_k_stride)
+                        : load_invariant_i32(a.cu_seqlens_k, (b + 1) * a.cu_k_stride) - kcu;
+  r.left = a.leftpad_k ? load_invariant_i32(a.leftpad_k, b * a.leftpad_stride) : 0;
   r.causal = a.causal_by_batch ? a.causal_by_batch[b * a.causal_stride] != 0 : a.causal != 0;
   return r;
 }

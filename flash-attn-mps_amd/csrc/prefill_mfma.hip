@@ -9,43 +9,54 @@
 // in {(64,64), (128,128), (256,256), (192,128)}.
 //
 // gfx950 design
-// * A workgroup is W waves; each wave owns NB x 32 query rows of one head.
-//   K/V tiles of BN = 32*KT keys are staged in LDS, double buffered; the
-//   next tile's global loads are issued before the current tile's MFMAs and
-//   only waited for when that tile is written to LDS.
-// * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16
-//   (A = K rows from LDS, B = Q^T held in registers for the whole kernel).  A
-//   lane then holds 32 keys of ONE query column, so the row max / row sum of
-//   the softmax are in-lane reductions plus one exchange with lane ^ 32.
-// * K rows are stored in LDS at row sigma(r) (bits 2 and 3 of r swapped) so
-//   that, in the score layout, every lane's 8 consecutive accumulator values
-//   are 8 consecutive keys.  Those 8 probabilities, rounded to bf16/fp16, are
-//   directly the B operand of O^T += V^T P^T; V is written transposed into LDS
-//   (V^T rows = head dims, 16-byte key chunks XOR-swizzled) so its A operand
-//   is one 16-byte LDS read.
-// * K/V tiles are read with buffer loads: each 16-key group gets a scalar
-//   resource descriptor whose base is the group's first row and whose size
-//   ends at the request's last key, so rows past the keys read as zero in
-//   hardware and lane offsets are loop-invariant registers.
-// * exp2 with softmax_scale*log2(e) folded into one FMA; the running max is
-//   only moved (and O rescaled) when a tile raises it by more than 2^8, which
-//   keeps probabilities <= 256 and skips almost all rescales.
+// * A workgroup is W waves; each wave owns 32 query rows of one head.  K/V
+//   tiles of 64 keys live in LDS, two K and two V buffers.
+// * Tiles move global -> LDS with buffer_load ... lds (16 bytes a lane, one
+//   contiguous KiB per instruction): no registers, no VALU.  Every 16-key
+//   group gets a scalar buffer descriptor bounded at the request's last key,
+//   so rows past the end read as zero; lane offsets are loop-invariant.
+// * LDS layout, K and V alike: 64-dim column groups of 64 rows x 128 bytes,
+//   the eight 16-byte chunks of a row XOR-swizzled by (row / 2) % 8 (K), the
+//   sixteen 8-byte units by 4 * ((row / 2) % 2) (V).  Every operand read is
+//   bank-conflict free and addressed as a lane register plus an immediate.
+// * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16 (A =
+//   K rows from LDS, B = Q^T held in registers for the whole kernel).  A lane
+//   holds 32 keys of ONE query column, so the row max / sum are in-lane plus
+//   one v_permlane32_swap.  K rows are stored at sigma(r) (bits 2 and 3 of r
+//   swapped) so each lane's 8 consecutive accumulators are 8 consecutive
+//   keys: rounded to bf16/fp16 they are directly the B operand of
+//   O^T += V^T P^T.  The V^T operand is read from the row-major V tile with
+//   ds_read_b64_tr_b16 (two per MFMA).
+// * Software pipeline per wave over 32-key stages: while the MFMAs of
+//   S(s+1) = K(s+1) Q^T run, the VALU turns S(s) into P(s) (exp2, pack, row
+//   sums); while the MFMAs of O += V(s) P(s) run, the VALU takes the row max
+//   of S(s+1).  One barrier per 64-key tile; the next tiles' K and V are in
+//   flight meanwhile.
+// * exp2 with softmax_scale*log2(e) folded into one FMA; the running max only
+//   moves (and O is rescaled) when a tile raises it by more than 2^8.
 // * Work is ordered per XCD: each XCD runs whole (request, KV head) pairs one
-//   after another, query blocks heaviest-first within a pair (the causal
-//   triangle makes late blocks the longest), so resident workgroups share K/V
-//   in their XCD's L2.
+//   after another, query blocks heaviest-first within a pair, so resident
+//   workgroups share K/V in their XCD's L2.
 #include "attn_common.h"
+
+#include <type_traits>
 
 namespace {
 
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
 typedef __attribute__((ext_vector_type(16))) float f32x16;
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+typedef __attribute__((ext_vector_type(4))) short s16x4;
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-constexpr float PF_RESCALE = 8.0f;  // log2 headroom before the running max moves
+constexpr float PF_RESCALE = 8.0f;        // log2 headroom before the running max moves
+constexpr int PF_BN = 64;                 // keys per tile
+constexpr int PF_GROUP_BYTES = 64 * 128;  // one 64-dim column group of a tile
 
 template <typename T> FA_DEV f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c);
 template <> FA_DEV f32x16 mfma32<BF16T>(u32x4 a, u32x4 b, f32x16 c) {
@@ -73,69 +84,66 @@ template <> FA_DEV uint32_t pack2<F16T>(float lo, float hi) {
 // Swap bits 2 and 3 of a row index (an involution).
 FA_DEV int sigma(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 
+// x combined with the value of lane ^ 32 (v_permlane32_swap exchanges the
+// wave halves; max / sum of the two results is symmetric in them).
+FA_DEV float max_hh(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+FA_DEV float sum_hh(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// 16 bytes a lane from a buffer straight into LDS at lds + 16 * lane.  The
+// host compilation pass rejects this builtin (and would drop the kernel
+// stub without a diagnostic), so only the device pass sees the call.
+// IMM is added to both the global and the LDS address.
+template <int IMM>
+FA_DEV void dma16(__amdgpu_buffer_rsrc_t rsrc, char* lds, int voffset) {
+#if __HIP_DEVICE_COMPILE__
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(lds - IMM), 16, voffset, 0, IMM, 0);
+#endif
+}
+
+// One row block (8 rows x 128 bytes) of each of N column groups.
+template <int N, int I = 0>
+FA_DEV void dma_columns(__amdgpu_buffer_rsrc_t rsrc, char* lds, int voffset) {
+  if constexpr (I < N) {
+    dma16<128 * I>(rsrc, lds + I * PF_GROUP_BYTES, voffset);
+    dma_columns<N, I + 1>(rsrc, lds, voffset);
+  }
+}
+
+FA_DEV u32x4 lds_read16(const char* base, int off) { return *(const u32x4*)(base + off); }
+FA_DEV u32x2 lds_read_tr(const char* base, int off) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + off)));
+}
+
 struct PrefillShape {
   int n_qblocks;
   int log2_page;   // paged K/V: page size = 1 << log2_page
 };
 
-// True when every wave's rows of every V unit stay inside one 16-key group
-// (K chunks always do for the supported head dims), so group storage bases
-// are wave-uniform.
-constexpr bool groups_uniform(int dq, int dv, int threads) {
-  const int kcpr = dq / 8, vcpr = dv / 8;
-  for (int c = 0; c * threads < 64 * kcpr; ++c)
-    for (int w = 0; w * 64 < threads; ++w) {
-      const int s = 64 * w + threads * c, e = s + 63;
-      if ((s / kcpr) / 16 != (e / kcpr) / 16) return false;
-    }
-  for (int u = 0; u * threads < 16 * vcpr; ++u)
-    for (int w = 0; w * 64 < threads; ++w) {
-      const int s = 64 * w + threads * u;
-      if (s >= 16 * vcpr) continue;
-      const int e = s + 63 < 16 * vcpr - 1 ? s + 63 : 16 * vcpr - 1;
-      if ((4 * (s / vcpr)) / 16 != (4 * (e / vcpr) + 3) / 16) return false;
-    }
-  return true;
-}
-
-constexpr bool k_groups_uniform(int dq, int threads) {
-  const int kcpr = dq / 8;
-  for (int c = 0; c * threads < 64 * kcpr; ++c)
-    for (int w = 0; w * 64 < threads; ++w) {
-      const int s = 64 * w + threads * c, e = s + 63;
-      if ((s / kcpr) / 16 != (e / kcpr) / 16) return false;
-    }
-  return true;
-}
-
-template <typename T, int DQ, int DV, int NB, int KT, int W, int MINB, bool CAUSAL>
+template <typename T, int DQ, int DV, int W, int MINB, bool CAUSAL, bool CAP>
 __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_args a, const PrefillShape shp) {
-  constexpr int THREADS = 64 * W;
-  constexpr int BM = W * NB * 32;
-  constexpr int BN = 32 * KT;
+  constexpr int BM = 32 * W;
   constexpr int KST = DQ / 16;                 // k-steps of the QK^T MFMA
-  constexpr int DB = DV / 32;                  // 32-row blocks of O^T
-  constexpr int KLD = DQ + 8;                  // LDS row stride of K (elements)
-  constexpr int VLD = BN + 8;                  // LDS row stride of V^T
-  constexpr int KTILE = BN * KLD, VTILE = DV * VLD;
-  constexpr int KCPR = DQ / 8, VCPR = DV / 8;  // 16-byte chunks per K / V row
-  constexpr int KCH = BN * KCPR / THREADS;     // K chunks per thread
-  constexpr int VUNITS = (BN / 4) * VCPR;      // (4 keys x 8 dims) V units per tile
-  constexpr int VPT = (VUNITS + THREADS - 1) / THREADS;
-  constexpr bool UNIFORM_V = groups_uniform(DQ, DV, THREADS);
-  static_assert(KCH >= 1 && BN * KCPR % THREADS == 0, "K staging shape");
-  static_assert(k_groups_uniform(DQ, THREADS), "K chunks must stay inside 16-key groups");
-  static_assert(BN == 64, "the V^T swizzle assumes 8 key chunks per row");
+  constexpr int DB = DV / 32;                  // 32-dim blocks of O^T
+  constexpr int KG = DQ / 64, VG = DV / 64;    // 64-dim column groups
+  constexpr int KTILE = KG * PF_GROUP_BYTES, VTILE = VG * PF_GROUP_BYTES;
+  static_assert(DQ % 64 == 0 && DV % 64 == 0, "head dims are multiples of 64");
 
-  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  char* const kbuf0 = smem;
+  char* const vbuf0 = smem + 2 * KTILE;
 
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int wave_u = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index as a scalar
   // Work order.  Workgroups are dispatched round-robin over the 8 XCDs
   // (XCD = blockIdx % 8), each with its own L2.  XCD x takes the (request,
   // KV head) pairs p = x, x + 8, ... one after another, and within a pair the
-  // query blocks of its G query heads heaviest-first, so the workgroups
-  // resident on an XCD at any time share one pair's K/V in that XCD's L2.
+  // query blocks of its G query heads heaviest-first.
   const int G = (int)(a.heads_q / a.heads_k);
   const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
   const int per_pair = shp.n_qblocks * G;
@@ -153,329 +161,328 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   const int off = r.k_len - r.q_len;   // absolute position of query row i is i + off
   int kv_end = r.k_len;
   if (CAUSAL) kv_end = min(kv_end, min(q0 + BM, r.q_len) - 1 + off + 1);
-  const int n_tiles = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
-
-  const uint16_t* qg = (const uint16_t*)a.q;
-  const uint16_t* kg = (const uint16_t*)a.k;
-  const uint16_t* vg = (const uint16_t*)a.v;
+  const int n_tiles = kv_end > 0 ? (kv_end + PF_BN - 1) / PF_BN : 0;
 
   // Q^T operand for the whole kernel: lane holds Q[row][16kk + 8hh .. +8].
-  const int wq0 = q0 + wave_u * NB * 32;
-  u32x4 qop[NB][KST];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int row = wq0 + nb * 32 + l32;
+  const int wq0 = q0 + wave_u * 32;
+  u32x4 qop[KST];
+  {
+    const int row = wq0 + l32;
     const bool ok = row < r.q_len;
-    const uint16_t* qp = qg + ((int64_t)r.q_begin + row) * a.q_stride[0] + (int64_t)h * a.q_stride[1] + 8 * hh;
+    const uint16_t* qp = (const uint16_t*)a.q + ((int64_t)r.q_begin + row) * a.q_stride[0] +
+                         (int64_t)h * a.q_stride[1] + 8 * hh;
 #pragma unroll
     for (int kk = 0; kk < KST; ++kk) {
       u32x4 v = {0u, 0u, 0u, 0u};
       if (ok) v = *(const u32x4*)(qp + 16 * kk);
-      qop[nb][kk] = v;
+      qop[kk] = v;
     }
   }
-  // Complete the Q loads here: otherwise the loop header cannot prove them
-  // done and every iteration would wait for all in-flight K/V loads before
-  // its first MFMA (s_waitcnt vmcnt(0); expcnt/lgkmcnt left unconstrained).
-  __builtin_amdgcn_s_waitcnt(0x0F70);
 
-  const bool paged = a.page_size != 0;
-  const int lp = shp.log2_page;
-  // Storage offset (elements) of key `key`; per lane only for V layouts whose
-  // wave rows can span two 16-key groups (Dv = 64).
-  auto row_offset = [&](const int64_t* st, int key) -> int64_t {
-    if (paged) {
-      const int page = key >> lp;
-      const int64_t blk = a.block_table[b * a.bt_stride[0] + (int64_t)page * a.bt_stride[1]];
-      return blk * st[0] + (int64_t)(key - (page << lp)) * st[1] + (int64_t)kh * st[2];
-    }
-    return ((int64_t)r.k_base + key) * st[1] + (int64_t)kh * st[2];
-  };
-  auto group_base = [&](const int64_t* st, int key0) -> int64_t {
-    if (paged) {
-      const int64_t blk = load_invariant_i32(a.block_table, b * a.bt_stride[0] + (int64_t)(key0 >> lp) * a.bt_stride[1]);
-      return blk * st[0] + (int64_t)(key0 & ((1 << lp) - 1)) * st[1] + (int64_t)kh * st[2];
-    }
-    return ((int64_t)r.k_base + key0) * st[1] + (int64_t)kh * st[2];
-  };
-
-  // Staging layout.  K: chunk c of a thread is 16 bytes of row idx / KCPR at
-  // column 8 * (idx % KCPR), idx = 64 * wave + THREADS * c + lane, stored at
-  // LDS row sigma(row).  V: unit u of a thread covers 4 keys x 8 dims with
-  // the dims fastest across lanes (coalesced global reads).
-  int kgrp[KCH], koff[KCH], kst[KCH];
-#pragma unroll
-  for (int c = 0; c < KCH; ++c) {
-    const int idx0 = 64 * wave_u + THREADS * c;
-    const int idx = idx0 + lane;
-    const int row = idx / KCPR, col = idx % KCPR;
-    kgrp[c] = (idx0 / KCPR) & ~15;
-    koff[c] = 2 * ((row - kgrp[c]) * (int)a.k_stride[1] + col * 8);   // bytes
-    kst[c] = sigma(row) * KLD + col * 8;
-  }
-  int vgrp[VPT], voff[VPT][4], vst[VPT];
-  bool vunit[VPT];
-#pragma unroll
-  for (int u = 0; u < VPT; ++u) {
-    const int uid0 = 64 * wave_u + THREADS * u;
-    const int uid = uid0 + lane;
-    const int kgp = uid / VCPR, dc = uid % VCPR;
-    vunit[u] = uid < VUNITS;
-    vgrp[u] = (4 * (uid0 / VCPR)) & ~15;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) voff[u][rr] = 2 * ((4 * kgp + rr - vgrp[u]) * (int)a.v_stride[1] + dc * 8);
-    // V^T element (dim, key) lives at dim*VLD + 8*((key/8) ^ ((dim/16) & 7)) + key%8.
-    vst[u] = 8 * dc * VLD + 8 * ((kgp >> 1) ^ ((dc >> 1) & 7)) + 4 * (kgp & 1);
-  }
-
-  // Packed K/V: running address of each group's first key for the current
-  // tile, advanced by one tile per load (no per-tile 64-bit products).
-  const uint16_t* kcur[KCH];
-  const uint16_t* vcur[VPT];
-#pragma unroll
-  for (int c = 0; c < KCH; ++c) kcur[c] = kg + ((int64_t)r.k_base + kgrp[c]) * a.k_stride[1] + (int64_t)kh * a.k_stride[2];
-#pragma unroll
-  for (int u = 0; u < VPT; ++u) vcur[u] = vg + ((int64_t)r.k_base + vgrp[u]) * a.v_stride[1] + (int64_t)kh * a.v_stride[2];
-  const int64_t kstep = (int64_t)BN * a.k_stride[1], vstep = (int64_t)BN * a.v_stride[1];
-  auto group_rsrc = [&](const uint16_t* base, const uint16_t* packed_ptr, const int64_t* st, int key0, int row_elems) {
-    const int nvalid = min(max(r.k_len - key0, 0), 16);
-    const uint16_t* gptr = paged ? (nvalid > 0 ? base + group_base(st, key0) : base) : packed_ptr;
-    const int bytes = nvalid > 0 ? 2 * ((nvalid - 1) * (int)st[1] + row_elems) : 0;
-    return __builtin_amdgcn_make_buffer_rsrc((void*)gptr, (short)0, bytes, 0x00020000);
-  };
-
-  u32x4 kreg[KCH];
-  u32x4 vreg[VPT][4];
-  uint32_t vmask = ~0u;
-  const int64_t safe_v = UNIFORM_V ? 0 : group_base(a.v_stride, 0);
-  auto load_tile = [&](int t0) {
-#pragma unroll
-    for (int c = 0; c < KCH; ++c) {
-      const auto rsrc = group_rsrc(kg, kcur[c], a.k_stride, t0 + kgrp[c], DQ);
-      kcur[c] += kstep;
-      kreg[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, koff[c], 0, 0));
-    }
-#pragma unroll
-    for (int u = 0; u < VPT; ++u) {
-      if (UNIFORM_V) {
-        const auto rsrc = group_rsrc(vg, vcur[u], a.v_stride, t0 + vgrp[u], DV);
-        vcur[u] += vstep;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          vreg[u][rr] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff[u][rr], 0, 0));
-      } else {
-        const int uid = 64 * wave_u + THREADS * u + lane;
-        const int kgp = uid / VCPR, dc = uid % VCPR;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int key = t0 + 4 * kgp + rr;
-          const bool ok = vunit[u] && key < r.k_len;
-          vreg[u][rr] = *(const u32x4*)(vg + (ok ? row_offset(a.v_stride, key) : safe_v) + dc * 8);
-          vmask = ok ? (vmask | (1u << (4 * u + rr))) : (vmask & ~(1u << (4 * u + rr)));
-        }
-      }
-    }
-  };
-  auto store_tile = [&](int buf) {
-    const u32x4 zero = {0u, 0u, 0u, 0u};
-    uint16_t* kl = smem + buf * (KTILE + VTILE);
-#pragma unroll
-    for (int c = 0; c < KCH; ++c) *(u32x4*)(kl + kst[c]) = kreg[c];
-    uint16_t* vl = kl + KTILE;
-#pragma unroll
-    for (int u = 0; u < VPT; ++u) {
-      if (!vunit[u]) continue;
-      if (!UNIFORM_V) {
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          if (!((vmask >> (4 * u + rr)) & 1)) vreg[u][rr] = zero;
-      }
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const uint32_t w0 = vreg[u][0][p], w1 = vreg[u][1][p], w2 = vreg[u][2][p], w3 = vreg[u][3][p];
-        uint2 even, odd;
-        even.x = (w0 & 0xffffu) | (w1 << 16);
-        even.y = (w2 & 0xffffu) | (w3 << 16);
-        odd.x = (w0 >> 16) | (w1 & 0xffff0000u);
-        odd.y = (w2 >> 16) | (w3 & 0xffff0000u);
-        *(uint2*)(vl + vst[u] + (2 * p) * VLD) = even;
-        *(uint2*)(vl + vst[u] + (2 * p + 1) * VLD) = odd;
-      }
-    }
-  };
-
-  const bool cap = a.softcap > 0.0f;
-  const float c_scale = a.softmax_scale * LOG2E;          // raw dot -> log2 units
-  const float cap_in = cap ? a.softmax_scale / a.softcap : 0.0f;
-  const float cap_out = a.softcap * LOG2E;
-  // A sink logit seeds the running state (max = sink, sum = 1) of every row.
-  const float sink2 = a.sinks ? a.sinks[(int64_t)h * a.sink_stride] * LOG2E : -INFINITY;
-
-  float m_run[NB], l_run[NB];
-  f32x16 o[DB][NB];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    m_run[nb] = sink2;
-    l_run[nb] = (a.sinks && hh == 0) ? 1.0f : 0.0f;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) o[db][nb][i] = 0.0f;
-  }
-
-  const bool wave_rows = wq0 < r.q_len;
-  const int wave_qabs_lo = wq0 + off;
-  const int wave_qabs_hi = min(wq0 + NB * 32, r.q_len) - 1 + off;
-
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
+  // Rows past the request's last key are never written by the DMA loads of
+  // some hardware paths; zeroed V buffers keep p * v finite for them.
+  for (int i = tid; i < 2 * VTILE / 16; i += 64 * W) {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    *(u32x4*)(vbuf0 + 16 * i) = z;
   }
   __syncthreads();
 
-  for (int j = 0; j < n_tiles; ++j) {
-    const int buf = j & 1;
-    const int t0 = j * BN;
-    if (j + 1 < n_tiles) load_tile(t0 + BN);
-    const bool active = wave_rows && (!CAUSAL || t0 <= wave_qabs_hi);
-    if (active) {
-      const uint16_t* kl = smem + buf * (KTILE + VTILE);
-      const uint16_t* vl = kl + KTILE;
-      f32x16 s[KT][NB];
-#pragma unroll
-      for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) s[kt][nb][i] = 0.0f;
-      const uint16_t* krow = kl + l32 * KLD + 8 * hh;
-#pragma unroll
-      for (int kk = 0; kk < KST; ++kk)
-#pragma unroll
-        for (int kt = 0; kt < KT; ++kt) {
-          const u32x4 av = *(const u32x4*)(krow + 32 * kt * KLD + 16 * kk);
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb) s[kt][nb] = mfma32<T>(av, qop[nb][kk], s[kt][nb]);
-        }
-      const bool need_mask = (t0 + BN > r.k_len) || (CAUSAL && t0 + BN - 1 > wave_qabs_lo);
-      u32x4 pop[KT][2][NB];
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        if (cap) {
-#pragma unroll
-          for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-              const float x = s[kt][nb][i] * cap_in;
-              const float e = fast_exp2(2.0f * LOG2E * x);
-              s[kt][nb][i] = cap_out * (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f));
-            }
-        }
-        if (need_mask) {
-          const int qabs = wq0 + nb * 32 + l32 + off;
-#pragma unroll
-          for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-              const int key = t0 + 32 * kt + 16 * (i >> 3) + 8 * hh + (i & 7);
-              const bool ok = key < r.k_len && (!CAUSAL || key <= qabs);
-              if (!ok) s[kt][nb][i] = -INFINITY;
-            }
-        }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kt][nb][i]);
-        mx = fmaxf(mx, shfl_xor_f(mx, 32));
-        const float cand = cap ? mx : mx * c_scale;
-        const bool need = cand > m_run[nb] + PF_RESCALE;
-        if (__any(need)) {
-          const float f = need ? fast_exp2(m_run[nb] - cand) : 1.0f;
-          if (need) m_run[nb] = cand;
-          l_run[nb] *= f;
-#pragma unroll
-          for (int db = 0; db < DB; ++db)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) o[db][nb][i] *= f;
-        }
-        const float mref = m_run[nb] == -INFINITY ? 0.0f : m_run[nb];
-        const float sc = cap ? 1.0f : c_scale;
-        float psum = 0.0f;
-#pragma unroll
-        for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const float p = fast_exp2(fmaf(s[kt][nb][i], sc, -mref));
-            s[kt][nb][i] = p;
-            psum += p;
-          }
-        l_run[nb] += psum;
-#pragma unroll
-        for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-          for (int c = 0; c < 2; ++c) {
-            u32x4 w;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) w[q] = pack2<T>(s[kt][nb][8 * c + 2 * q], s[kt][nb][8 * c + 2 * q + 1]);
-            pop[kt][c][nb] = w;
-          }
+  // ---- DMA addressing.  Instruction n of a tile covers column group n / 8,
+  // rows 8 (n % 8) .. +8; lane p fills LDS row 8 (n % 8) + p / 8, 16-byte
+  // slot p % 8, which holds chunk (p % 8) ^ ((row / 2) % 8) of that row (V:
+  // the unit pair 2 (p % 8) ^ 4 ((row / 2) % 2)).  K rows hold key
+  // sigma(row).  Offsets are relative to the first key of the row's 16-key
+  // group, whose address the per-group descriptor carries.  Wave w issues
+  // n = w, w + W, ...: with W in {4, 8} every one of them has n % 2 = w % 2,
+  // so one lane offset serves them all and the column group (n / 8 = W i / 8)
+  // is an immediate.
+  static_assert(W == 4 || W == 8, "wave count");
+  const bool paged = a.page_size != 0;
+  const int lp = shp.log2_page;
+  const int drow = 8 * (wave_u & 1) + (lane >> 3);   // row within its 16-key group
+  const int kdoff = 2 * (int)(sigma(drow) * a.k_stride[1]) + (((lane & 7) ^ ((drow >> 1) & 7)) * 16);
+  const int vdoff = 2 * (int)(drow * a.v_stride[1]) + (((2 * (lane & 7)) ^ (4 * ((drow >> 1) & 1))) * 8);
+  // Per-wave DMA share: W = 4 -> row blocks rb = w (rows 0..31) and w + 4
+  // (rows 32..63) of every column group; W = 8 -> row block w of every column
+  // group.  One descriptor serves all column groups of a row block.
+  const char* const khead = (const char*)a.k + 2 * (int64_t)kh * a.k_stride[2];
+  const char* const vhead = (const char*)a.v + 2 * (int64_t)kh * a.v_stride[2];
+  const uint32_t krow_b = (uint32_t)(2 * a.k_stride[1]), vrow_b = (uint32_t)(2 * a.v_stride[1]);
+  const uint32_t kpage_b = (uint32_t)(2 * a.k_stride[0]), vpage_b = (uint32_t)(2 * a.v_stride[0]);
+  const int32_t* const trow = paged ? a.block_table + b * a.bt_stride[0] : nullptr;
+  const int bt1 = (int)a.bt_stride[1];
+  const int pmask = (1 << lp) - 1;
+  // Descriptor of the 16-key group starting at key0: base = that key's row,
+  // size ends at the request's last key (0 bytes for groups past it).
+  auto group_rsrc = [&](const char* head, uint32_t row_b, uint32_t page_b, int key0, int row_bytes) {
+    const int nvalid = min(max(r.k_len - key0, 0), 16);
+    const char* g = head;
+    if (nvalid > 0) {
+      if (paged) {
+        const uint32_t blk = (uint32_t)load_invariant_i32(trow, (int64_t)(key0 >> lp) * bt1);
+        g = head + (uint64_t)blk * page_b + (uint32_t)(key0 & pmask) * row_b;
+      } else {
+        g = head + (uint64_t)(uint32_t)(r.k_base + key0) * row_b;
       }
-#pragma unroll
-      for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-          for (int db = 0; db < DB; ++db) {
-            const int dim = 32 * db + l32;
-            const int chunk = (4 * kt + 2 * c + hh) ^ ((dim >> 4) & 7);
-            const u32x4 av = *(const u32x4*)(vl + dim * VLD + 8 * chunk);
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) o[db][nb] = mfma32<T>(av, pop[kt][c][nb], o[db][nb]);
-          }
     }
-    if (j + 1 < n_tiles) store_tile(buf ^ 1);
-    __syncthreads();
-  }
-
-  // Epilogue: O = O^T / l, LSE = m * ln2 + ln(l).
+    // readfirstlane keeps the (uniform) size in an SGPR: a VGPR-held
+    // descriptor field would make the compiler wrap each load in a loop over
+    // distinct descriptors.
+    const int bytes = __builtin_amdgcn_readfirstlane(nvalid > 0 ? (nvalid - 1) * (int)row_b + row_bytes : 0);
+    return __builtin_amdgcn_make_buffer_rsrc((void*)g, (short)0, bytes, 0x00020000);
+  };
+  // K rows 32 half .. +32 of a tile.
+  auto dma_k = [&](int tile, int buf, int half) {
+    if (W == 8 && (wave_u >> 2) != half) return;
+    const int rb = W == 4 ? wave_u + 4 * half : wave_u;
+    const auto rsrc = group_rsrc(khead, krow_b, kpage_b, tile * PF_BN + 16 * (rb >> 1), 2 * DQ);
+    dma_columns<KG>(rsrc, kbuf0 + buf * KTILE + rb * 1024, kdoff);
+  };
+  auto dma_v = [&](int tile, int buf) {
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const float lt = l_run[nb] + shfl_xor_f(l_run[nb], 32);
-    const int row = wq0 + nb * 32 + l32;
-    if (row < r.q_len) {
-      const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-      const int64_t tq = (int64_t)r.q_begin + row;
-      uint16_t* op = (uint16_t*)a.out + tq * a.out_stride[0] + (int64_t)h * a.out_stride[1] + 4 * hh;
+    for (int half = 0; half < 2; ++half) {
+      if (W == 8 && (wave_u >> 2) != half) continue;
+      const int rb = W == 4 ? wave_u + 4 * half : wave_u;
+      const auto rsrc = group_rsrc(vhead, vrow_b, vpage_b, tile * PF_BN + 16 * (rb >> 1), 2 * DV);
+      dma_columns<VG>(rsrc, vbuf0 + buf * VTILE + rb * 1024, vdoff);
+    }
+  };
+
+  // ---- Operand read offsets (bytes within a tile buffer).
+  // K (A of S^T): LDS row 32 kt + l32, chunk 2 kk + hh -> column group
+  // kk / 4, slot (2 (kk % 4) + hh) ^ ((l32 / 2) % 8); kt and kk / 4 are
+  // immediates.
+  int krd[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) krd[s] = l32 * 128 + (((2 * s + hh) ^ ((l32 >> 1) & 7)) * 16);
+  // V^T (A of O^T) through ds_read_b64_tr_b16: in each 16-lane group g, lane
+  // i = a + 4 t' reads row 8 (g / 2) + t' (+ 32 kt + 16 c + 4 t) at dims
+  // 32 db + 16 (g % 2) + 4 a .. +4; the hardware hands lane 4 a + e dim
+  // 4 a + e of those four rows, i.e. four consecutive keys of one dim.
+  const int vg16 = lane >> 4, vi = lane & 15, va = vi & 3, vt = vi >> 2;
+  const int vrd = (8 * (vg16 >> 1) + vt) * 128 + (((4 * (vg16 & 1) + va) ^ (4 * ((vt >> 1) & 1))) * 8);
+
+  const float c_scale = a.softmax_scale * LOG2E;          // raw dot -> log2 units
+  const float cap_in = CAP ? 2.0f * LOG2E * a.softmax_scale / a.softcap : 0.0f;
+  const float cap_out = a.softcap * LOG2E;
+  // A sink logit seeds the running state (max = sink, sum = 1) of every row.
+  const float sink2 = a.sinks ? a.sinks[(int64_t)h * a.sink_stride] * LOG2E : -INFINITY;
+  float m_run = sink2;
+  float l_run = (a.sinks && hh == 0) ? 1.0f : 0.0f;
+  f32x16 o[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
+
+  const bool wave_rows = wq0 < r.q_len;
+  const int wave_qabs_lo = wq0 + off;
+  const int wave_qabs_hi = min(wq0 + 32, r.q_len) - 1 + off;
+  const int qabs = wq0 + l32 + off;
+  // The pipeline runs over 32-key stages: stage st is half st % 2 of tile
+  // st / 2 (keys 32 st .. +32).
+  const int n_stages = kv_end > 0 ? (kv_end + 31) / 32 : 0;
+  auto active = [&](int st) { return wave_rows && (!CAUSAL || st * 32 <= wave_qabs_hi); };
+  auto needs_mask = [&](int st) {
+    const int t0 = st * 32;
+    return (t0 + 32 > r.k_len) || (CAUSAL && t0 + 31 > wave_qabs_lo);
+  };
+
+  // S^T of one stage: s[i] = score of key 32 st + 16 (i >> 3) + 8 hh + (i & 7).
+  auto qk = [&](int st, f32x16& s) {
+    const char* kl = kbuf0 + ((st >> 1) & 1) * KTILE + (st & 1) * 32 * 128;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KST; ++kk) {
+      const u32x4 av = lds_read16(kl, krd[kk % 4] + (kk / 4) * PF_GROUP_BYTES);
+      s = mfma32<T>(av, qop[kk], s);
+    }
+  };
+  // Phase A: softcap, mask, row max and the lazy rescale of (m, l); returns
+  // O's factor, applied before the stage's P.V.  With commit false (a stage
+  // past this wave's causal range) the running state is left untouched.
+  auto phase_a = [&](auto mask_tag, int st, f32x16& s, bool commit) -> float {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    if constexpr (CAP) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float e = fast_exp2(cap_in * s[i]);
+        s[i] = cap_out * (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f));
+      }
+    }
+    if constexpr (MASK) {
+      // Key t0 + 16 (i >> 3) + 8 hh + (i & 7) is visible iff its offset
+      // 16 (i >> 3) + (i & 7) (an inline constant) <= lim.
+      const int t0 = st * 32;
+      int lim = r.k_len - 1 - t0;
+      if (CAUSAL) lim = min(lim, qabs - t0);
+      lim -= 8 * hh;
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (16 * (i >> 3) + (i & 7) > lim) s[i] = -INFINITY;
+    }
+    float mx = fmaxf(s[0], s[1]);
+#pragma unroll
+    for (int i = 2; i < 16; ++i) mx = fmaxf(mx, s[i]);
+    mx = max_hh(mx);
+    const float cand = CAP ? mx : mx * c_scale;
+    const bool need = commit && cand > m_run + PF_RESCALE;
+    const float f = need ? fast_exp2(m_run - cand) : 1.0f;
+    m_run = need ? cand : m_run;
+    l_run *= f;
+    return f;
+  };
+  // Phase B: probabilities (<= 2^8), row sums, packed B operand of O^T.
+  auto phase_b = [&](f32x16& s, u32x4 (&pop)[2]) {
+    const float mref = m_run == -INFINITY ? 0.0f : m_run;
+    const float sc = CAP ? 1.0f : c_scale;
+    float psum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float p = fast_exp2(fmaf(s[i], sc, -mref));
+      s[i] = p;
+      psum += p;
+    }
+    l_run += psum;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      u32x4 w;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) w[q] = pack2<T>(s[8 * c + 2 * q], s[8 * c + 2 * q + 1]);
+      pop[c] = w;
+    }
+  };
+  auto pv = [&](int st, const u32x4 (&pop)[2]) {
+    const char* vl = vbuf0 + ((st >> 1) & 1) * VTILE + (st & 1) * 32 * 128;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const int imm = 16 * c * 128 + (db >> 1) * PF_GROUP_BYTES + (db & 1) * 64;
+        const u32x2 lo = lds_read_tr(vl, vrd + imm);
+        const u32x2 hi = lds_read_tr(vl, vrd + imm + 4 * 128);
+        const u32x4 av = {lo[0], lo[1], hi[0], hi[1]};
+        o[db] = mfma32<T>(av, pop[c], o[db]);
+      }
+  };
+  auto rescale_o = [&](float f) {
+    if (__builtin_expect(__any(f != 1.0f), 0)) {
 #pragma unroll
       for (int db = 0; db < DB; ++db)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          uint2 w;
-          w.x = pack2<T>(o[db][nb][4 * g] * inv, o[db][nb][4 * g + 1] * inv);
-          w.y = pack2<T>(o[db][nb][4 * g + 2] * inv, o[db][nb][4 * g + 3] * inv);
-          *(uint2*)(op + 32 * db + 8 * g) = w;
-        }
-      if (hh == 0)
-        a.lse[(int64_t)h * a.lse_stride[0] + tq * a.lse_stride[1]] =
-            lt > 0.0f ? m_run[nb] * LN2 + logf(lt) : -INFINITY;
+        for (int i = 0; i < 16; ++i) o[db][i] *= f;
     }
+  };
+
+  // One pipeline stage: P(st) from S(st), S(st+1), O += V P(st), phase A of
+  // S(st+1); f carries O's pending rescale factor.
+  //
+  // LDS traffic, at the start of tile j (even stages): wait for this wave's
+  // DMAs and barrier, after which V(j), K(j) rows 32..63 and K(j+1) rows
+  // 0..31 are resident and every wave is done with V(j-1), K(j-1) rows
+  // 32..63 and K(j) rows 0..31; then V(j+1), K(j+1) rows 32..63 and K(j+2)
+  // rows 0..31 are issued into the freed buffer halves.
+  auto tile_start = [&](int st) {
+    if ((st & 1) == 0) {
+      const int j = st >> 1;
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      __syncthreads();
+      if (j + 1 < n_tiles) {
+        dma_v(j + 1, (j + 1) & 1);
+        dma_k(j + 1, (j + 1) & 1, 1);
+      }
+      if (j + 2 < n_tiles) dma_k(j + 2, j & 1, 0);
+    }
+  };
+  // Steady state: stage st and st+1 both active, st+1 unmasked.  One
+  // straight scheduling region: phase B(st) under the MFMAs of S(st+1),
+  // phase A(st+1) under the MFMAs of P.V(st).
+  auto step_hot = [&](int st, f32x16& sc, f32x16& sn, float& f) {
+    tile_start(st);
+    rescale_o(f);
+    u32x4 pop[2];
+    phase_b(sc, pop);
+    qk(st + 1, sn);
+    pv(st, pop);
+    f = phase_a(std::integral_constant<bool, false>(), st + 1, sn, true);
+  };
+  // Any stage: inactive waves only keep the barrier cadence; S(st+1) is
+  // computed even when stage st+1 lies past this wave's causal range (its K
+  // rows hold valid or stale finite data) and its phase A then commits
+  // nothing.
+  auto step_any = [&](int st, f32x16& sc, f32x16& sn, float& f) {
+    tile_start(st);
+    if (!active(st)) return;
+    const bool act_n = st + 1 < n_stages && active(st + 1);
+    rescale_o(f);
+    u32x4 pop[2];
+    phase_b(sc, pop);
+    qk(st + 1, sn);
+    pv(st, pop);
+    if (needs_mask(st + 1)) f = phase_a(std::integral_constant<bool, true>(), st + 1, sn, act_n);
+    else f = phase_a(std::integral_constant<bool, false>(), st + 1, sn, act_n);
+  };
+  auto hot = [&](int st) { return st < n_stages && active(st) && !needs_mask(st); };
+
+  if (n_stages > 0) {
+    // Prologue: tile 0 and K(1) rows 0..31 in LDS; S(0) and its phase A.
+    dma_k(0, 0, 0);
+    dma_k(0, 0, 1);
+    dma_v(0, 0);
+    if (n_tiles > 1) dma_k(1, 1, 0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    f32x16 sa, sb;
+    float f = 1.0f;
+    if (active(0)) {
+      qk(0, sa);
+      f = phase_a(std::integral_constant<bool, true>(), 0, sa, true);
+    }
+    int st = 0;
+    if (active(0))
+      for (; hot(st + 1) && hot(st + 2); st += 2) {
+        step_hot(st, sa, sb, f);
+        step_hot(st + 1, sb, sa, f);
+      }
+    for (; st < n_stages; ++st) {
+      if (st & 1) step_any(st, sb, sa, f);
+      else step_any(st, sa, sb, f);
+    }
+  }
+
+  // Epilogue: O = O^T / l, LSE = m * ln2 + ln(l).
+  const float lt = sum_hh(l_run);
+  const int row = wq0 + l32;
+  if (row < r.q_len) {
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    const int64_t tq = (int64_t)r.q_begin + row;
+    uint16_t* op = (uint16_t*)a.out + tq * a.out_stride[0] + (int64_t)h * a.out_stride[1] + 4 * hh;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        uint2 w;
+        w.x = pack2<T>(o[db][4 * g] * inv, o[db][4 * g + 1] * inv);
+        w.y = pack2<T>(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
+        *(uint2*)(op + 32 * db + 8 * g) = w;
+      }
+    if (hh == 0)
+      a.lse[(int64_t)h * a.lse_stride[0] + tq * a.lse_stride[1]] = lt > 0.0f ? m_run * LN2 + logf(lt) : -INFINITY;
   }
 }
 
-// Tile shape per head-dim pair: NB query blocks per wave, W waves per
-// workgroup, MINB workgroups per CU.  Two waves per SIMD either as two
-// 4-wave workgroups (when LDS holds two double-buffered tile pairs) or as
-// one 8-wave workgroup sharing its tiles.
+// Waves per workgroup and workgroups per CU per head-dim pair (LDS holds two
+// K and two V tiles per workgroup).
 template <int DQ, int DV> struct PrefillTile;
-template <> struct PrefillTile<64, 64> { static constexpr int NB = 1, W = 4, MINB = 2; };
-template <> struct PrefillTile<128, 128> { static constexpr int NB = 1, W = 4, MINB = 2; };
-template <> struct PrefillTile<192, 128> { static constexpr int NB = 1, W = 8, MINB = 1; };
-template <> struct PrefillTile<256, 256> { static constexpr int NB = 1, W = 4, MINB = 1; };
+template <> struct PrefillTile<64, 64> { static constexpr int W = 4, MINB = 2; };
+template <> struct PrefillTile<128, 128> { static constexpr int W = 4, MINB = 2; };
+template <> struct PrefillTile<192, 128> { static constexpr int W = 8, MINB = 1; };
+template <> struct PrefillTile<256, 256> { static constexpr int W = 4, MINB = 1; };
 
 template <int DQ, int DV>
 constexpr size_t lds_bytes() {
-  return 2 * (size_t)(64 * (DQ + 8) + DV * (64 + 8)) * sizeof(uint16_t);
+  return 2 * (size_t)(DQ / 64 + DV / 64) * PF_GROUP_BYTES;
 }
 
 using PrefillKernel = void (*)(fa_attn_args, PrefillShape);
@@ -486,31 +493,36 @@ struct PrefillChoice {
   size_t lds;
 };
 
-template <typename T, int DQ, int DV>
-PrefillChoice pick(bool causal) {
+template <typename T, int DQ, int DV, bool CAUSAL>
+PrefillChoice pick_cap(bool cap) {
   using S = PrefillTile<DQ, DV>;
   PrefillChoice c;
-  c.kern = causal ? prefill_kernel<T, DQ, DV, S::NB, 2, S::W, S::MINB, true>
-                  : prefill_kernel<T, DQ, DV, S::NB, 2, S::W, S::MINB, false>;
-  c.bm = 32 * S::NB * S::W;
+  c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::MINB, CAUSAL, true>
+               : prefill_kernel<T, DQ, DV, S::W, S::MINB, CAUSAL, false>;
+  c.bm = 32 * S::W;
   c.threads = 64 * S::W;
   c.lds = lds_bytes<DQ, DV>();
   return c;
 }
 
+template <typename T, int DQ, int DV>
+PrefillChoice pick(bool causal, bool cap) {
+  return causal ? pick_cap<T, DQ, DV, true>(cap) : pick_cap<T, DQ, DV, false>(cap);
+}
+
 template <typename T>
-PrefillChoice pick_dims(int64_t dq, int64_t dv, bool causal) {
-  if (dq == 64 && dv == 64) return pick<T, 64, 64>(causal);
-  if (dq == 128 && dv == 128) return pick<T, 128, 128>(causal);
-  if (dq == 192 && dv == 128) return pick<T, 192, 128>(causal);
-  if (dq == 256 && dv == 256) return pick<T, 256, 256>(causal);
+PrefillChoice pick_dims(int64_t dq, int64_t dv, bool causal, bool cap) {
+  if (dq == 64 && dv == 64) return pick<T, 64, 64>(causal, cap);
+  if (dq == 128 && dv == 128) return pick<T, 128, 128>(causal, cap);
+  if (dq == 192 && dv == 128) return pick<T, 192, 128>(causal, cap);
+  if (dq == 256 && dv == 256) return pick<T, 256, 256>(causal, cap);
   return PrefillChoice{nullptr, 0, 0, 0};
 }
 
 PrefillChoice select_prefill(const fa_attn_args& a) {
-  const bool causal = a.causal != 0;
-  return a.q_dtype == FA_BF16 ? pick_dims<BF16T>(a.head_dim_qk, a.head_dim_v, causal)
-                              : pick_dims<F16T>(a.head_dim_qk, a.head_dim_v, causal);
+  const bool causal = a.causal != 0, cap = a.softcap > 0.0f;
+  return a.q_dtype == FA_BF16 ? pick_dims<BF16T>(a.head_dim_qk, a.head_dim_v, causal, cap)
+                              : pick_dims<F16T>(a.head_dim_qk, a.head_dim_v, causal, cap);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -535,6 +547,8 @@ bool prefill_ok(const fa_attn_args& a) {
   if (16 * a.k_stride[1] * 2 >= 0x7fffffffll || 16 * a.v_stride[1] * 2 >= 0x7fffffffll) return false;
   if (a.page_size) {
     if (a.page_size < 16 || (a.page_size & (a.page_size - 1))) return false;
+    // Page strides are 32-bit byte counts in the group descriptors.
+    if (2 * a.k_stride[0] >= (1ll << 32) || 2 * a.v_stride[0] >= (1ll << 32)) return false;
   }
   return true;
 }
