@@ -125,14 +125,15 @@ struct PrefillShape {
   int log2_page;   // paged K/V: page size = 1 << log2_page
 };
 
-template <typename T, int DQ, int DV, int W, int MINB, bool CAUSAL, bool CAP>
+template <typename T, int DQ, int DV, int W, int NB, int MINB, bool CAUSAL, bool CAP>
 __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_args a, const PrefillShape shp) {
-  constexpr int BM = 32 * W;
+  constexpr int BM = 32 * NB * W;              // query rows per workgroup
   constexpr int KST = DQ / 16;                 // k-steps of the QK^T MFMA
   constexpr int DB = DV / 32;                  // 32-dim blocks of O^T
   constexpr int KG = DQ / 64, VG = DV / 64;    // 64-dim column groups
   constexpr int KTILE = KG * PF_GROUP_BYTES, VTILE = VG * PF_GROUP_BYTES;
   static_assert(DQ % 64 == 0 && DV % 64 == 0, "head dims are multiples of 64");
+  static_assert(W == 2 || W == 4 || W == 8, "wave count");
 
   extern __shared__ __attribute__((aligned(16))) char smem[];
   char* const kbuf0 = smem;
@@ -163,11 +164,13 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   if (CAUSAL) kv_end = min(kv_end, min(q0 + BM, r.q_len) - 1 + off + 1);
   const int n_tiles = kv_end > 0 ? (kv_end + PF_BN - 1) / PF_BN : 0;
 
-  // Q^T operand for the whole kernel: lane holds Q[row][16kk + 8hh .. +8].
-  const int wq0 = q0 + wave_u * 32;
-  u32x4 qop[KST];
-  {
-    const int row = wq0 + l32;
+  // Q^T operands for the whole kernel: block nb, lane holds
+  // Q[wq0 + 32 nb + l32][16 kk + 8 hh .. +8].
+  const int wq0 = q0 + wave_u * 32 * NB;
+  u32x4 qop[NB][KST];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int row = wq0 + 32 * nb + l32;
     const bool ok = row < r.q_len;
     const uint16_t* qp = (const uint16_t*)a.q + ((int64_t)r.q_begin + row) * a.q_stride[0] +
                          (int64_t)h * a.q_stride[1] + 8 * hh;
@@ -175,7 +178,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     for (int kk = 0; kk < KST; ++kk) {
       u32x4 v = {0u, 0u, 0u, 0u};
       if (ok) v = *(const u32x4*)(qp + 16 * kk);
-      qop[kk] = v;
+      qop[nb][kk] = v;
     }
   }
 
@@ -187,24 +190,20 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   }
   __syncthreads();
 
-  // ---- DMA addressing.  Instruction n of a tile covers column group n / 8,
-  // rows 8 (n % 8) .. +8; lane p fills LDS row 8 (n % 8) + p / 8, 16-byte
-  // slot p % 8, which holds chunk (p % 8) ^ ((row / 2) % 8) of that row (V:
-  // the unit pair 2 (p % 8) ^ 4 ((row / 2) % 2)).  K rows hold key
-  // sigma(row).  Offsets are relative to the first key of the row's 16-key
-  // group, whose address the per-group descriptor carries.  Wave w issues
-  // n = w, w + W, ...: with W in {4, 8} every one of them has n % 2 = w % 2,
-  // so one lane offset serves them all and the column group (n / 8 = W i / 8)
-  // is an immediate.
-  static_assert(W == 4 || W == 8, "wave count");
+  // ---- DMA addressing.  A tile is 8 row blocks (8 rows each) per column
+  // group; one instruction moves one row block of one column group.  Lane p
+  // fills LDS row 8 rb + p / 8, 16-byte slot p % 8, which holds chunk
+  // (p % 8) ^ ((row / 2) % 8) of that row (V: the unit pair
+  // 2 (p % 8) ^ 4 ((row / 2) % 2)).  K rows hold key sigma(row).  Offsets are
+  // relative to the first key of the row's 16-key group, whose address the
+  // per-group descriptor carries.  Wave w owns row blocks rb = w + W i: all
+  // have rb % 2 = w % 2, so one lane offset serves them all and the column
+  // group is an immediate.
   const bool paged = a.page_size != 0;
   const int lp = shp.log2_page;
   const int drow = 8 * (wave_u & 1) + (lane >> 3);   // row within its 16-key group
   const int kdoff = 2 * (int)(sigma(drow) * a.k_stride[1]) + (((lane & 7) ^ ((drow >> 1) & 7)) * 16);
   const int vdoff = 2 * (int)(drow * a.v_stride[1]) + (((2 * (lane & 7)) ^ (4 * ((drow >> 1) & 1))) * 8);
-  // Per-wave DMA share: W = 4 -> row blocks rb = w (rows 0..31) and w + 4
-  // (rows 32..63) of every column group; W = 8 -> row block w of every column
-  // group.  One descriptor serves all column groups of a row block.
   const char* const khead = (const char*)a.k + 2 * (int64_t)kh * a.k_stride[2];
   const char* const vhead = (const char*)a.v + 2 * (int64_t)kh * a.v_stride[2];
   const uint32_t krow_b = (uint32_t)(2 * a.k_stride[1]), vrow_b = (uint32_t)(2 * a.v_stride[1]);
@@ -231,33 +230,34 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     const int bytes = __builtin_amdgcn_readfirstlane(nvalid > 0 ? (nvalid - 1) * (int)row_b + row_bytes : 0);
     return __builtin_amdgcn_make_buffer_rsrc((void*)g, (short)0, bytes, 0x00020000);
   };
-  // K rows 32 half .. +32 of a tile.
+  // K rows 32 half .. +32 of a tile (row blocks 4 half .. +4).
   auto dma_k = [&](int tile, int buf, int half) {
-    if (W == 8 && (wave_u >> 2) != half) return;
-    const int rb = W == 4 ? wave_u + 4 * half : wave_u;
-    const auto rsrc = group_rsrc(khead, krow_b, kpage_b, tile * PF_BN + 16 * (rb >> 1), 2 * DQ);
-    dma_columns<KG>(rsrc, kbuf0 + buf * KTILE + rb * 1024, kdoff);
+#pragma unroll
+    for (int i = 0; i < 8 / W; ++i) {
+      const int rb = wave_u + W * i;
+      if ((rb >> 2) != half) continue;
+      const auto rsrc = group_rsrc(khead, krow_b, kpage_b, tile * PF_BN + 16 * (rb >> 1), 2 * DQ);
+      dma_columns<KG>(rsrc, kbuf0 + buf * KTILE + rb * 1024, kdoff);
+    }
   };
   auto dma_v = [&](int tile, int buf) {
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      if (W == 8 && (wave_u >> 2) != half) continue;
-      const int rb = W == 4 ? wave_u + 4 * half : wave_u;
+    for (int i = 0; i < 8 / W; ++i) {
+      const int rb = wave_u + W * i;
       const auto rsrc = group_rsrc(vhead, vrow_b, vpage_b, tile * PF_BN + 16 * (rb >> 1), 2 * DV);
       dma_columns<VG>(rsrc, vbuf0 + buf * VTILE + rb * 1024, vdoff);
     }
   };
 
   // ---- Operand read offsets (bytes within a tile buffer).
-  // K (A of S^T): LDS row 32 kt + l32, chunk 2 kk + hh -> column group
-  // kk / 4, slot (2 (kk % 4) + hh) ^ ((l32 / 2) % 8); kt and kk / 4 are
-  // immediates.
+  // K (A of S^T): LDS row 32 (st % 2) + l32, chunk 2 kk + hh -> column group
+  // kk / 4, slot (2 (kk % 4) + hh) ^ ((l32 / 2) % 8); kk / 4 is an immediate.
   int krd[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) krd[s] = l32 * 128 + (((2 * s + hh) ^ ((l32 >> 1) & 7)) * 16);
   // V^T (A of O^T) through ds_read_b64_tr_b16: in each 16-lane group g, lane
-  // i = a + 4 t' reads row 8 (g / 2) + t' (+ 32 kt + 16 c + 4 t) at dims
-  // 32 db + 16 (g % 2) + 4 a .. +4; the hardware hands lane 4 a + e dim
+  // i = a + 4 t' reads row 8 (g / 2) + t' (+ 32 (st % 2) + 16 c + 4 t) at
+  // dims 32 db + 16 (g % 2) + 4 a .. +4; the hardware hands lane 4 a + e dim
   // 4 a + e of those four rows, i.e. four consecutive keys of one dim.
   const int vg16 = lane >> 4, vi = lane & 15, va = vi & 3, vt = vi >> 2;
   const int vrd = (8 * (vg16 >> 1) + vt) * 128 + (((4 * (vg16 & 1) + va) ^ (4 * ((vt >> 1) & 1))) * 8);
@@ -267,18 +267,21 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   const float cap_out = a.softcap * LOG2E;
   // A sink logit seeds the running state (max = sink, sum = 1) of every row.
   const float sink2 = a.sinks ? a.sinks[(int64_t)h * a.sink_stride] * LOG2E : -INFINITY;
-  float m_run = sink2;
-  float l_run = (a.sinks && hh == 0) ? 1.0f : 0.0f;
-  f32x16 o[DB];
+  float m_run[NB], l_run[NB];
+  f32x16 o[NB][DB];
 #pragma unroll
-  for (int db = 0; db < DB; ++db)
+  for (int nb = 0; nb < NB; ++nb) {
+    m_run[nb] = sink2;
+    l_run[nb] = (a.sinks && hh == 0) ? 1.0f : 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[nb][db][i] = 0.0f;
+  }
 
   const bool wave_rows = wq0 < r.q_len;
   const int wave_qabs_lo = wq0 + off;
-  const int wave_qabs_hi = min(wq0 + 32, r.q_len) - 1 + off;
-  const int qabs = wq0 + l32 + off;
+  const int wave_qabs_hi = min(wq0 + 32 * NB, r.q_len) - 1 + off;
   // The pipeline runs over 32-key stages: stage st is half st % 2 of tile
   // st / 2 (keys 32 st .. +32).
   const int n_stages = kv_end > 0 ? (kv_end + 31) / 32 : 0;
@@ -288,72 +291,80 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     return (t0 + 32 > r.k_len) || (CAUSAL && t0 + 31 > wave_qabs_lo);
   };
 
-  // S^T of one stage: s[i] = score of key 32 st + 16 (i >> 3) + 8 hh + (i & 7).
-  auto qk = [&](int st, f32x16& s) {
+  // S^T of one stage: s[nb][i] = score of key 32 st + 16 (i >> 3) + 8 hh + (i & 7).
+  auto qk = [&](int st, f32x16 (&s)[NB]) {
     const char* kl = kbuf0 + ((st >> 1) & 1) * KTILE + (st & 1) * 32 * 128;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[nb][i] = 0.0f;
 #pragma unroll
     for (int kk = 0; kk < KST; ++kk) {
       const u32x4 av = lds_read16(kl, krd[kk % 4] + (kk / 4) * PF_GROUP_BYTES);
-      s = mfma32<T>(av, qop[kk], s);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) s[nb] = mfma32<T>(av, qop[nb][kk], s[nb]);
     }
   };
-  // Phase A: softcap, mask, row max and the lazy rescale of (m, l); returns
-  // O's factor, applied before the stage's P.V.  With commit false (a stage
+  // Phase A: softcap, mask, row max and the lazy rescale of (m, l); fills
+  // O's factors, applied before the stage's P.V.  With commit false (a stage
   // past this wave's causal range) the running state is left untouched.
-  auto phase_a = [&](auto mask_tag, int st, f32x16& s, bool commit) -> float {
+  auto phase_a = [&](auto mask_tag, int st, f32x16 (&s)[NB], bool commit, float (&f)[NB]) {
     constexpr bool MASK = decltype(mask_tag)::value;
-    if constexpr (CAP) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float e = fast_exp2(cap_in * s[i]);
-        s[i] = cap_out * (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f));
+    for (int nb = 0; nb < NB; ++nb) {
+      if constexpr (CAP) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float e = fast_exp2(cap_in * s[nb][i]);
+          s[nb][i] = cap_out * (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f));
+        }
       }
-    }
-    if constexpr (MASK) {
-      // Key t0 + 16 (i >> 3) + 8 hh + (i & 7) is visible iff its offset
-      // 16 (i >> 3) + (i & 7) (an inline constant) <= lim.
-      const int t0 = st * 32;
-      int lim = r.k_len - 1 - t0;
-      if (CAUSAL) lim = min(lim, qabs - t0);
-      lim -= 8 * hh;
+      if constexpr (MASK) {
+        // Key t0 + 16 (i >> 3) + 8 hh + (i & 7) is visible iff its offset
+        // 16 (i >> 3) + (i & 7) (an inline constant) <= lim.
+        const int t0 = st * 32;
+        int lim = r.k_len - 1 - t0;
+        if (CAUSAL) lim = min(lim, wq0 + 32 * nb + l32 + off - t0);
+        lim -= 8 * hh;
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        if (16 * (i >> 3) + (i & 7) > lim) s[i] = -INFINITY;
-    }
-    float mx = fmaxf(s[0], s[1]);
+        for (int i = 0; i < 16; ++i)
+          if (16 * (i >> 3) + (i & 7) > lim) s[nb][i] = -INFINITY;
+      }
+      float mx = fmaxf(s[nb][0], s[nb][1]);
 #pragma unroll
-    for (int i = 2; i < 16; ++i) mx = fmaxf(mx, s[i]);
-    mx = max_hh(mx);
-    const float cand = CAP ? mx : mx * c_scale;
-    const bool need = commit && cand > m_run + PF_RESCALE;
-    const float f = need ? fast_exp2(m_run - cand) : 1.0f;
-    m_run = need ? cand : m_run;
-    l_run *= f;
-    return f;
+      for (int i = 2; i < 16; ++i) mx = fmaxf(mx, s[nb][i]);
+      mx = max_hh(mx);
+      const float cand = CAP ? mx : mx * c_scale;
+      const bool need = commit && cand > m_run[nb] + PF_RESCALE;
+      f[nb] = need ? fast_exp2(m_run[nb] - cand) : 1.0f;
+      m_run[nb] = need ? cand : m_run[nb];
+      l_run[nb] *= f[nb];
+    }
   };
   // Phase B: probabilities (<= 2^8), row sums, packed B operand of O^T.
-  auto phase_b = [&](f32x16& s, u32x4 (&pop)[2]) {
-    const float mref = m_run == -INFINITY ? 0.0f : m_run;
+  auto phase_b = [&](f32x16 (&s)[NB], u32x4 (&pop)[NB][2]) {
     const float sc = CAP ? 1.0f : c_scale;
-    float psum = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float p = fast_exp2(fmaf(s[i], sc, -mref));
-      s[i] = p;
-      psum += p;
-    }
-    l_run += psum;
+    for (int nb = 0; nb < NB; ++nb) {
+      const float mref = m_run[nb] == -INFINITY ? 0.0f : m_run[nb];
+      float psum = 0.0f;
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      u32x4 w;
+      for (int i = 0; i < 16; ++i) {
+        const float p = fast_exp2(fmaf(s[nb][i], sc, -mref));
+        s[nb][i] = p;
+        psum += p;
+      }
+      l_run[nb] += psum;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) w[q] = pack2<T>(s[8 * c + 2 * q], s[8 * c + 2 * q + 1]);
-      pop[c] = w;
+      for (int c = 0; c < 2; ++c) {
+        u32x4 w;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) w[q] = pack2<T>(s[nb][8 * c + 2 * q], s[nb][8 * c + 2 * q + 1]);
+        pop[nb][c] = w;
+      }
     }
   };
-  auto pv = [&](int st, const u32x4 (&pop)[2]) {
+  auto pv = [&](int st, const u32x4 (&pop)[NB][2]) {
     const char* vl = vbuf0 + ((st >> 1) & 1) * VTILE + (st & 1) * 32 * 128;
 #pragma unroll
     for (int c = 0; c < 2; ++c)
@@ -363,20 +374,24 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
         const u32x2 lo = lds_read_tr(vl, vrd + imm);
         const u32x2 hi = lds_read_tr(vl, vrd + imm + 4 * 128);
         const u32x4 av = {lo[0], lo[1], hi[0], hi[1]};
-        o[db] = mfma32<T>(av, pop[c], o[db]);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) o[nb][db] = mfma32<T>(av, pop[nb][c], o[nb][db]);
       }
   };
-  auto rescale_o = [&](float f) {
-    if (__builtin_expect(__any(f != 1.0f), 0)) {
+  auto rescale_o = [&](const float (&f)[NB]) {
 #pragma unroll
-      for (int db = 0; db < DB; ++db)
+    for (int nb = 0; nb < NB; ++nb) {
+      if (__builtin_expect(__any(f[nb] != 1.0f), 0)) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) o[db][i] *= f;
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) o[nb][db][i] *= f[nb];
+      }
     }
   };
 
   // One pipeline stage: P(st) from S(st), S(st+1), O += V P(st), phase A of
-  // S(st+1); f carries O's pending rescale factor.
+  // S(st+1); f carries O's pending rescale factors.
   //
   // LDS traffic, at the start of tile j (even stages): wait for this wave's
   // DMAs and barrier, after which V(j), K(j) rows 32..63 and K(j+1) rows
@@ -398,30 +413,30 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // Steady state: stage st and st+1 both active, st+1 unmasked.  One
   // straight scheduling region: phase B(st) under the MFMAs of S(st+1),
   // phase A(st+1) under the MFMAs of P.V(st).
-  auto step_hot = [&](int st, f32x16& sc, f32x16& sn, float& f) {
+  auto step_hot = [&](int st, f32x16 (&sc)[NB], f32x16 (&sn)[NB], float (&f)[NB]) {
     tile_start(st);
     rescale_o(f);
-    u32x4 pop[2];
+    u32x4 pop[NB][2];
     phase_b(sc, pop);
     qk(st + 1, sn);
     pv(st, pop);
-    f = phase_a(std::integral_constant<bool, false>(), st + 1, sn, true);
+    phase_a(std::integral_constant<bool, false>(), st + 1, sn, true, f);
   };
   // Any stage: inactive waves only keep the barrier cadence; S(st+1) is
   // computed even when stage st+1 lies past this wave's causal range (its K
   // rows hold valid or stale finite data) and its phase A then commits
   // nothing.
-  auto step_any = [&](int st, f32x16& sc, f32x16& sn, float& f) {
+  auto step_any = [&](int st, f32x16 (&sc)[NB], f32x16 (&sn)[NB], float (&f)[NB]) {
     tile_start(st);
     if (!active(st)) return;
     const bool act_n = st + 1 < n_stages && active(st + 1);
     rescale_o(f);
-    u32x4 pop[2];
+    u32x4 pop[NB][2];
     phase_b(sc, pop);
     qk(st + 1, sn);
     pv(st, pop);
-    if (needs_mask(st + 1)) f = phase_a(std::integral_constant<bool, true>(), st + 1, sn, act_n);
-    else f = phase_a(std::integral_constant<bool, false>(), st + 1, sn, act_n);
+    if (needs_mask(st + 1)) phase_a(std::integral_constant<bool, true>(), st + 1, sn, act_n, f);
+    else phase_a(std::integral_constant<bool, false>(), st + 1, sn, act_n, f);
   };
   auto hot = [&](int st) { return st < n_stages && active(st) && !needs_mask(st); };
 
@@ -433,11 +448,13 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     if (n_tiles > 1) dma_k(1, 1, 0);
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
-    f32x16 sa, sb;
-    float f = 1.0f;
+    f32x16 sa[NB], sb[NB];
+    float f[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) f[nb] = 1.0f;
     if (active(0)) {
       qk(0, sa);
-      f = phase_a(std::integral_constant<bool, true>(), 0, sa, true);
+      phase_a(std::integral_constant<bool, true>(), 0, sa, true, f);
     }
     int st = 0;
     if (active(0))
@@ -452,33 +469,41 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   }
 
   // Epilogue: O = O^T / l, LSE = m * ln2 + ln(l).
-  const float lt = sum_hh(l_run);
-  const int row = wq0 + l32;
-  if (row < r.q_len) {
-    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-    const int64_t tq = (int64_t)r.q_begin + row;
-    uint16_t* op = (uint16_t*)a.out + tq * a.out_stride[0] + (int64_t)h * a.out_stride[1] + 4 * hh;
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+  for (int nb = 0; nb < NB; ++nb) {
+    const float lt = sum_hh(l_run[nb]);
+    const int row = wq0 + 32 * nb + l32;
+    if (row < r.q_len) {
+      const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+      const int64_t tq = (int64_t)r.q_begin + row;
+      uint16_t* op = (uint16_t*)a.out + tq * a.out_stride[0] + (int64_t)h * a.out_stride[1] + 4 * hh;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        uint2 w;
-        w.x = pack2<T>(o[db][4 * g] * inv, o[db][4 * g + 1] * inv);
-        w.y = pack2<T>(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
-        *(uint2*)(op + 32 * db + 8 * g) = w;
-      }
-    if (hh == 0)
-      a.lse[(int64_t)h * a.lse_stride[0] + tq * a.lse_stride[1]] = lt > 0.0f ? m_run * LN2 + logf(lt) : -INFINITY;
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          uint2 w;
+          w.x = pack2<T>(o[nb][db][4 * g] * inv, o[nb][db][4 * g + 1] * inv);
+          w.y = pack2<T>(o[nb][db][4 * g + 2] * inv, o[nb][db][4 * g + 3] * inv);
+          *(uint2*)(op + 32 * db + 8 * g) = w;
+        }
+      if (hh == 0)
+        a.lse[(int64_t)h * a.lse_stride[0] + tq * a.lse_stride[1]] = lt > 0.0f ? m_run[nb] * LN2 + logf(lt) : -INFINITY;
+    }
   }
 }
 
-// Waves per workgroup and workgroups per CU per head-dim pair (LDS holds two
-// K and two V tiles per workgroup).
+// Waves per workgroup, 32-row query blocks per wave and workgroups per CU
+// per head-dim pair (LDS holds two K and two V tiles per workgroup).
+#ifndef FA_PF128_W
+#define FA_PF128_W 4
+#define FA_PF128_NB 1
+#define FA_PF128_MINB 2
+#endif
 template <int DQ, int DV> struct PrefillTile;
-template <> struct PrefillTile<64, 64> { static constexpr int W = 4, MINB = 2; };
-template <> struct PrefillTile<128, 128> { static constexpr int W = 4, MINB = 2; };
-template <> struct PrefillTile<192, 128> { static constexpr int W = 8, MINB = 1; };
-template <> struct PrefillTile<256, 256> { static constexpr int W = 4, MINB = 1; };
+template <> struct PrefillTile<64, 64> { static constexpr int W = 4, NB = 1, MINB = 2; };
+template <> struct PrefillTile<128, 128> { static constexpr int W = FA_PF128_W, NB = FA_PF128_NB, MINB = FA_PF128_MINB; };
+template <> struct PrefillTile<192, 128> { static constexpr int W = 4, NB = 1, MINB = 1; };
+template <> struct PrefillTile<256, 256> { static constexpr int W = 4, NB = 1, MINB = 1; };
 
 template <int DQ, int DV>
 constexpr size_t lds_bytes() {
@@ -497,9 +522,9 @@ template <typename T, int DQ, int DV, bool CAUSAL>
 PrefillChoice pick_cap(bool cap) {
   using S = PrefillTile<DQ, DV>;
   PrefillChoice c;
-  c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::MINB, CAUSAL, true>
-               : prefill_kernel<T, DQ, DV, S::W, S::MINB, CAUSAL, false>;
-  c.bm = 32 * S::W;
+  c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, true>
+               : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false>;
+  c.bm = 32 * S::NB * S::W;
   c.threads = 64 * S::W;
   c.lds = lds_bytes<DQ, DV>();
   return c;
