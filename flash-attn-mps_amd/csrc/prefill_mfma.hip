@@ -15,10 +15,12 @@
 //   contiguous KiB per instruction): no registers, no VALU.  Every 16-key
 //   group gets a scalar buffer descriptor bounded at the request's last key,
 //   so rows past the end read as zero; lane offsets are loop-invariant.
-// * LDS layout, K and V alike: 64-dim column groups of 64 rows x 128 bytes,
-//   the eight 16-byte chunks of a row XOR-swizzled by (row / 2) % 8 (K), the
-//   sixteen 8-byte units by 4 * ((row / 2) % 2) (V).  Every operand read is
-//   bank-conflict free and addressed as a lane register plus an immediate.
+// * LDS layout.  K: 64-dim column groups of 64 rows x 128 bytes, the eight
+//   16-byte chunks of a row XOR-swizzled by (row / 2) % 8.  V: 32-dim blocks
+//   of 64 rows x 64 bytes, unswizzled: the eight rows {0..3, 8..11} (+4k)
+//   that one transpose read touches then cover the banks evenly.  Every
+//   operand read is bank-conflict free and addressed as a lane register plus
+//   an immediate.
 // * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16 (A =
 //   K rows from LDS, B = Q^T held in registers for the whole kernel).  A lane
 //   holds 32 keys of ONE query column, so the row max / sum are in-lane plus
@@ -56,7 +58,8 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 constexpr float PF_RESCALE = 8.0f;        // log2 headroom before the running max moves
 constexpr int PF_BN = 64;                 // keys per tile
-constexpr int PF_GROUP_BYTES = 64 * 128;  // one 64-dim column group of a tile
+constexpr int PF_GROUP_BYTES = 64 * 128;  // one 64-dim column group of a K tile
+constexpr int PF_VBLOCK_BYTES = 64 * 64;  // one 32-dim block of a V tile
 
 template <typename T> FA_DEV f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c);
 template <> FA_DEV f32x16 mfma32<BF16T>(u32x4 a, u32x4 b, f32x16 c) {
@@ -115,6 +118,15 @@ FA_DEV void dma_columns(__amdgpu_buffer_rsrc_t rsrc, char* lds, int voffset) {
   }
 }
 
+// One 16-key group (16 rows x 64 bytes) of each of N 32-dim blocks.
+template <int N, int I = 0>
+FA_DEV void dma_blocks(__amdgpu_buffer_rsrc_t rsrc, char* lds, int voffset) {
+  if constexpr (I < N) {
+    dma16<64 * I>(rsrc, lds + I * PF_VBLOCK_BYTES, voffset);
+    dma_blocks<N, I + 1>(rsrc, lds, voffset);
+  }
+}
+
 FA_DEV u32x4 lds_read16(const char* base, int off) { return *(const u32x4*)(base + off); }
 FA_DEV u32x2 lds_read_tr(const char* base, int off) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + off)));
@@ -130,7 +142,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   constexpr int BM = 32 * NB * W;              // query rows per workgroup
   constexpr int KST = DQ / 16;                 // k-steps of the QK^T MFMA
   constexpr int DB = DV / 32;                  // 32-dim blocks of O^T
-  constexpr int KG = DQ / 64, VG = DV / 64;    // 64-dim column groups
+  constexpr int KG = DQ / 64, VG = DV / 64;    // 64-dim column groups (K), pairs of 32-dim blocks (V)
   constexpr int KTILE = KG * PF_GROUP_BYTES, VTILE = VG * PF_GROUP_BYTES;
   static_assert(DQ % 64 == 0 && DV % 64 == 0, "head dims are multiples of 64");
   static_assert(W == 2 || W == 4 || W == 8, "wave count");
@@ -193,17 +205,19 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // ---- DMA addressing.  A tile is 8 row blocks (8 rows each) per column
   // group; one instruction moves one row block of one column group.  Lane p
   // fills LDS row 8 rb + p / 8, 16-byte slot p % 8, which holds chunk
-  // (p % 8) ^ ((row / 2) % 8) of that row (V: the unit pair
-  // 2 (p % 8) ^ 4 ((row / 2) % 2)).  K rows hold key sigma(row).  Offsets are
-  // relative to the first key of the row's 16-key group, whose address the
-  // per-group descriptor carries.  Wave w owns row blocks rb = w + W i: all
-  // have rb % 2 = w % 2, so one lane offset serves them all and the column
-  // group is an immediate.
+  // (p % 8) ^ ((row / 2) % 8) of that row; K rows hold key sigma(row).
+  // Offsets are relative to the first key of the row's 16-key group, whose
+  // address the per-group descriptor carries.  Wave w owns K row blocks
+  // rb = w + W i: all have rb % 2 = w % 2, so one lane offset serves them all
+  // and the column group is an immediate.  V: one instruction moves one
+  // 16-key group of one 32-dim block (16 rows x 64 bytes, lane p -> row
+  // p / 4, chunk p % 4); wave w owns the groups w + W i, the block is an
+  // immediate.
   const bool paged = a.page_size != 0;
   const int lp = shp.log2_page;
   const int drow = 8 * (wave_u & 1) + (lane >> 3);   // row within its 16-key group
   const int kdoff = 2 * (int)(sigma(drow) * a.k_stride[1]) + (((lane & 7) ^ ((drow >> 1) & 7)) * 16);
-  const int vdoff = 2 * (int)(drow * a.v_stride[1]) + (((2 * (lane & 7)) ^ (4 * ((drow >> 1) & 1))) * 8);
+  const int vdoff = 2 * (int)((lane >> 2) * a.v_stride[1]) + (lane & 3) * 16;
   const char* const khead = (const char*)a.k + 2 * (int64_t)kh * a.k_stride[2];
   const char* const vhead = (const char*)a.v + 2 * (int64_t)kh * a.v_stride[2];
   const uint32_t krow_b = (uint32_t)(2 * a.k_stride[1]), vrow_b = (uint32_t)(2 * a.v_stride[1]);
@@ -242,10 +256,11 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   };
   auto dma_v = [&](int tile, int buf) {
 #pragma unroll
-    for (int i = 0; i < 8 / W; ++i) {
-      const int rb = wave_u + W * i;
-      const auto rsrc = group_rsrc(vhead, vrow_b, vpage_b, tile * PF_BN + 16 * (rb >> 1), 2 * DV);
-      dma_columns<VG>(rsrc, vbuf0 + buf * VTILE + rb * 1024, vdoff);
+    for (int i = 0; i < (4 + W - 1) / W; ++i) {
+      const int gi = wave_u + W * i;
+      if (gi >= 4) continue;
+      const auto rsrc = group_rsrc(vhead, vrow_b, vpage_b, tile * PF_BN + 16 * gi, 2 * DV);
+      dma_blocks<2 * VG>(rsrc, vbuf0 + buf * VTILE + gi * 1024, vdoff);
     }
   };
 
@@ -256,11 +271,11 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
 #pragma unroll
   for (int s = 0; s < 4; ++s) krd[s] = l32 * 128 + (((2 * s + hh) ^ ((l32 >> 1) & 7)) * 16);
   // V^T (A of O^T) through ds_read_b64_tr_b16: in each 16-lane group g, lane
-  // i = a + 4 t' reads row 8 (g / 2) + t' (+ 32 (st % 2) + 16 c + 4 t) at
-  // dims 32 db + 16 (g % 2) + 4 a .. +4; the hardware hands lane 4 a + e dim
-  // 4 a + e of those four rows, i.e. four consecutive keys of one dim.
+  // i = a + 4 t' reads row 8 (g / 2) + t' (+ 32 (st % 2) + 16 c + 4 t) of
+  // block db at dims 16 (g % 2) + 4 a .. +4; the hardware hands lane 4 a + e
+  // dim 4 a + e of those four rows, i.e. four consecutive keys of one dim.
   const int vg16 = lane >> 4, vi = lane & 15, va = vi & 3, vt = vi >> 2;
-  const int vrd = (8 * (vg16 >> 1) + vt) * 128 + (((4 * (vg16 & 1) + va) ^ (4 * ((vt >> 1) & 1))) * 8);
+  const int vrd = (8 * (vg16 >> 1) + vt) * 64 + (4 * (vg16 & 1) + va) * 8;
 
   const float c_scale = a.softmax_scale * LOG2E;          // raw dot -> log2 units
   const float cap_in = CAP ? 2.0f * LOG2E * a.softmax_scale / a.softcap : 0.0f;
@@ -365,14 +380,14 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     }
   };
   auto pv = [&](int st, const u32x4 (&pop)[NB][2]) {
-    const char* vl = vbuf0 + ((st >> 1) & 1) * VTILE + (st & 1) * 32 * 128;
+    const char* vl = vbuf0 + ((st >> 1) & 1) * VTILE + (st & 1) * 32 * 64;
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const int imm = 16 * c * 128 + (db >> 1) * PF_GROUP_BYTES + (db & 1) * 64;
+        const int imm = 16 * c * 64 + db * PF_VBLOCK_BYTES;
         const u32x2 lo = lds_read_tr(vl, vrd + imm);
-        const u32x2 hi = lds_read_tr(vl, vrd + imm + 4 * 128);
+        const u32x2 hi = lds_read_tr(vl, vrd + imm + 4 * 64);
         const u32x4 av = {lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) o[nb][db] = mfma32<T>(av, pop[nb][c], o[nb][db]);
