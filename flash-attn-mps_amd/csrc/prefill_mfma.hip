@@ -244,22 +244,39 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     const int bytes = __builtin_amdgcn_readfirstlane(nvalid > 0 ? (nvalid - 1) * (int)row_b + row_bytes : 0);
     return __builtin_amdgcn_make_buffer_rsrc((void*)g, (short)0, bytes, 0x00020000);
   };
+  // The same for a group known to hold 16 keys of the request: scalar
+  // arithmetic only, size = 16 rows.
+  const int knrec = 15 * (int)krow_b + 2 * DQ, vnrec = 15 * (int)vrow_b + 2 * DV;
+  auto full_rsrc = [&](const char* head, uint32_t row_b, uint32_t page_b, int key0, int nrec) {
+    const char* g;
+    if (paged) {
+      const uint32_t blk = (uint32_t)load_invariant_i32(trow, (int64_t)(key0 >> lp) * bt1);
+      g = head + (uint64_t)blk * page_b + (uint32_t)(key0 & pmask) * row_b;
+    } else {
+      g = head + (uint64_t)(uint32_t)(r.k_base + key0) * row_b;
+    }
+    return __builtin_amdgcn_make_buffer_rsrc((void*)g, (short)0, nrec, 0x00020000);
+  };
   // K rows 32 half .. +32 of a tile (row blocks 4 half .. +4).
-  auto dma_k = [&](int tile, int buf, int half) {
+  auto dma_k = [&](auto full_tag, int tile, int buf, int half) {
 #pragma unroll
     for (int i = 0; i < 8 / W; ++i) {
       const int rb = wave_u + W * i;
       if ((rb >> 2) != half) continue;
-      const auto rsrc = group_rsrc(khead, krow_b, kpage_b, tile * PF_BN + 16 * (rb >> 1), 2 * DQ);
+      const int key0 = tile * PF_BN + 16 * (rb >> 1);
+      const auto rsrc = decltype(full_tag)::value ? full_rsrc(khead, krow_b, kpage_b, key0, knrec)
+                                                  : group_rsrc(khead, krow_b, kpage_b, key0, 2 * DQ);
       dma_columns<KG>(rsrc, kbuf0 + buf * KTILE + rb * 1024, kdoff);
     }
   };
-  auto dma_v = [&](int tile, int buf) {
+  auto dma_v = [&](auto full_tag, int tile, int buf) {
 #pragma unroll
     for (int i = 0; i < (4 + W - 1) / W; ++i) {
       const int gi = wave_u + W * i;
       if (gi >= 4) continue;
-      const auto rsrc = group_rsrc(vhead, vrow_b, vpage_b, tile * PF_BN + 16 * gi, 2 * DV);
+      const int key0 = tile * PF_BN + 16 * gi;
+      const auto rsrc = decltype(full_tag)::value ? full_rsrc(vhead, vrow_b, vpage_b, key0, vnrec)
+                                                  : group_rsrc(vhead, vrow_b, vpage_b, key0, 2 * DV);
       dma_blocks<2 * VG>(rsrc, vbuf0 + buf * VTILE + gi * 1024, vdoff);
     }
   };
@@ -412,24 +429,27 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // DMAs and barrier, after which V(j), K(j) rows 32..63 and K(j+1) rows
   // 0..31 are resident and every wave is done with V(j-1), K(j-1) rows
   // 32..63 and K(j) rows 0..31; then V(j+1), K(j+1) rows 32..63 and K(j+2)
-  // rows 0..31 are issued into the freed buffer halves.
-  auto tile_start = [&](int st) {
+  // rows 0..31 are issued into the freed buffer halves.  With full_tag
+  // true the caller guarantees that those tiles lie inside the request.
+  auto tile_start = [&](auto full_tag, int st) {
     if ((st & 1) == 0) {
       const int j = st >> 1;
       __builtin_amdgcn_s_waitcnt(0x0F70);
       __syncthreads();
       if (j + 1 < n_tiles) {
-        dma_v(j + 1, (j + 1) & 1);
-        dma_k(j + 1, (j + 1) & 1, 1);
+        dma_v(full_tag, j + 1, (j + 1) & 1);
+        dma_k(full_tag, j + 1, (j + 1) & 1, 1);
       }
-      if (j + 2 < n_tiles) dma_k(j + 2, j & 1, 0);
+      if (j + 2 < n_tiles) dma_k(full_tag, j + 2, j & 1, 0);
     }
   };
+  // Tiles j + 1 and (if it exists) j + 2 hold 64 keys of the request each.
+  auto dma_full = [&](int j) { return PF_BN * (j + 2 < n_tiles ? j + 3 : j + 2) <= r.k_len; };
   // Steady state: stage st and st+1 both active, st+1 unmasked.  One
   // straight scheduling region: phase B(st) under the MFMAs of S(st+1),
   // phase A(st+1) under the MFMAs of P.V(st).
   auto step_hot = [&](int st, f32x16 (&sc)[NB], f32x16 (&sn)[NB], float (&f)[NB]) {
-    tile_start(st);
+    tile_start(std::integral_constant<bool, true>(), st);
     rescale_o(f);
     u32x4 pop[NB][2];
     phase_b(sc, pop);
@@ -442,7 +462,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // rows hold valid or stale finite data) and its phase A then commits
   // nothing.
   auto step_any = [&](int st, f32x16 (&sc)[NB], f32x16 (&sn)[NB], float (&f)[NB]) {
-    tile_start(st);
+    tile_start(std::integral_constant<bool, false>(), st);
     if (!active(st)) return;
     const bool act_n = st + 1 < n_stages && active(st + 1);
     rescale_o(f);
@@ -457,10 +477,11 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
 
   if (n_stages > 0) {
     // Prologue: tile 0 and K(1) rows 0..31 in LDS; S(0) and its phase A.
-    dma_k(0, 0, 0);
-    dma_k(0, 0, 1);
-    dma_v(0, 0);
-    if (n_tiles > 1) dma_k(1, 1, 0);
+    const std::integral_constant<bool, false> any_tile;
+    dma_k(any_tile, 0, 0, 0);
+    dma_k(any_tile, 0, 0, 1);
+    dma_v(any_tile, 0, 0);
+    if (n_tiles > 1) dma_k(any_tile, 1, 1, 0);
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
     f32x16 sa[NB], sb[NB];
@@ -473,7 +494,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     }
     int st = 0;
     if (active(0))
-      for (; hot(st + 1) && hot(st + 2); st += 2) {
+      for (; hot(st + 1) && hot(st + 2) && dma_full(st >> 1); st += 2) {
         step_hot(st, sa, sb, f);
         step_hot(st + 1, sb, sa, f);
       }
