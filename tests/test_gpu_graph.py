@@ -1,0 +1,169 @@
+"""HIP-graph capture of the cache, decode and prefill paths.
+
+The host layer reads no device values while it dispatches (the reference
+makes the same point for its decode route, flash_attn_mps/_attention.py:96-98),
+so one call can be captured into a torch.cuda.CUDAGraph and replayed.  Each
+test writes fresh inputs into the captured buffers, runs the same call eagerly
+(other GPU work between replays), replays the graph several times and
+requires every replay to equal the eager result bit for bit.  The first
+eager result is also held to the fp64 oracle.
+"""
+import pytest
+import torch
+
+import flash_attn_mps_amd as fa
+from flash_attn_mps_amd import vllm
+from helpers import assert_attention_close, attention_reference
+
+pytestmark = pytest.mark.gpu
+
+REPLAYS = 3
+
+
+def capture(fn):
+    """Warm up on a side stream (default priority), then capture fn once."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        result = fn()
+    torch.cuda.synchronize()
+    return graph, result
+
+
+def paged_cache(ctx, page, hkv, dq, dv, dtype, device, gen, scale=None):
+    """Caches filled by store_kvcache through a random page permutation."""
+    pages = [(c + page - 1) // page for c in ctx]
+    pool = sum(pages) + 3
+    perm = torch.randperm(pool, generator=gen)
+    width = max(pages)
+    table = torch.zeros(len(ctx), width, dtype=torch.int32)
+    start = 0
+    slots = []
+    for b, (c, n) in enumerate(zip(ctx, pages)):
+        table[b, :n] = perm[start:start + n].int()
+        start += n
+        pos = torch.arange(c)
+        slots.append(table[b, pos // page].long() * page + pos % page)
+    slots = torch.cat(slots).to(device)
+    src = torch.bfloat16 if dtype == torch.float8_e4m3fn else dtype
+    k = torch.randn(len(slots), hkv, dq, generator=gen).to(src).to(device)
+    v = torch.randn(len(slots), hkv, dv, generator=gen).to(src).to(device)
+    kc = torch.zeros(pool, page, hkv, dq, dtype=dtype, device=device)
+    vc = torch.zeros(pool, page, hkv, dv, dtype=dtype, device=device)
+    fa.store_kvcache(k, v, kc, vc, slots, k_scale=scale, v_scale=scale)
+    return kc, vc, table.to(device)
+
+
+def test_graph_kvcache_decode_with_growing_lengths(device):
+    gen = torch.Generator().manual_seed(71)
+    ctx = [2900, 17, 1500, 2048, 640, 1, 3000, 999]
+    hq, hkv, d, page = 32, 8, 128, 16
+    kc, vc, table = paged_cache(ctx, page, hkv, d, d, torch.bfloat16, device, gen)
+    lens = torch.tensor([c - REPLAYS for c in ctx], dtype=torch.int32, device=device).clamp_(min=0)
+    q = torch.randn(len(ctx), 1, hq, d, generator=gen).to(torch.bfloat16).to(device)
+
+    def call():
+        return fa.flash_attn_with_kvcache(q, kc, vc, cache_seqlens=lens, block_table=table,
+                                          causal=True, return_softmax_lse=True)
+
+    graph, (g_out, g_lse) = capture(call)
+    for it in range(REPLAYS):
+        q.copy_(torch.randn(q.shape, generator=gen).to(torch.bfloat16))
+        lens.add_(1)                       # decode step: every request grows by one key
+        e_out, e_lse = call()
+        if it == 0:
+            cq = torch.arange(len(ctx) + 1, dtype=torch.int32)
+            ref, _ = attention_reference(q[:, 0], kc, vc, cq, used_k=lens, block_table=table, causal=True)
+            assert_attention_close(e_out[:, 0], ref, torch.bfloat16)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(g_out, e_out), f"replay {it}"
+        assert torch.equal(g_lse, e_lse), f"replay {it}"
+
+
+def test_graph_vllm_fp8_decode_into_caller_out(device):
+    gen = torch.Generator().manual_seed(72)
+    ctx = [4100, 1024, 6000, 333, 2500, 4096]
+    hq, hkv, d, page = 16, 8, 256, 16
+    scale = torch.empty(hkv).uniform_(0.01, 0.1, generator=gen).to(device)
+    kc, vc, table = paged_cache(ctx, page, hkv, d, d, torch.float8_e4m3fn, device, gen, scale=scale)
+    b = len(ctx)
+    q = torch.randn(b, hq, d, generator=gen).to(torch.bfloat16).to(device)
+    cuq = torch.arange(b + 1, dtype=torch.int32, device=device)
+    used = torch.tensor(ctx, dtype=torch.int32, device=device)
+    desc = scale.expand(b, hkv)
+    out = torch.empty(b, hq, d, dtype=torch.bfloat16, device=device)
+
+    def call():
+        return vllm.flash_attn_varlen_func(q, kc, vc, 1, cuq, max(ctx), seqused_k=used, block_table=table,
+                                           causal=True, softcap=50.0, window_size=(4095, 0),
+                                           k_descale=desc, v_descale=desc, out=out)
+
+    graph, _ = capture(call)
+    for it in range(REPLAYS):
+        q.copy_(torch.randn(q.shape, generator=gen).to(torch.bfloat16))
+        call()
+        eager = out.clone()
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {it}"
+
+
+def test_graph_varlen_prefill_with_lse(device):
+    gen = torch.Generator().manual_seed(73)
+    lengths = [700, 1, 256, 1300, 64]
+    hq, hkv, d = 16, 8, 128
+    total = sum(lengths)
+    q = torch.randn(total, hq, d, generator=gen).to(torch.bfloat16).to(device)
+    k = torch.randn(total, hkv, d, generator=gen).to(torch.bfloat16).to(device)
+    v = torch.randn(total, hkv, d, generator=gen).to(torch.bfloat16).to(device)
+    cu = torch.tensor([0] + torch.tensor(lengths).cumsum(0).tolist(), dtype=torch.int32, device=device)
+
+    def call():
+        return fa.flash_attn_varlen_func(q, k, v, cu, cu, max(lengths), max(lengths), causal=True,
+                                         return_softmax_lse=True)
+
+    graph, (g_out, g_lse) = capture(call)
+    for it in range(REPLAYS):
+        for t in (q, k, v):
+            t.copy_(torch.randn(t.shape, generator=gen).to(torch.bfloat16))
+        e_out, e_lse = call()
+        if it == 0:
+            ref, ref_lse = attention_reference(q, k, v, cu, cu, causal=True)
+            assert_attention_close(e_out, ref, torch.bfloat16)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(g_out, e_out), f"replay {it}"
+        assert torch.equal(g_lse, e_lse), f"replay {it}"
+
+
+def test_graph_store_kvcache(device):
+    gen = torch.Generator().manual_seed(74)
+    tokens, hkv, d, page, pool = 300, 8, 128, 16, 40
+    kc = torch.zeros(pool, page, hkv, d, dtype=torch.bfloat16, device=device)
+    vc = torch.zeros_like(kc)
+    slots = torch.randperm(pool * page, generator=gen)[:tokens].to(device)
+    slots[::37] = -1                                   # skipped slots
+    k = torch.randn(tokens, hkv, d, generator=gen).to(torch.bfloat16).to(device)
+    v = torch.randn(tokens, hkv, d, generator=gen).to(torch.bfloat16).to(device)
+
+    def call():
+        fa.store_kvcache(k, v, kc, vc, slots)
+
+    graph, _ = capture(call)
+    for it in range(REPLAYS):
+        k.copy_(torch.randn(k.shape, generator=gen).to(torch.bfloat16))
+        v.copy_(torch.randn(v.shape, generator=gen).to(torch.bfloat16))
+        graph.replay()
+        torch.cuda.synchronize()
+        ok = slots >= 0
+        s = slots[ok].long()
+        assert torch.equal(kc.view(-1, hkv, d)[s], k[ok]), f"replay {it}"
+        assert torch.equal(vc.view(-1, hkv, d)[s], v[ok]), f"replay {it}"
