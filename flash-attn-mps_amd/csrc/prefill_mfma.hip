@@ -132,10 +132,83 @@ FA_DEV u32x2 lds_read_tr(const char* base, int off) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + off)));
 }
 
+// The request of rank `rank` when the batch (at most 64 requests) is ordered
+// by decreasing key count, ties by index.  Lane i ranks request i; every
+// wave computes the same answer.
+FA_DEV int64_t request_by_rank(const fa_attn_args& a, int64_t rank, int lane) {
+  const int n = (int)a.batch;
+  int len = -1;
+  if (lane < n) {
+    len = a.seqused_k ? a.seqused_k[lane * a.used_k_stride]
+                      : a.cu_seqlens_k[(lane + 1) * a.cu_k_stride] - a.cu_seqlens_k[lane * a.cu_k_stride];
+  }
+  int r = 0;
+  for (int j = 0; j < n; ++j) {
+    const int lj = __builtin_amdgcn_readlane(len, j);
+    r += (lj > len || (lj == len && j < lane)) ? 1 : 0;
+  }
+  const uint64_t hit = __ballot(lane < n && r == rank);
+  return (int64_t)__builtin_ctzll(hit);
+}
+
 struct PrefillShape {
   int n_qblocks;
   int log2_page;   // paged K/V: page size = 1 << log2_page
+  int compact;     // 1: workgroups map onto the compact work list
 };
+
+// One workgroup's share of the compact work list.  XCD x owns KV heads
+// x, x + 8, ... (Hkv a multiple of 8) of every request; requests come in
+// order of decreasing key count (ties by index), and request b contributes
+// m = Hkv / 8 KV heads x ceil(q_len / BM) query blocks x G query heads,
+// ordered KV head, then query block heaviest-first, then query head.  Slots
+// past the end of the list get no item.  Lane i evaluates request i (at
+// most 64 requests); every wave computes the same answer.
+struct WorkItem {
+  int64_t b;
+  int qb, kh, g;
+  RequestInfo r;
+};
+
+template <int BM>
+FA_DEV bool compact_item(const fa_attn_args& a, int slot, int xcd, int lane, int G, WorkItem& w) {
+  const int n = (int)a.batch;
+  int qbeg = 0, qlen = 0, klen = -1, kbase = 0;
+  if (lane < n) {
+    qbeg = a.cu_seqlens_q[lane * a.cu_q_stride];
+    qlen = a.cu_seqlens_q[(lane + 1) * a.cu_q_stride] - qbeg;
+    const int kc = a.cu_seqlens_k ? a.cu_seqlens_k[lane * a.cu_k_stride] : 0;
+    kbase = a.page_size ? 0 : kc;
+    klen = a.seqused_k ? a.seqused_k[lane * a.used_k_stride] : a.cu_seqlens_k[(lane + 1) * a.cu_k_stride] - kc;
+  }
+  const bool skip = (a.flags & FA_FLAG_SKIP_SINGLE_QUERY) && qlen == 1;   // the decode kernel owns it
+  const int nqb = (lane < n && !skip) ? (qlen + BM - 1) / BM : 0;
+  int before = 0;   // query blocks of the requests ranked ahead of this one
+  for (int j = 0; j < n; ++j) {
+    const int lj = __builtin_amdgcn_readlane(klen, j);
+    const int nj = __builtin_amdgcn_readlane(nqb, j);
+    before += (lj > klen || (lj == klen && j < lane)) ? nj : 0;
+  }
+  const int per_block = (int)(a.heads_k / 8) * G;
+  const int lo = before * per_block;
+  const uint64_t hit = __ballot(lane < n && slot >= lo && slot < lo + nqb * per_block);
+  if (hit == 0) return false;
+  const int i = __builtin_ctzll(hit);
+  const int nq = __builtin_amdgcn_readlane(nqb, i);
+  const int t = slot - __builtin_amdgcn_readlane(lo, i);
+  const int t2 = t % (nq * G);
+  w.b = i;
+  w.kh = xcd + 8 * (t / (nq * G));
+  w.qb = nq - 1 - t2 / G;
+  w.g = t2 % G;
+  w.r.q_begin = __builtin_amdgcn_readlane(qbeg, i);
+  w.r.q_len = __builtin_amdgcn_readlane(qlen, i);
+  w.r.k_len = __builtin_amdgcn_readlane(klen, i);
+  w.r.k_base = __builtin_amdgcn_readlane(kbase, i);
+  w.r.left = 0;
+  w.r.causal = a.causal != 0;
+  return true;
+}
 
 template <typename T, int DQ, int DV, int W, int NB, int MINB, bool CAUSAL, bool CAP>
 __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_args a, const PrefillShape shp) {
@@ -154,21 +227,34 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int wave_u = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index as a scalar
   // Work order.  Workgroups are dispatched round-robin over the 8 XCDs
-  // (XCD = blockIdx % 8), each with its own L2.  XCD x takes the (request,
-  // KV head) pairs p = x, x + 8, ... one after another, and within a pair the
-  // query blocks of its G query heads heaviest-first.
+  // (XCD = blockIdx % 8), each with its own L2, and every XCD works through
+  // whole (request, KV head) pairs one after another, query blocks
+  // heaviest-first, so the resident workgroups of an XCD share K/V in its L2.
+  // Requests come longest first (batches of up to 64), so the grid ends on
+  // the blocks of short requests rather than on the heavy blocks of a long
+  // one.  Compact mode launches only real work; otherwise XCD x takes the
+  // pairs p = x, x + 8, ... with n_qblocks slots each and skips the slots
+  // past a request's end.
   const int G = (int)(a.heads_q / a.heads_k);
   const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
-  const int per_pair = shp.n_qblocks * G;
-  const int64_t pair = (int64_t)(slot / per_pair) * 8 + xcd;
-  if (pair >= a.batch * a.heads_k) return;
-  const int rem = slot % per_pair;
-  const int qb = shp.n_qblocks - 1 - rem / G;
-  const int64_t b = pair / a.heads_k;
-  const int kh = (int)(pair % a.heads_k);
-  const int h = kh * G + rem % G;
-  const RequestInfo r = load_request(a, b);
-  if ((a.flags & FA_FLAG_SKIP_SINGLE_QUERY) && r.q_len == 1) return;   // the decode kernel owns it
+  WorkItem wi;
+  if (shp.compact) {
+    if (!compact_item<BM>(a, slot, xcd, lane, G, wi)) return;
+  } else {
+    const int per_pair = shp.n_qblocks * G;
+    const int64_t pair = (int64_t)(slot / per_pair) * 8 + xcd;
+    if (pair >= a.batch * a.heads_k) return;
+    const int rem = slot % per_pair;
+    wi.qb = shp.n_qblocks - 1 - rem / G;
+    wi.g = rem % G;
+    wi.b = a.batch > 1 && a.batch <= 64 ? request_by_rank(a, pair / a.heads_k, lane) : pair / a.heads_k;
+    wi.kh = (int)(pair % a.heads_k);
+    wi.r = load_request(a, wi.b);
+    if ((a.flags & FA_FLAG_SKIP_SINGLE_QUERY) && wi.r.q_len == 1) return;   // the decode kernel owns it
+  }
+  const int64_t b = wi.b;
+  const int qb = wi.qb, kh = wi.kh, h = kh * G + wi.g;
+  const RequestInfo r = wi.r;
   const int q0 = qb * BM;
   if (q0 >= r.q_len) return;
   const int off = r.k_len - r.q_len;   // absolute position of query row i is i + off
@@ -636,7 +722,19 @@ extern "C" int fa_prefill_fwd(const fa_attn_args* a, void* stream) {
   if (a->page_size)
     while ((1ll << shp.log2_page) < a->page_size) ++shp.log2_page;
   const int64_t pairs = a->batch * a->heads_k;
-  const int64_t blocks = fa_ceil_div(pairs, 8) * 8 * shp.n_qblocks * (a->heads_q / a->heads_k);
+  const int64_t group = a->heads_q / a->heads_k;
+  int64_t blocks = fa_ceil_div(pairs, 8) * 8 * shp.n_qblocks * group;
+  // Compact work list: at most sum ceil(q_len / BM) <= (T + B (BM - 1)) / BM
+  // query blocks per request-ordered KV head.
+  shp.compact = 0;
+  if (a->batch <= 64 && a->heads_k % 8 == 0) {
+    const int64_t qblocks = (a->total_q + a->batch * (ch.bm - 1)) / ch.bm;
+    const int64_t compact = 8 * (a->heads_k / 8) * group * qblocks;
+    if (compact < blocks) {
+      blocks = compact;
+      shp.compact = 1;
+    }
+  }
   FA_REQUIRE(blocks <= 0x7fffffffll, "fa_prefill_fwd: grid too large");
   hipError_t err = hipFuncSetAttribute((const void*)ch.kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ch.lds);
   if (err != hipSuccess) {
