@@ -219,3 +219,57 @@ def test_mixed_batch_routes_single_queries_to_decode(device, dq, dv):
         many += [start + i for i in range(n) if m - n + i + 1 >= 32]
         start += n
     assert_north_star(out, lse, ref, ref_lse, torch.bfloat16, rows=torch.tensor(many))
+
+
+@pytest.mark.parametrize("batch,hq,hkv", [(64, 16, 8), (65, 16, 8), (7, 16, 16), (33, 48, 24), (20, 12, 4)])
+def test_prefill_work_list_modes(device, batch, hq, hkv):
+    """Batches of at most 64 requests with a multiple of 8 KV heads launch the
+    compact work list (longest request first); other shapes the per-pair
+    grid.  Lengths include empty and one-row requests, and q carries spare
+    rows past the last request."""
+    g = torch.Generator().manual_seed(batch * 100 + hkv)
+    q_lens = torch.randint(0, 200, (batch,), generator=g)
+    q_lens[::9] = 0
+    q_lens[1::11] = 1
+    extra = torch.randint(0, 64, (batch,), generator=g)
+    k_lens = (q_lens + extra).tolist()
+    q_lens = q_lens.tolist()
+    spare = 70
+    q = (torch.randn(sum(q_lens) + spare, hq, 128, generator=g) * 0.5).to(torch.bfloat16).to(device)
+    k = (torch.randn(sum(k_lens), hkv, 128, generator=g) * 0.5).to(torch.bfloat16).to(device)
+    v = torch.randn(sum(k_lens), hkv, 128, generator=g).to(torch.bfloat16).to(device)
+    cuq, cuk = cu_from_lengths(q_lens, device), cu_from_lengths(k_lens, device)
+    out = torch.full_like(q, float("nan"))
+    res = flash_attn_varlen_func(q, k, v, cuq, cuk, max(q_lens), max(k_lens), causal=True,
+                                 return_softmax_lse=True, out=out)
+    lse = res[1]
+    ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=True)
+    rows = torch.arange(sum(q_lens))
+    assert_north_star(out, lse, ref, ref_lse, torch.bfloat16, rows=rows)
+    assert torch.isnan(out[sum(q_lens):].float()).all(), "spare rows past the last request were written"
+
+
+def test_mixed_batch_compact_work_list(device):
+    """Mixed chunked prefill + decode with 8 KV heads: the compact work list
+    gives single-query requests no prefill workgroups."""
+    g = torch.Generator().manual_seed(5)
+    page, hq, hkv, d = 16, 16, 8, 128
+    q_lens = [1, 300, 1, 1, 77, 1, 2, 129]
+    k_lens = [900, 700, 1, 4000, 77, 33, 2, 1000]
+    cols = max((n + page - 1) // page for n in k_lens)
+    pool = cols * len(k_lens)
+    table = torch.randperm(pool, generator=g).int().reshape(len(k_lens), cols)
+    kc = torch.randn(pool, page, hkv, d, generator=g).to(torch.bfloat16).to(device)
+    vc = torch.randn(pool, page, hkv, d, generator=g).to(torch.bfloat16).to(device)
+    q = (torch.randn(sum(q_lens), hq, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
+    cuq = cu_from_lengths(q_lens, device)
+    used = torch.tensor(k_lens, dtype=torch.int32, device=device)
+    out, lse = vllm.flash_attn_varlen_func(q, kc, vc, max(q_lens), cuq, cols * page, seqused_k=used,
+                                           block_table=table.to(device), causal=True, return_softmax_lse=True)
+    ref, ref_lse = attention_reference(q, kc, vc, cuq, used_k=used, block_table=table, causal=True)
+    assert_reference_tol(out, lse, ref, ref_lse, torch.bfloat16)
+    many, start = [], 0
+    for n, m in zip(q_lens, k_lens):
+        many += [start + i for i in range(n) if m - n + i + 1 >= 32]
+        start += n
+    assert_north_star(out, lse, ref, ref_lse, torch.bfloat16, rows=torch.tensor(many))
