@@ -625,6 +625,12 @@ template <int DQ, int DV> struct PrefillTile;
 template <> struct PrefillTile<64, 64> { static constexpr int W = 4, NB = 1, MINB = 2; };
 template <> struct PrefillTile<128, 128> { static constexpr int W = FA_PF128_W, NB = FA_PF128_NB, MINB = FA_PF128_MINB; };
 template <> struct PrefillTile<192, 128> { static constexpr int W = 4, NB = 1, MINB = 1; };
+// Large grids of 192/128 heads: two workgroups per CU (2 x 80 KiB of LDS)
+// trade registers for a second wave per SIMD.  Few-workgroup launches keep
+// one workgroup per CU, whose heavy blocks then run at full speed.
+template <int DQ, int DV> struct PrefillTileWide { static constexpr bool exists = false; };
+template <> struct PrefillTileWide<192, 128> { static constexpr bool exists = true; static constexpr int W = 4, NB = 1, MINB = 2; };
+constexpr int64_t PF_WIDE_MIN_BLOCKS = 2048;
 template <> struct PrefillTile<256, 256> { static constexpr int W = 4, NB = 1, MINB = 1; };
 
 template <int DQ, int DV>
@@ -640,9 +646,8 @@ struct PrefillChoice {
   size_t lds;
 };
 
-template <typename T, int DQ, int DV, bool CAUSAL>
-PrefillChoice pick_cap(bool cap) {
-  using S = PrefillTile<DQ, DV>;
+template <typename T, int DQ, int DV, bool CAUSAL, typename S>
+PrefillChoice pick_tile(bool cap) {
   PrefillChoice c;
   c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, true>
                : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false>;
@@ -652,24 +657,35 @@ PrefillChoice pick_cap(bool cap) {
   return c;
 }
 
+template <typename T, int DQ, int DV, bool CAUSAL>
+PrefillChoice pick_cap(bool cap, bool wide) {
+  if constexpr (PrefillTileWide<DQ, DV>::exists) {
+    static_assert(32 * PrefillTileWide<DQ, DV>::NB * PrefillTileWide<DQ, DV>::W ==
+                      32 * PrefillTile<DQ, DV>::NB * PrefillTile<DQ, DV>::W,
+                  "both tiles cover the same query rows per workgroup");
+    if (wide) return pick_tile<T, DQ, DV, CAUSAL, PrefillTileWide<DQ, DV>>(cap);
+  }
+  return pick_tile<T, DQ, DV, CAUSAL, PrefillTile<DQ, DV>>(cap);
+}
+
 template <typename T, int DQ, int DV>
-PrefillChoice pick(bool causal, bool cap) {
-  return causal ? pick_cap<T, DQ, DV, true>(cap) : pick_cap<T, DQ, DV, false>(cap);
+PrefillChoice pick(bool causal, bool cap, bool wide) {
+  return causal ? pick_cap<T, DQ, DV, true>(cap, wide) : pick_cap<T, DQ, DV, false>(cap, wide);
 }
 
 template <typename T>
-PrefillChoice pick_dims(int64_t dq, int64_t dv, bool causal, bool cap) {
-  if (dq == 64 && dv == 64) return pick<T, 64, 64>(causal, cap);
-  if (dq == 128 && dv == 128) return pick<T, 128, 128>(causal, cap);
-  if (dq == 192 && dv == 128) return pick<T, 192, 128>(causal, cap);
-  if (dq == 256 && dv == 256) return pick<T, 256, 256>(causal, cap);
+PrefillChoice pick_dims(int64_t dq, int64_t dv, bool causal, bool cap, bool wide) {
+  if (dq == 64 && dv == 64) return pick<T, 64, 64>(causal, cap, wide);
+  if (dq == 128 && dv == 128) return pick<T, 128, 128>(causal, cap, wide);
+  if (dq == 192 && dv == 128) return pick<T, 192, 128>(causal, cap, wide);
+  if (dq == 256 && dv == 256) return pick<T, 256, 256>(causal, cap, wide);
   return PrefillChoice{nullptr, 0, 0, 0};
 }
 
-PrefillChoice select_prefill(const fa_attn_args& a) {
+PrefillChoice select_prefill(const fa_attn_args& a, bool wide) {
   const bool causal = a.causal != 0, cap = a.softcap > 0.0f;
-  return a.q_dtype == FA_BF16 ? pick_dims<BF16T>(a.head_dim_qk, a.head_dim_v, causal, cap)
-                              : pick_dims<F16T>(a.head_dim_qk, a.head_dim_v, causal, cap);
+  return a.q_dtype == FA_BF16 ? pick_dims<BF16T>(a.head_dim_qk, a.head_dim_v, causal, cap, wide)
+                              : pick_dims<F16T>(a.head_dim_qk, a.head_dim_v, causal, cap, wide);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -715,7 +731,7 @@ extern "C" int fa_prefill_fwd(const fa_attn_args* a, void* stream) {
   }
   if (a->total_q == 0) return FA_OK;
   FA_REQUIRE(a->max_seqlen_q >= 1, "fa_prefill_fwd: max_seqlen_q must be positive");
-  const PrefillChoice ch = select_prefill(*a);
+  PrefillChoice ch = select_prefill(*a, false);
   PrefillShape shp;
   shp.n_qblocks = (int)fa_ceil_div(a->max_seqlen_q, ch.bm);
   shp.log2_page = 0;
@@ -736,6 +752,9 @@ extern "C" int fa_prefill_fwd(const fa_attn_args* a, void* stream) {
     }
   }
   FA_REQUIRE(blocks <= 0x7fffffffll, "fa_prefill_fwd: grid too large");
+  // Workgroups of real work are about Hq x T / BM (empty slots of the grid
+  // and single-query requests of a mixed batch exit at once).
+  if (a->heads_q * fa_ceil_div(a->total_q, ch.bm) >= PF_WIDE_MIN_BLOCKS) ch = select_prefill(*a, true);
   hipError_t err = hipFuncSetAttribute((const void*)ch.kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ch.lds);
   if (err != hipSuccess) {
     fa_set_error("fa_prefill_fwd: cannot reserve %zu bytes of LDS: %s", ch.lds, hipGetErrorString(err));

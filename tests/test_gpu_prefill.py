@@ -273,3 +273,18 @@ def test_mixed_batch_compact_work_list(device):
         many += [start + i for i in range(n) if m - n + i + 1 >= 32]
         start += n
     assert_north_star(out, lse, ref, ref_lse, torch.bfloat16, rows=torch.tensor(many))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_diffkv_192_128_large_grid(device, causal):
+    """A DIFFKV launch of more than 2048 workgroups takes the two-workgroups-
+    per-CU tile; sampled rows of every request against the fp64 oracle."""
+    q_lens = [2048, 1500, 3000, 1800]
+    hq, hkv = 32, 16
+    q, k, v, cuq, cuk = _case_dims(device, torch.bfloat16, 192, 128, hq, hkv, q_lens, q_lens, seed=11 + causal)
+    out, lse = attention(q, k, v, cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=max(q_lens),
+                         max_seqlen_k=max(q_lens), causal=causal)
+    g = torch.Generator().manual_seed(3)
+    rows = torch.randperm(sum(q_lens), generator=g)[:96].sort().values
+    ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=causal, rows=rows)
+    assert_north_star(out, lse, ref, ref_lse, torch.bfloat16, rows=rows)
