@@ -6,7 +6,8 @@
 // attention.metal:60-181): packed or paged K/V, GQA, lower-right causality,
 // optional softcap, a per-head sink logit that joins the softmax
 // denominator only, fp32 softmax and natural-log LSE.  Head dims (Dqk, Dv)
-// in {(64,64), (128,128), (256,256), (192,128)}.
+// in {(32,32), (64,64), (72,72), (80,80), (96,96), (128,128), (256,256),
+// (192,128)}; 32 and 72/80/96 run zero-padded in the 64 and 128 tiles.
 //
 // gfx950 design
 // * A workgroup is W waves; each wave owns 32 query rows of one head.  K/V
@@ -210,10 +211,16 @@ FA_DEV bool compact_item(const fa_attn_args& a, int slot, int xcd, int lane, int
   return true;
 }
 
-template <typename T, int DQ, int DV, int W, int NB, int MINB, bool CAUSAL, bool CAP>
+// DQ / DV are the tile's head dims (multiples of 64); DQT / DVT <= them are
+// the tensors' own (multiples of 8): the query's extra dims load as zero,
+// their K columns are never multiplied (K-steps past DQT are skipped, a half
+// step is masked), and extra output columns are not stored.
+template <typename T, int DQ, int DV, int W, int NB, int MINB, bool CAUSAL, bool CAP, int DQT = DQ, int DVT = DV>
 __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_args a, const PrefillShape shp) {
   constexpr int BM = 32 * NB * W;              // query rows per workgroup
   constexpr int KST = DQ / 16;                 // k-steps of the QK^T MFMA
+  constexpr int KSTT = (DQT + 15) / 16;        // k-steps holding real dims
+  static_assert(DQT % 8 == 0 && DVT % 8 == 0 && DQT <= DQ && DVT <= DV, "true head dims");
   constexpr int DB = DV / 32;                  // 32-dim blocks of O^T
   constexpr int KG = DQ / 64, VG = DV / 64;    // 64-dim column groups (K), pairs of 32-dim blocks (V)
   constexpr int KTILE = KG * PF_GROUP_BYTES, VTILE = VG * PF_GROUP_BYTES;
@@ -275,7 +282,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
 #pragma unroll
     for (int kk = 0; kk < KST; ++kk) {
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (ok) v = *(const u32x4*)(qp + 16 * kk);
+      if (ok && 16 * kk + 8 * hh + 8 <= DQT) v = *(const u32x4*)(qp + 16 * kk);
       qop[nb][kk] = v;
     }
   }
@@ -332,7 +339,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   };
   // The same for a group known to hold 16 keys of the request: scalar
   // arithmetic only, size = 16 rows.
-  const int knrec = 15 * (int)krow_b + 2 * DQ, vnrec = 15 * (int)vrow_b + 2 * DV;
+  const int knrec = 15 * (int)krow_b + 2 * DQT, vnrec = 15 * (int)vrow_b + 2 * DVT;
   auto full_rsrc = [&](const char* head, uint32_t row_b, uint32_t page_b, int key0, int nrec) {
     const char* g;
     if (paged) {
@@ -351,7 +358,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
       if ((rb >> 2) != half) continue;
       const int key0 = tile * PF_BN + 16 * (rb >> 1);
       const auto rsrc = decltype(full_tag)::value ? full_rsrc(khead, krow_b, kpage_b, key0, knrec)
-                                                  : group_rsrc(khead, krow_b, kpage_b, key0, 2 * DQ);
+                                                  : group_rsrc(khead, krow_b, kpage_b, key0, 2 * DQT);
       dma_columns<KG>(rsrc, kbuf0 + buf * KTILE + rb * 1024, kdoff);
     }
   };
@@ -362,7 +369,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
       if (gi >= 4) continue;
       const int key0 = tile * PF_BN + 16 * gi;
       const auto rsrc = decltype(full_tag)::value ? full_rsrc(vhead, vrow_b, vpage_b, key0, vnrec)
-                                                  : group_rsrc(vhead, vrow_b, vpage_b, key0, 2 * DV);
+                                                  : group_rsrc(vhead, vrow_b, vpage_b, key0, 2 * DVT);
       dma_blocks<2 * VG>(rsrc, vbuf0 + buf * VTILE + gi * 1024, vdoff);
     }
   };
@@ -417,8 +424,11 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
 #pragma unroll
       for (int i = 0; i < 16; ++i) s[nb][i] = 0.0f;
 #pragma unroll
-    for (int kk = 0; kk < KST; ++kk) {
-      const u32x4 av = lds_read16(kl, krd[kk % 4] + (kk / 4) * PF_GROUP_BYTES);
+    for (int kk = 0; kk < KSTT; ++kk) {
+      u32x4 av = lds_read16(kl, krd[kk % 4] + (kk / 4) * PF_GROUP_BYTES);
+      if constexpr (DQT % 16 == 8) {
+        if (kk == KSTT - 1 && hh) av = u32x4{0u, 0u, 0u, 0u};   // dims past DQT: whatever the DMA read
+      }
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) s[nb] = mfma32<T>(av, qop[nb][kk], s[nb]);
     }
@@ -603,6 +613,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
       for (int db = 0; db < DB; ++db)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
+          if (32 * db + 8 * g + 8 > DVT) continue;   // padding columns
           uint2 w;
           w.x = pack2<T>(o[nb][db][4 * g] * inv, o[nb][db][4 * g + 1] * inv);
           w.y = pack2<T>(o[nb][db][4 * g + 2] * inv, o[nb][db][4 * g + 3] * inv);
@@ -646,40 +657,51 @@ struct PrefillChoice {
   size_t lds;
 };
 
-template <typename T, int DQ, int DV, bool CAUSAL, typename S>
+template <typename T, int DQ, int DV, bool CAUSAL, typename S, int DQT, int DVT>
 PrefillChoice pick_tile(bool cap) {
   PrefillChoice c;
-  c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, true>
-               : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false>;
+  c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, true, DQT, DVT>
+               : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false, DQT, DVT>;
   c.bm = 32 * S::NB * S::W;
   c.threads = 64 * S::W;
   c.lds = lds_bytes<DQ, DV>();
   return c;
 }
 
-template <typename T, int DQ, int DV, bool CAUSAL>
+template <typename T, int DQ, int DV, bool CAUSAL, int DQT, int DVT>
 PrefillChoice pick_cap(bool cap, bool wide) {
   if constexpr (PrefillTileWide<DQ, DV>::exists) {
     static_assert(32 * PrefillTileWide<DQ, DV>::NB * PrefillTileWide<DQ, DV>::W ==
                       32 * PrefillTile<DQ, DV>::NB * PrefillTile<DQ, DV>::W,
                   "both tiles cover the same query rows per workgroup");
-    if (wide) return pick_tile<T, DQ, DV, CAUSAL, PrefillTileWide<DQ, DV>>(cap);
+    if (wide) return pick_tile<T, DQ, DV, CAUSAL, PrefillTileWide<DQ, DV>, DQT, DVT>(cap);
   }
-  return pick_tile<T, DQ, DV, CAUSAL, PrefillTile<DQ, DV>>(cap);
+  return pick_tile<T, DQ, DV, CAUSAL, PrefillTile<DQ, DV>, DQT, DVT>(cap);
 }
 
-template <typename T, int DQ, int DV>
+// (DQ, DV) = the tile; (DQT, DVT) = the tensors' head dims padded into it.
+template <typename T, int DQ, int DV, int DQT = DQ, int DVT = DV>
 PrefillChoice pick(bool causal, bool cap, bool wide) {
-  return causal ? pick_cap<T, DQ, DV, true>(cap, wide) : pick_cap<T, DQ, DV, false>(cap, wide);
+  return causal ? pick_cap<T, DQ, DV, true, DQT, DVT>(cap, wide) : pick_cap<T, DQ, DV, false, DQT, DVT>(cap, wide);
 }
 
+// Head dims of the reference's fast path (flash_attn_mps/_attention.py:149-158:
+// 32, 64, 72, 80, 96, 128, 256) plus DIFFKV 192/128; 32 runs in the 64-dim
+// tile and 72/80/96 in the 128-dim tile.
 template <typename T>
 PrefillChoice pick_dims(int64_t dq, int64_t dv, bool causal, bool cap, bool wide) {
-  if (dq == 64 && dv == 64) return pick<T, 64, 64>(causal, cap, wide);
-  if (dq == 128 && dv == 128) return pick<T, 128, 128>(causal, cap, wide);
-  if (dq == 192 && dv == 128) return pick<T, 192, 128>(causal, cap, wide);
-  if (dq == 256 && dv == 256) return pick<T, 256, 256>(causal, cap, wide);
-  return PrefillChoice{nullptr, 0, 0, 0};
+  if (dq != dv && !(dq == 192 && dv == 128)) return PrefillChoice{nullptr, 0, 0, 0};
+  switch (dq) {
+    case 32: return pick<T, 64, 64, 32, 32>(causal, cap, wide);
+    case 64: return pick<T, 64, 64>(causal, cap, wide);
+    case 72: return pick<T, 128, 128, 72, 72>(causal, cap, wide);
+    case 80: return pick<T, 128, 128, 80, 80>(causal, cap, wide);
+    case 96: return pick<T, 128, 128, 96, 96>(causal, cap, wide);
+    case 128: return pick<T, 128, 128>(causal, cap, wide);
+    case 192: return pick<T, 192, 128>(causal, cap, wide);
+    case 256: return pick<T, 256, 256>(causal, cap, wide);
+    default: return PrefillChoice{nullptr, 0, 0, 0};
+  }
 }
 
 PrefillChoice select_prefill(const fa_attn_args& a, bool wide) {
@@ -694,7 +716,9 @@ bool prefill_ok(const fa_attn_args& a) {
   if (!(a.q_dtype == a.k_dtype && a.k_dtype == a.v_dtype && a.v_dtype == a.out_dtype)) return false;
   if (a.q_dtype != FA_BF16 && a.q_dtype != FA_F16) return false;
   const int64_t dq = a.head_dim_qk, dv = a.head_dim_v;
-  if (!((dq == dv && (dq == 64 || dq == 128 || dq == 256)) || (dq == 192 && dv == 128))) return false;
+  if (!((dq == dv && (dq == 32 || dq == 64 || dq == 72 || dq == 80 || dq == 96 || dq == 128 || dq == 256)) ||
+        (dq == 192 && dv == 128)))
+    return false;
   if (a.leftpad_k || a.alibi || a.q_descale || a.k_descale || a.v_descale) return false;
   if (a.mask_kind != 0 || a.causal_by_batch || a.window_left != -1 || a.window_right != -1) return false;
   if (a.num_splits != 1) return false;

@@ -32,7 +32,7 @@ def _case(device, dtype, d, hq, hkv, q_lens, k_lens, scale=1.0, seed=0):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("d", [32, 64, 72, 80, 96, 128, 256])
 @pytest.mark.parametrize("causal", [True, False])
 def test_prefill_dims_causal(device, dtype, d, causal):
     q_lens, k_lens = [1, 37, 300, 64, 513], [5, 37, 300, 200, 700]
@@ -288,3 +288,52 @@ def test_prefill_diffkv_192_128_large_grid(device, causal):
     rows = torch.randperm(sum(q_lens), generator=g)[:96].sort().values
     ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=causal, rows=rows)
     assert_north_star(out, lse, ref, ref_lse, torch.bfloat16, rows=rows)
+
+
+@pytest.mark.parametrize("d", [32, 72, 80, 96])
+@pytest.mark.parametrize("paged", [False, True])
+def test_prefill_padded_dims_ignore_neighbouring_columns(device, d, paged):
+    """Head dims 32/72/80/96 run in the 64/128-dim tiles.  K, V and out are
+    views into wider NaN-filled storage, so the columns the tile reads or
+    computes past d hold NaN: results must still match the oracle, the MFMA
+    route must be the one taken, and out's columns past d stay untouched."""
+    g = torch.Generator().manual_seed(d + 7 * paged)
+    hq, hkv, width, page = 8, 2, 128, 16
+    q_lens, k_lens = [5, 130, 257], [40, 130, 300]
+    q = (torch.randn(sum(q_lens), hq, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
+    cuq = cu_from_lengths(q_lens, device)
+    if paged:
+        cols = max((n + page - 1) // page for n in k_lens)
+        pool = cols * len(k_lens) + 2
+        table = torch.randperm(pool, generator=g)[:cols * len(k_lens)].int().reshape(len(k_lens), cols)
+        kst = torch.full((pool, page, hkv, width), float("nan"), dtype=torch.bfloat16, device=device)
+        vst = torch.full_like(kst, float("nan"))
+        k, v = kst[..., :d], vst[..., :d]
+        k.copy_((torch.randn(pool, page, hkv, d, generator=g) * 0.5).to(torch.bfloat16))
+        v.copy_(torch.randn(pool, page, hkv, d, generator=g).to(torch.bfloat16))
+        used = torch.tensor(k_lens, dtype=torch.int32, device=device)
+        kw = dict(cu_seqlens_k=None, seqused_k=used, block_table=table.to(device))
+        ref_kw = dict(used_k=used, block_table=table)
+        cuk = None
+    else:
+        kst = torch.full((sum(k_lens), hkv, width), float("nan"), dtype=torch.bfloat16, device=device)
+        vst = torch.full_like(kst, float("nan"))
+        k, v = kst[..., :d], vst[..., :d]
+        k.copy_((torch.randn(sum(k_lens), hkv, d, generator=g) * 0.5).to(torch.bfloat16))
+        v.copy_(torch.randn(sum(k_lens), hkv, d, generator=g).to(torch.bfloat16))
+        cuk = cu_from_lengths(k_lens, device)
+        kw = dict(cu_seqlens_k=cuk, seqused_k=None, block_table=None)
+        ref_kw = dict()
+    ost = torch.full((sum(q_lens), hq, width), float("nan"), dtype=torch.bfloat16, device=device)
+    out = ost[..., :d]
+    lse = torch.empty(hq, q.shape[0], device=device)
+    common = dict(max_seqlen_q=max(q_lens), max_seqlen_k=max(k_lens), softmax_scale=None, causal=True,
+                  window_size=(-1, -1), alibi_slopes=None, softcap=0., s_aux=None, q_descale=None,
+                  k_descale=None, v_descale=None, mask_mod=None, aux_tensors=None, leftpad_k=None)
+    assert _uses_mfma(q, k, v, out, lse, cu_seqlens_q=cuq, **kw, **common)
+    res, lse = attention(q, k, v, cu_seqlens_q=cuq, cu_seqlens_k=kw["cu_seqlens_k"], seqused_k=kw["seqused_k"],
+                         block_table=kw["block_table"], max_seqlen_q=max(q_lens), max_seqlen_k=max(k_lens),
+                         causal=True, out=out)
+    ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=True, **ref_kw)
+    assert_north_star(out, lse, ref, ref_lse, torch.bfloat16)
+    assert torch.isnan(ost[..., d:].float()).all(), "columns past the head dim were written"
