@@ -137,9 +137,15 @@ FA_DEV int decode_vis_begin(const fa_attn_args& a, int k_len) {
   return a.window_left >= 0 ? max(0, k_len - a.window_left - 1) : 0;
 }
 
-template <typename CT, typename KT, typename VT, int D, int DV, int GT, bool CAP>
+// D / DV: the tile's head dims; DT / DVT <= them: the tensors' own.  Lanes
+// past the real dims read the row's last real chunk (always in bounds), with
+// a zero query there, so they add nothing to Q.K; their V columns are never
+// stored.
+template <typename CT, typename KT, typename VT, int D, int DV, int GT, bool CAP, int DT = D, int DVT = DV>
 __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const fa_attn_args a, const int span) {
   constexpr int EK = D / 16, EV = DV / 16;
+  constexpr int LK = DT / EK, LV = DVT / EV;   // lanes of a 16-lane row holding real dims
+  static_assert(DT % EK == 0 && DVT % EV == 0 && DT <= D && DVT <= DV, "true head dims fill whole lane chunks");
   constexpr int KB = EK * KT::bytes, VB = EV * VT::bytes;
   constexpr int NT = DecodeRows<KB, VB>::value;
   constexpr int STEP = 4 * NT;          // positions of one wave step
@@ -176,12 +182,17 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
   for (int g = 0; g < GT; ++g) {
     const int64_t q0 = tq * a.q_stride[0] + (int64_t)(h0 + g) * a.q_stride[1];
     if (a.q_stride[2] == 1) {
-      load_words<EK * 2>((const char*)a.q + (q0 + l16 * EK) * 2, qp[g]);
+      load_words<EK * 2>((const char*)a.q + (q0 + min(l16, LK - 1) * EK) * 2, qp[g]);
     } else {
+      const int lq = min(l16, LK - 1);
 #pragma unroll
       for (int j = 0; j < EK / 2; ++j)
-        qp[g][j] = pack_pair_bits<CT>(load_elem<CT>(a.q, q0 + (int64_t)(l16 * EK + 2 * j) * a.q_stride[2]),
-                                      load_elem<CT>(a.q, q0 + (int64_t)(l16 * EK + 2 * j + 1) * a.q_stride[2]));
+        qp[g][j] = pack_pair_bits<CT>(load_elem<CT>(a.q, q0 + (int64_t)(lq * EK + 2 * j) * a.q_stride[2]),
+                                      load_elem<CT>(a.q, q0 + (int64_t)(lq * EK + 2 * j + 1) * a.q_stride[2]));
+    }
+    if (LK < 16 && l16 >= LK) {
+#pragma unroll
+      for (int j = 0; j < EK / 2; ++j) qp[g][j] = 0u;   // padding dims: no contribution to Q.K
     }
   }
 
@@ -205,8 +216,8 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
   // base + blk * page_stride + r * row_stride + kh * head_stride + l16 * E * bytes.
   const uint32_t kpage_b = (uint32_t)(a.k_stride[0] * KT::bytes), vpage_b = (uint32_t)(a.v_stride[0] * VT::bytes);
   const uint32_t krow_b = (uint32_t)(a.k_stride[1] * KT::bytes), vrow_b = (uint32_t)(a.v_stride[1] * VT::bytes);
-  const char* kbase = (const char*)a.k + (int64_t)kh * a.k_stride[2] * KT::bytes + l16 * KB;
-  const char* vbase = (const char*)a.v + (int64_t)kh * a.v_stride[2] * VT::bytes + l16 * VB;
+  const char* kbase = (const char*)a.k + (int64_t)kh * a.k_stride[2] * KT::bytes + min(l16, LK - 1) * KB;
+  const char* vbase = (const char*)a.v + (int64_t)kh * a.v_stride[2] * VT::bytes + min(l16, LV - 1) * VB;
 
   // Address of the split's first key: the read target of rows with no valid position.
   const char* ksafe = kbase;
@@ -404,8 +415,8 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
     }
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < GT * DV; idx += DEC_THREADS) {
-    const int g = idx / DV, d = idx - g * DV;
+  for (int idx = threadIdx.x; idx < GT * DVT; idx += DEC_THREADS) {
+    const int g = idx / DVT, d = idx - g * DVT;
     float M = sm_m[0][g];
 #pragma unroll
     for (int w = 1; w < 4; ++w) M = fmaxf(M, sm_m[w][g]);
@@ -426,7 +437,7 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
       if (d == 0) a.lse[(int64_t)h * a.lse_stride[0] + tq * a.lse_stride[1]] = lse;
     } else {
       const int64_t row = (b * a.heads_q + h) * S + split;
-      a.partial_out[row * DV + d] = O * norm;
+      a.partial_out[row * DVT + d] = O * norm;
       if (d == 0) a.partial_lse[row] = lse;
     }
   }
@@ -489,23 +500,42 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const fa_attn_args a,
 
 using DecodeKernel = void (*)(fa_attn_args, int);
 
-template <typename CT, typename KT, typename VT, int D, int DV, bool CAP>
+template <typename CT, typename KT, typename VT, int D, int DV, bool CAP, int DT = D, int DVT = DV>
 DecodeKernel pick_group(int gt) {
   switch (gt) {
-    case 4: if constexpr (4 * (D + DV) <= 64 * 16) return decode_kernel<CT, KT, VT, D, DV, 4, CAP>; else return nullptr;
-    case 2: if constexpr (2 * (D + DV) <= 64 * 16) return decode_kernel<CT, KT, VT, D, DV, 2, CAP>; else return nullptr;
-    case 1: return decode_kernel<CT, KT, VT, D, DV, 1, CAP>;
+    case 4: if constexpr (4 * (D + DV) <= 64 * 16) return decode_kernel<CT, KT, VT, D, DV, 4, CAP, DT, DVT>; else return nullptr;
+    case 2: if constexpr (2 * (D + DV) <= 64 * 16) return decode_kernel<CT, KT, VT, D, DV, 2, CAP, DT, DVT>; else return nullptr;
+    case 1: return decode_kernel<CT, KT, VT, D, DV, 1, CAP, DT, DVT>;
     default: return nullptr;
   }
 }
 
+// Head dims 32 and 72/80/96 (dq == dv) run in the 64- and 128-dim tiles.
 template <typename CT, typename KT, typename VT, bool CAP>
 DecodeKernel pick_dims_cap(int64_t d, int64_t dv, int gt) {
-  if (d == 64 && dv == 64) return pick_group<CT, KT, VT, 64, 64, CAP>(gt);
-  if (d == 128 && dv == 128) return pick_group<CT, KT, VT, 128, 128, CAP>(gt);
   if (d == 192 && dv == 128) return pick_group<CT, KT, VT, 192, 128, CAP>(gt);
-  if (d == 256 && dv == 256) return pick_group<CT, KT, VT, 256, 256, CAP>(gt);
-  return nullptr;
+  if (d != dv) return nullptr;
+  switch (d) {
+    case 32: return pick_group<CT, KT, VT, 64, 64, CAP, 32, 32>(gt);
+    case 64: return pick_group<CT, KT, VT, 64, 64, CAP>(gt);
+    case 72: return pick_group<CT, KT, VT, 128, 128, CAP, 72, 72>(gt);
+    case 80: return pick_group<CT, KT, VT, 128, 128, CAP, 80, 80>(gt);
+    case 96: return pick_group<CT, KT, VT, 128, 128, CAP, 96, 96>(gt);
+    case 128: return pick_group<CT, KT, VT, 128, 128, CAP>(gt);
+    case 256: return pick_group<CT, KT, VT, 256, 256, CAP>(gt);
+    default: return nullptr;
+  }
+}
+
+// The tile head dim a tensor head dim runs in (0: none).
+int64_t decode_tile_dim(int64_t d) {
+  switch (d) {
+    case 32: case 64: return 64;
+    case 72: case 80: case 96: case 128: return 128;
+    case 192: return 192;
+    case 256: return 256;
+    default: return 0;
+  }
 }
 
 template <typename CT, typename KT, typename VT>
@@ -519,7 +549,7 @@ int elem_size(int dt) { return dt == FA_F32 ? 4 : dt == FA_E4M3 ? 1 : 2; }
 // within 64 fp32 registers per lane.
 int decode_group_tile(const fa_attn_args& a) {
   const int64_t group = a.heads_q / a.heads_k;
-  const int64_t per = (a.head_dim_qk + a.head_dim_v) / 16;
+  const int64_t per = (decode_tile_dim(a.head_dim_qk) + decode_tile_dim(a.head_dim_v)) / 16;
   for (int gt = 4; gt >= 1; gt >>= 1)
     if (group % gt == 0 && gt * per <= 64) return gt;
   return 1;
@@ -544,13 +574,16 @@ DecodeKernel select_decode(const fa_attn_args& a, int* gt_out) {
       return nullptr;
   if (a.k_stride[3] != 1 || a.v_stride[3] != 1) return nullptr;
   const int esz = elem_size(a.k_dtype);
-  if ((a.head_dim_qk / 16) * esz % 4 || (a.head_dim_v / 16) * esz % 4) return nullptr;
-  if (!chunk_aligned(a.k, a.k_stride, 3, esz, (int)(a.head_dim_qk / 16) * esz)) return nullptr;
-  if (!chunk_aligned(a.v, a.v_stride, 3, esz, (int)(a.head_dim_v / 16) * esz)) return nullptr;
+  // Lane chunks are tile dims / 16 elements (the tile may pad the head dim).
+  const int64_t tq = decode_tile_dim(a.head_dim_qk), tv = decode_tile_dim(a.head_dim_v);
+  if (!tq || !tv) return nullptr;
+  if ((tq / 16) * esz % 4 || (tv / 16) * esz % 4) return nullptr;
+  if (!chunk_aligned(a.k, a.k_stride, 3, esz, (int)(tq / 16) * esz)) return nullptr;
+  if (!chunk_aligned(a.v, a.v_stride, 3, esz, (int)(tv / 16) * esz)) return nullptr;
   // Q.K runs on 16-bit pairs of the query's type: 16-bit K must match it,
   // FP8 K widens exactly to either.
   if (a.q_dtype != FA_BF16 && a.q_dtype != FA_F16) return nullptr;
-  if (a.q_stride[2] == 1 && !chunk_aligned(a.q, a.q_stride, 2, 2, (int)(a.head_dim_qk / 16) * 2)) return nullptr;
+  if (a.q_stride[2] == 1 && !chunk_aligned(a.q, a.q_stride, 2, 2, (int)(tq / 16) * 2)) return nullptr;
   const int gt = decode_group_tile(a);
   *gt_out = gt;
   const bool qbf = a.q_dtype == FA_BF16, cap = a.softcap > 0.0f;

@@ -34,10 +34,15 @@ def split_plan(batch, head_groups, effective_max, num_splits):
     return -(-effective_max // span), span
 
 
+def _tile_dim(d):
+    """Head dim of the decode tile a tensor head dim runs in (decode_tile_dim)."""
+    return {32: 64, 72: 128, 80: 128, 96: 128}.get(d, d)
+
+
 def decode_group_tile(heads, kvheads, dq, dv):
     """Query heads per workgroup; must match decode_group_tile() in decode_kernel.hip."""
     group = heads // kvheads
-    per = (dq + dv) // 16
+    per = (_tile_dim(dq) + _tile_dim(dv)) // 16
     for gt in (4, 2, 1):
         if group % gt == 0 and gt * per <= 64:
             return gt

@@ -244,3 +244,45 @@ def test_decode_kernel_choice_ignores_lengths(device):
                        k_descale=None, v_descale=None, mask_mod=None, aux_tensors=None, leftpad_k=None, keep=keep)
         choices.add(_lib.supported("fa_decode_supported", a))
     assert choices == {True}
+
+
+@pytest.mark.parametrize("d", [32, 72, 80, 96])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("splits", [0, 3])
+def test_decode_padded_head_dims(device, d, dtype, splits):
+    """Head dims 32 and 72/80/96 run on the decode kernel in its 64/128-dim
+    tiles.  The caches are views into wider NaN-filled storage, so any read
+    past the head dim would poison the result; out's extra columns must stay
+    untouched."""
+    from flash_attn_mps_amd._attention import build_args
+    g = torch.Generator().manual_seed(d * 3 + splits)
+    lengths = [1, 40, 777, 0, 1500]
+    page, hkv, heads, width = 16, 2, 8, 128
+    cols = max((n + page - 1) // page for n in lengths) + 1
+    pool = len(lengths) * cols
+    table = torch.randperm(pool, generator=g).int().reshape(len(lengths), cols).to(device)
+    qdt = torch.float16 if dtype == torch.float16 else torch.bfloat16
+    kst = torch.full((pool, page, hkv, width), float("nan")).to(dtype).to(device)
+    vst = torch.full((pool, page, hkv, width), float("nan")).to(dtype).to(device)
+    kc, vc = kst[..., :d], vst[..., :d]
+    kc.copy_(torch.randn(pool, page, hkv, d, generator=g).to(dtype))
+    vc.copy_(torch.randn(pool, page, hkv, d, generator=g).to(dtype))
+    q = torch.randn(len(lengths), heads, d, generator=g).to(qdt).to(device)
+    cq = torch.arange(len(lengths) + 1, device=device, dtype=torch.int32)
+    used = torch.tensor(lengths, device=device, dtype=torch.int32)
+    ost = torch.full((len(lengths), heads, width), 7.0, device=device, dtype=torch.float32)
+    out = ost[..., :d]
+    desc = torch.tensor([[0.5, 0.25]], device=device).expand(len(lengths), 2) if dtype == torch.float8_e4m3fn else None
+    lse_buf = torch.empty(heads, len(lengths), device=device)
+    keep = []
+    args = build_args(q, kc, vc, out, lse_buf, cu_seqlens_q=cq, cu_seqlens_k=None, seqused_k=used, max_seqlen_q=1,
+                      max_seqlen_k=max(lengths), block_table=table, softmax_scale=None, causal=True,
+                      window_size=(-1, -1), alibi_slopes=None, softcap=0., s_aux=None, q_descale=None,
+                      k_descale=desc, v_descale=desc, mask_mod=None, aux_tensors=None, leftpad_k=None, keep=keep)
+    assert _lib.supported("fa_decode_supported", args)
+    actual, lse = decode_attention(q, kc, vc, cu_seqlens_q=cq, seqused_k=used, max_seqlen_k=max(lengths),
+                                   block_table=table, num_splits=splits, out=out, k_descale=desc, v_descale=desc)
+    expected, el = attention_reference(q, kc, vc, cq, used_k=used, block_table=table, k_descale=desc, v_descale=desc)
+    torch.testing.assert_close(actual.cpu().double(), expected, atol=2e-3 if qdt == torch.float16 else 1e-2, rtol=0)
+    torch.testing.assert_close(lse.cpu().double(), el, atol=1e-4, rtol=0)
+    assert torch.all(ost[..., d:] == 7.0)
