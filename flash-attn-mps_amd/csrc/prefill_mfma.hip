@@ -4,7 +4,7 @@
 // flash_attn_mps/kernels/attention_fast.metal:103-597) plus the DIFFKV head
 // dims and attention sinks of its tiled path (flash_attn_mps/kernels/
 // attention.metal:60-181): packed or paged K/V, GQA, lower-right causality,
-// optional softcap, a per-head sink logit that joins the softmax
+// optional softcap, left/right sliding windows, a per-head sink logit that joins the softmax
 // denominator only, fp32 softmax and natural-log LSE.  Head dims (Dqk, Dv)
 // in {(32,32), (64,64), (72,72), (80,80), (96,96), (128,128), (256,256),
 // (192,128)}; 32 and 72/80/96 run zero-padded in the 64 and 128 tiles.
@@ -42,6 +42,7 @@
 //   workgroups share K/V in their XCD's L2.
 #include "attn_common.h"
 
+#include <climits>
 #include <type_traits>
 
 namespace {
@@ -215,7 +216,10 @@ FA_DEV bool compact_item(const fa_attn_args& a, int slot, int xcd, int lane, int
 // the tensors' own (multiples of 8): the query's extra dims load as zero,
 // their K columns are never multiplied (K-steps past DQT are skipped, a half
 // step is masked), and extra output columns are not stored.
-template <typename T, int DQ, int DV, int W, int NB, int MINB, bool CAUSAL, bool CAP, int DQT = DQ, int DVT = DV>
+// WIN: sliding windows (a.window_left / a.window_right); without it they are
+// ignored and the window code folds away.
+template <typename T, int DQ, int DV, int W, int NB, int MINB, bool CAUSAL, bool CAP, bool WIN, int DQT = DQ,
+          int DVT = DV>
 __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_args a, const PrefillShape shp) {
   constexpr int BM = 32 * NB * W;              // query rows per workgroup
   constexpr int KST = DQ / 16;                 // k-steps of the QK^T MFMA
@@ -265,9 +269,18 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   const int q0 = qb * BM;
   if (q0 >= r.q_len) return;
   const int off = r.k_len - r.q_len;   // absolute position of query row i is i + off
+  // Row qa sees keys j with qa - WL <= j (WL >= 0), j <= qa (causal) or
+  // j <= qa + WR (WR >= 0, not causal), j < k_len (flash_attn_mps/kernels/
+  // attention.metal:29-45, window kind).  The workgroup's key range follows
+  // from its first and last rows.
+  const int WL = WIN ? a.window_left : -1, WR = (WIN && !CAUSAL) ? a.window_right : -1;
+  const int qa_first = q0 + off, qa_last = min(q0 + BM, r.q_len) - 1 + off;
   int kv_end = r.k_len;
-  if (CAUSAL) kv_end = min(kv_end, min(q0 + BM, r.q_len) - 1 + off + 1);
+  if (CAUSAL) kv_end = min(kv_end, qa_last + 1);
+  else if (WR >= 0) kv_end = min(kv_end, max(qa_last + WR + 1, 0));
+  const int kv_begin = WL >= 0 ? min(max(qa_first - WL, 0), max(kv_end, 0)) : 0;
   const int n_tiles = kv_end > 0 ? (kv_end + PF_BN - 1) / PF_BN : 0;
+  const int tile0 = kv_begin / PF_BN;   // first tile with a visible key
 
   // Q^T operands for the whole kernel: block nb, lane holds
   // Q[wq0 + 32 nb + l32][16 kk + 8 hh .. +8].
@@ -410,10 +423,15 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // The pipeline runs over 32-key stages: stage st is half st % 2 of tile
   // st / 2 (keys 32 st .. +32).
   const int n_stages = kv_end > 0 ? (kv_end + 31) / 32 : 0;
-  auto active = [&](int st) { return wave_rows && (!CAUSAL || st * 32 <= wave_qabs_hi); };
+  const int st0 = 2 * tile0;
+  // Keys some row of this wave sees: [wave_key_lo, wave_key_hi].
+  const int wave_key_lo = WL >= 0 ? wave_qabs_lo - WL : INT_MIN;
+  const int wave_key_hi = CAUSAL ? wave_qabs_hi : (WR >= 0 ? wave_qabs_hi + WR : INT_MAX);
+  auto active = [&](int st) { return wave_rows && st * 32 <= wave_key_hi && st * 32 + 31 >= wave_key_lo; };
   auto needs_mask = [&](int st) {
     const int t0 = st * 32;
-    return (t0 + 32 > r.k_len) || (CAUSAL && t0 + 31 > wave_qabs_lo);
+    return (t0 + 32 > r.k_len) || (CAUSAL && t0 + 31 > wave_qabs_lo) ||
+           (WL >= 0 && t0 < wave_qabs_hi - WL) || (WR >= 0 && t0 + 31 > wave_qabs_lo + WR);
   };
 
   // S^T of one stage: s[nb][i] = score of key 32 st + 16 (i >> 3) + 8 hh + (i & 7).
@@ -450,13 +468,16 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
       if constexpr (MASK) {
         // Key t0 + 16 (i >> 3) + 8 hh + (i & 7) is visible iff its offset
         // 16 (i >> 3) + (i & 7) (an inline constant) <= lim.
-        const int t0 = st * 32;
+        const int t0 = st * 32, qa = wq0 + 32 * nb + l32 + off;
         int lim = r.k_len - 1 - t0;
-        if (CAUSAL) lim = min(lim, wq0 + 32 * nb + l32 + off - t0);
+        if (CAUSAL) lim = min(lim, qa - t0);
+        else if (WR >= 0) lim = min(lim, qa + WR - t0);
         lim -= 8 * hh;
+        // ... and >= lo (left window).
+        const int lo = WL >= 0 ? qa - WL - t0 - 8 * hh : INT_MIN;
 #pragma unroll
         for (int i = 0; i < 16; ++i)
-          if (16 * (i >> 3) + (i & 7) > lim) s[nb][i] = -INFINITY;
+          if (16 * (i >> 3) + (i & 7) > lim || 16 * (i >> 3) + (i & 7) < lo) s[nb][i] = -INFINITY;
       }
       float mx = fmaxf(s[nb][0], s[nb][1]);
 #pragma unroll
@@ -557,46 +578,76 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // computed even when stage st+1 lies past this wave's causal range (its K
   // rows hold valid or stale finite data) and its phase A then commits
   // nothing.
+  // With windows, a wave inactive at st (left of its window) but active at
+  // st+1 only computes S(st+1).
   auto step_any = [&](int st, f32x16 (&sc)[NB], f32x16 (&sn)[NB], float (&f)[NB]) {
     tile_start(std::integral_constant<bool, false>(), st);
-    if (!active(st)) return;
-    const bool act_n = st + 1 < n_stages && active(st + 1);
-    rescale_o(f);
+    const bool act = active(st), act_n = st + 1 < n_stages && active(st + 1);
     u32x4 pop[NB][2];
-    phase_b(sc, pop);
-    qk(st + 1, sn);
-    pv(st, pop);
+    if constexpr (WIN) {
+      if (!act && !act_n) return;
+      if (act) {
+        rescale_o(f);
+        phase_b(sc, pop);
+      }
+      qk(st + 1, sn);
+      if (act) pv(st, pop);
+    } else {
+      if (!act) return;
+      rescale_o(f);
+      phase_b(sc, pop);
+      qk(st + 1, sn);
+      pv(st, pop);
+    }
     if (needs_mask(st + 1)) phase_a(std::integral_constant<bool, true>(), st + 1, sn, act_n, f);
     else phase_a(std::integral_constant<bool, false>(), st + 1, sn, act_n, f);
   };
   auto hot = [&](int st) { return st < n_stages && active(st) && !needs_mask(st); };
 
-  if (n_stages > 0) {
-    // Prologue: tile 0 and K(1) rows 0..31 in LDS; S(0) and its phase A.
+  if (st0 < n_stages) {
+    // Prologue: tile tile0 and K(tile0 + 1) rows 0..31 in LDS; S(st0) and
+    // its phase A.
     const std::integral_constant<bool, false> any_tile;
-    dma_k(any_tile, 0, 0, 0);
-    dma_k(any_tile, 0, 0, 1);
-    dma_v(any_tile, 0, 0);
-    if (n_tiles > 1) dma_k(any_tile, 1, 1, 0);
+    dma_k(any_tile, tile0, tile0 & 1, 0);
+    dma_k(any_tile, tile0, tile0 & 1, 1);
+    dma_v(any_tile, tile0, tile0 & 1);
+    if (tile0 + 1 < n_tiles) dma_k(any_tile, tile0 + 1, (tile0 + 1) & 1, 0);
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
     f32x16 sa[NB], sb[NB];
     float f[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) f[nb] = 1.0f;
-    if (active(0)) {
-      qk(0, sa);
-      phase_a(std::integral_constant<bool, true>(), 0, sa, true, f);
+    if (active(st0)) {
+      qk(st0, sa);
+      phase_a(std::integral_constant<bool, true>(), st0, sa, true, f);
     }
-    int st = 0;
-    if (active(0))
-      for (; hot(st + 1) && hot(st + 2) && dma_full(st >> 1); st += 2) {
-        step_hot(st, sa, sb, f);
-        step_hot(st + 1, sb, sa, f);
+    // Even stage st holds S in sa, odd in sb.  The unmasked two-stage loop
+    // runs first; with windows it is re-entered at even stages where this
+    // wave is active (its window may start after st0).
+    int st = st0;
+    if constexpr (WIN) {
+      while (st < n_stages) {
+        if (!(st & 1) && active(st))
+          for (; hot(st + 1) && hot(st + 2) && dma_full(st >> 1); st += 2) {
+            step_hot(st, sa, sb, f);
+            step_hot(st + 1, sb, sa, f);
+          }
+        if (st >= n_stages) break;
+        if (st & 1) step_any(st, sb, sa, f);
+        else step_any(st, sa, sb, f);
+        ++st;
       }
-    for (; st < n_stages; ++st) {
-      if (st & 1) step_any(st, sb, sa, f);
-      else step_any(st, sa, sb, f);
+    } else {
+      if (active(st))
+        for (; hot(st + 1) && hot(st + 2) && dma_full(st >> 1); st += 2) {
+          step_hot(st, sa, sb, f);
+          step_hot(st + 1, sb, sa, f);
+        }
+      for (; st < n_stages; ++st) {
+        if (st & 1) step_any(st, sb, sa, f);
+        else step_any(st, sa, sb, f);
+      }
     }
   }
 
@@ -658,10 +709,14 @@ struct PrefillChoice {
 };
 
 template <typename T, int DQ, int DV, bool CAUSAL, typename S, int DQT, int DVT>
-PrefillChoice pick_tile(bool cap) {
+PrefillChoice pick_tile(bool cap, bool win) {
   PrefillChoice c;
-  c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, true, DQT, DVT>
-               : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false, DQT, DVT>;
+  if (win)
+    c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, true, true, DQT, DVT>
+                 : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false, true, DQT, DVT>;
+  else
+    c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, true, false, DQT, DVT>
+                 : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false, false, DQT, DVT>;
   c.bm = 32 * S::NB * S::W;
   c.threads = 64 * S::W;
   c.lds = lds_bytes<DQ, DV>();
@@ -669,45 +724,48 @@ PrefillChoice pick_tile(bool cap) {
 }
 
 template <typename T, int DQ, int DV, bool CAUSAL, int DQT, int DVT>
-PrefillChoice pick_cap(bool cap, bool wide) {
+PrefillChoice pick_cap(bool cap, bool wide, bool win) {
   if constexpr (PrefillTileWide<DQ, DV>::exists) {
     static_assert(32 * PrefillTileWide<DQ, DV>::NB * PrefillTileWide<DQ, DV>::W ==
                       32 * PrefillTile<DQ, DV>::NB * PrefillTile<DQ, DV>::W,
                   "both tiles cover the same query rows per workgroup");
-    if (wide) return pick_tile<T, DQ, DV, CAUSAL, PrefillTileWide<DQ, DV>, DQT, DVT>(cap);
+    if (wide) return pick_tile<T, DQ, DV, CAUSAL, PrefillTileWide<DQ, DV>, DQT, DVT>(cap, win);
   }
-  return pick_tile<T, DQ, DV, CAUSAL, PrefillTile<DQ, DV>, DQT, DVT>(cap);
+  return pick_tile<T, DQ, DV, CAUSAL, PrefillTile<DQ, DV>, DQT, DVT>(cap, win);
 }
 
 // (DQ, DV) = the tile; (DQT, DVT) = the tensors' head dims padded into it.
 template <typename T, int DQ, int DV, int DQT = DQ, int DVT = DV>
-PrefillChoice pick(bool causal, bool cap, bool wide) {
-  return causal ? pick_cap<T, DQ, DV, true, DQT, DVT>(cap, wide) : pick_cap<T, DQ, DV, false, DQT, DVT>(cap, wide);
+PrefillChoice pick(bool causal, bool cap, bool wide, bool win) {
+  return causal ? pick_cap<T, DQ, DV, true, DQT, DVT>(cap, wide, win)
+                : pick_cap<T, DQ, DV, false, DQT, DVT>(cap, wide, win);
 }
 
 // Head dims of the reference's fast path (flash_attn_mps/_attention.py:149-158:
 // 32, 64, 72, 80, 96, 128, 256) plus DIFFKV 192/128; 32 runs in the 64-dim
 // tile and 72/80/96 in the 128-dim tile.
 template <typename T>
-PrefillChoice pick_dims(int64_t dq, int64_t dv, bool causal, bool cap, bool wide) {
+PrefillChoice pick_dims(int64_t dq, int64_t dv, bool causal, bool cap, bool wide, bool win) {
   if (dq != dv && !(dq == 192 && dv == 128)) return PrefillChoice{nullptr, 0, 0, 0};
   switch (dq) {
-    case 32: return pick<T, 64, 64, 32, 32>(causal, cap, wide);
-    case 64: return pick<T, 64, 64>(causal, cap, wide);
-    case 72: return pick<T, 128, 128, 72, 72>(causal, cap, wide);
-    case 80: return pick<T, 128, 128, 80, 80>(causal, cap, wide);
-    case 96: return pick<T, 128, 128, 96, 96>(causal, cap, wide);
-    case 128: return pick<T, 128, 128>(causal, cap, wide);
-    case 192: return pick<T, 192, 128>(causal, cap, wide);
-    case 256: return pick<T, 256, 256>(causal, cap, wide);
+    case 32: return pick<T, 64, 64, 32, 32>(causal, cap, wide, win);
+    case 64: return pick<T, 64, 64>(causal, cap, wide, win);
+    case 72: return pick<T, 128, 128, 72, 72>(causal, cap, wide, win);
+    case 80: return pick<T, 128, 128, 80, 80>(causal, cap, wide, win);
+    case 96: return pick<T, 128, 128, 96, 96>(causal, cap, wide, win);
+    case 128: return pick<T, 128, 128>(causal, cap, wide, win);
+    case 192: return pick<T, 192, 128>(causal, cap, wide, win);
+    case 256: return pick<T, 256, 256>(causal, cap, wide, win);
     default: return PrefillChoice{nullptr, 0, 0, 0};
   }
 }
 
 PrefillChoice select_prefill(const fa_attn_args& a, bool wide) {
   const bool causal = a.causal != 0, cap = a.softcap > 0.0f;
-  return a.q_dtype == FA_BF16 ? pick_dims<BF16T>(a.head_dim_qk, a.head_dim_v, causal, cap, wide)
-                              : pick_dims<F16T>(a.head_dim_qk, a.head_dim_v, causal, cap, wide);
+  // A right window bounds nothing under causality.
+  const bool win = a.window_left >= 0 || (!causal && a.window_right >= 0);
+  return a.q_dtype == FA_BF16 ? pick_dims<BF16T>(a.head_dim_qk, a.head_dim_v, causal, cap, wide, win)
+                              : pick_dims<F16T>(a.head_dim_qk, a.head_dim_v, causal, cap, wide, win);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -720,7 +778,7 @@ bool prefill_ok(const fa_attn_args& a) {
         (dq == 192 && dv == 128)))
     return false;
   if (a.leftpad_k || a.alibi || a.q_descale || a.k_descale || a.v_descale) return false;
-  if (a.mask_kind != 0 || a.causal_by_batch || a.window_left != -1 || a.window_right != -1) return false;
+  if (a.mask_kind != 0 || a.causal_by_batch || a.window_left < -1 || a.window_right < -1) return false;
   if (a.num_splits != 1) return false;
   if (a.q_stride[2] != 1 || a.k_stride[3] != 1 || a.v_stride[3] != 1 || a.out_stride[2] != 1) return false;
   if (!aligned16(a.q) || !aligned16(a.k) || !aligned16(a.v) || ((uintptr_t)a.out & 7u)) return false;

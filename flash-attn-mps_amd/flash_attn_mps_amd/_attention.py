@@ -120,7 +120,6 @@ def _fast_candidate(q, k, v, out, num_splits, deterministic, causal, window_size
             and q.dtype == k.dtype == v.dtype == out.dtype
             and q.dtype in (torch.float16, torch.bfloat16)
             and not isinstance(causal, torch.Tensor)
-            and tuple(window_size) == (-1, -1)
             and alibi_slopes is None
             and q_descale is None and k_descale is None and v_descale is None
             and mask_mod is None and leftpad_k is None)

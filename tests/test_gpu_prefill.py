@@ -337,3 +337,62 @@ def test_prefill_padded_dims_ignore_neighbouring_columns(device, d, paged):
     ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=True, **ref_kw)
     assert_north_star(out, lse, ref, ref_lse, torch.bfloat16)
     assert torch.isnan(ost[..., d:].float()).all(), "columns past the head dim were written"
+
+
+@pytest.mark.parametrize("window", [(0, -1), (1, -1), (31, -1), (64, -1), (100, -1), (700, -1)])
+def test_prefill_causal_left_window(device, window):
+    """Causal sliding window on the MFMA kernel: row qa sees keys
+    [qa - WL, qa]; workgroups skip tiles left of their rows' windows."""
+    q_lens, k_lens = [1, 37, 300, 64, 513, 1000], [5, 37, 300, 200, 700, 1000]
+    q, k, v, cuq, cuk = _case(device, torch.bfloat16, 128, 8, 2, q_lens, k_lens, scale=0.5, seed=window[0])
+    out, lse = attention(q, k, v, cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=max(q_lens),
+                         max_seqlen_k=max(k_lens), causal=True, window_size=window)
+    ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=True, window=window)
+    assert_reference_tol(out, lse, ref, ref_lse, torch.bfloat16)
+    many, start = [], 0
+    for n, m in zip(q_lens, k_lens):
+        many += [start + i for i in range(n) if min(m - n + i + 1, window[0] + 1) >= 32]
+        start += n
+    if many:
+        assert_north_star(out, lse, ref, ref_lse, torch.bfloat16, rows=torch.tensor(many))
+
+
+@pytest.mark.parametrize("window", [(-1, 0), (-1, 50), (40, 40), (200, -1), (0, 0), (3, 130)])
+@pytest.mark.parametrize("paged", [False, True])
+def test_prefill_two_sided_window(device, window, paged):
+    """Non-causal left/right windows (q_len != k_len, lower-right aligned),
+    packed and paged, with GQA and sinks."""
+    g = torch.Generator().manual_seed(window[0] * 7 + window[1] + paged)
+    hq, hkv, d, page = 8, 2, 64, 16
+    q_lens, k_lens = [3, 129, 260, 64], [40, 129, 300, 600]
+    q = (torch.randn(sum(q_lens), hq, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
+    sinks = torch.randn(hq, generator=g).to(device)
+    cuq = cu_from_lengths(q_lens, device)
+    if paged:
+        cols = max((n + page - 1) // page for n in k_lens)
+        table = torch.randperm(cols * len(k_lens), generator=g).int().reshape(len(k_lens), cols)
+        k = (torch.randn(cols * len(k_lens), page, hkv, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
+        v = torch.randn(cols * len(k_lens), page, hkv, d, generator=g).to(torch.bfloat16).to(device)
+        used = torch.tensor(k_lens, dtype=torch.int32, device=device)
+        out, lse = attention(q, k, v, cu_seqlens_q=cuq, seqused_k=used, block_table=table.to(device),
+                             max_seqlen_q=max(q_lens), max_seqlen_k=max(k_lens), window_size=window, s_aux=sinks)
+        ref, ref_lse = attention_reference(q, k, v, cuq, used_k=used, block_table=table, window=window,
+                                           sinks=sinks.cpu())
+    else:
+        k = (torch.randn(sum(k_lens), hkv, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
+        v = torch.randn(sum(k_lens), hkv, d, generator=g).to(torch.bfloat16).to(device)
+        cuk = cu_from_lengths(k_lens, device)
+        out, lse = attention(q, k, v, cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=max(q_lens),
+                             max_seqlen_k=max(k_lens), window_size=window, s_aux=sinks)
+        ref, ref_lse = attention_reference(q, k, v, cuq, cuk, window=window, sinks=sinks.cpu())
+    assert_reference_tol(out, lse, ref, ref_lse, torch.bfloat16)
+
+
+def test_prefill_window_route_is_mfma(device):
+    q, k, v, cuq, cuk = _case(device, torch.bfloat16, 128, 16, 8, [300, 17], [300, 17])
+    out = torch.empty_like(q)
+    lse = torch.empty(16, q.shape[0], device=device)
+    assert _uses_mfma(q, k, v, out, lse, cu_seqlens_q=cuq, cu_seqlens_k=cuk, seqused_k=None, max_seqlen_q=300,
+                      max_seqlen_k=300, block_table=None, softmax_scale=None, causal=True, window_size=(63, 0),
+                      alibi_slopes=None, softcap=0., s_aux=None, q_descale=None, k_descale=None, v_descale=None,
+                      mask_mod=None, aux_tensors=None, leftpad_k=None)
