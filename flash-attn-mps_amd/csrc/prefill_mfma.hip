@@ -86,6 +86,29 @@ template <> FA_DEV uint32_t pack2<F16T>(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// Two E4M3 codes (bytes 2 HI .. 2 HI + 1 of w) -> two T values, exactly.
+template <typename T, bool HI> FA_DEV uint32_t widen_fp8_pair(uint32_t w);
+template <> FA_DEV uint32_t widen_fp8_pair<BF16T, false>(uint32_t w) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
+}
+template <> FA_DEV uint32_t widen_fp8_pair<BF16T, true>(uint32_t w) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true));
+}
+template <> FA_DEV uint32_t widen_fp8_pair<F16T, false>(uint32_t w) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false));
+}
+template <> FA_DEV uint32_t widen_fp8_pair<F16T, true>(uint32_t w) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true));
+}
+// 16 E4M3 codes -> 16 T values (dims 0..7 in lo, 8..15 in hi).
+template <typename T>
+FA_DEV void widen_fp8_16(u32x4 w, u32x4& lo, u32x4& hi) {
+  lo = u32x4{widen_fp8_pair<T, false>(w[0]), widen_fp8_pair<T, true>(w[0]), widen_fp8_pair<T, false>(w[1]),
+             widen_fp8_pair<T, true>(w[1])};
+  hi = u32x4{widen_fp8_pair<T, false>(w[2]), widen_fp8_pair<T, true>(w[2]), widen_fp8_pair<T, false>(w[3]),
+             widen_fp8_pair<T, true>(w[3])};
+}
+
 // Swap bits 2 and 3 of a row index (an involution).
 FA_DEV int sigma(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 
@@ -218,9 +241,15 @@ FA_DEV bool compact_item(const fa_attn_args& a, int slot, int xcd, int lane, int
 // step is masked), and extra output columns are not stored.
 // WIN: sliding windows (a.window_left / a.window_right); without it they are
 // ignored and the window code folds away.
+// KT: K/V storage type, T or E4M3 (FP8 tiles are staged in LDS and widened
+// exactly to T there; k/v descales scale the scores and the output).
 template <typename T, int DQ, int DV, int W, int NB, int MINB, bool CAUSAL, bool CAP, bool WIN, int DQT = DQ,
-          int DVT = DV>
+          int DVT = DV, typename KT = T>
 __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_args a, const PrefillShape shp) {
+  constexpr bool FP8 = KT::id == FA_E4M3;
+  constexpr int KEB = KT::bytes;               // bytes per K/V element
+  static_assert(!FP8 || (DQT == DQ && DVT == DV && DQ == DV && (DQ == 64 || DQ == 128 || DQ == 256)),
+                "FP8 K/V tiles: 64/128/256-dim heads");
   constexpr int BM = 32 * NB * W;              // query rows per workgroup
   constexpr int KST = DQ / 16;                 // k-steps of the QK^T MFMA
   constexpr int KSTT = (DQT + 15) / 16;        // k-steps holding real dims
@@ -234,6 +263,9 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   extern __shared__ __attribute__((aligned(16))) char smem[];
   char* const kbuf0 = smem;
   char* const vbuf0 = smem + 2 * KTILE;
+  // FP8: one staging tile of raw K and V rows (64 x DQ and 64 x DV bytes).
+  char* const stk = smem + 2 * KTILE + 2 * VTILE;
+  char* const stv = stk + 64 * DQ;
 
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int wave_u = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index as a scalar
@@ -302,9 +334,17 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
 
   // Rows past the request's last key are never written by the DMA loads of
   // some hardware paths; zeroed V buffers keep p * v finite for them.
-  for (int i = tid; i < 2 * VTILE / 16; i += 64 * W) {
-    const u32x4 z = {0u, 0u, 0u, 0u};
-    *(u32x4*)(vbuf0 + 16 * i) = z;
+  // (FP8: the staging tile, whose rows are converted whole.)
+  if constexpr (FP8) {
+    for (int i = tid; i < 64 * (DQ + DV) / 16; i += 64 * W) {
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      *(u32x4*)(stk + 16 * i) = z;
+    }
+  } else {
+    for (int i = tid; i < 2 * VTILE / 16; i += 64 * W) {
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      *(u32x4*)(vbuf0 + 16 * i) = z;
+    }
   }
   __syncthreads();
 
@@ -324,10 +364,10 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   const int drow = 8 * (wave_u & 1) + (lane >> 3);   // row within its 16-key group
   const int kdoff = 2 * (int)(sigma(drow) * a.k_stride[1]) + (((lane & 7) ^ ((drow >> 1) & 7)) * 16);
   const int vdoff = 2 * (int)((lane >> 2) * a.v_stride[1]) + (lane & 3) * 16;
-  const char* const khead = (const char*)a.k + 2 * (int64_t)kh * a.k_stride[2];
-  const char* const vhead = (const char*)a.v + 2 * (int64_t)kh * a.v_stride[2];
-  const uint32_t krow_b = (uint32_t)(2 * a.k_stride[1]), vrow_b = (uint32_t)(2 * a.v_stride[1]);
-  const uint32_t kpage_b = (uint32_t)(2 * a.k_stride[0]), vpage_b = (uint32_t)(2 * a.v_stride[0]);
+  const char* const khead = (const char*)a.k + KEB * (int64_t)kh * a.k_stride[2];
+  const char* const vhead = (const char*)a.v + KEB * (int64_t)kh * a.v_stride[2];
+  const uint32_t krow_b = (uint32_t)(KEB * a.k_stride[1]), vrow_b = (uint32_t)(KEB * a.v_stride[1]);
+  const uint32_t kpage_b = (uint32_t)(KEB * a.k_stride[0]), vpage_b = (uint32_t)(KEB * a.v_stride[0]);
   const int32_t* const trow = paged ? a.block_table + b * a.bt_stride[0] : nullptr;
   const int bt1 = (int)a.bt_stride[1];
   const int pmask = (1 << lp) - 1;
@@ -352,7 +392,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   };
   // The same for a group known to hold 16 keys of the request: scalar
   // arithmetic only, size = 16 rows.
-  const int knrec = 15 * (int)krow_b + 2 * DQT, vnrec = 15 * (int)vrow_b + 2 * DVT;
+  const int knrec = 15 * (int)krow_b + KEB * DQT, vnrec = 15 * (int)vrow_b + KEB * DVT;
   auto full_rsrc = [&](const char* head, uint32_t row_b, uint32_t page_b, int key0, int nrec) {
     const char* g;
     if (paged) {
@@ -371,7 +411,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
       if ((rb >> 2) != half) continue;
       const int key0 = tile * PF_BN + 16 * (rb >> 1);
       const auto rsrc = decltype(full_tag)::value ? full_rsrc(khead, krow_b, kpage_b, key0, knrec)
-                                                  : group_rsrc(khead, krow_b, kpage_b, key0, 2 * DQT);
+                                                  : group_rsrc(khead, krow_b, kpage_b, key0, KEB * DQT);
       dma_columns<KG>(rsrc, kbuf0 + buf * KTILE + rb * 1024, kdoff);
     }
   };
@@ -382,8 +422,66 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
       if (gi >= 4) continue;
       const int key0 = tile * PF_BN + 16 * gi;
       const auto rsrc = decltype(full_tag)::value ? full_rsrc(vhead, vrow_b, vpage_b, key0, vnrec)
-                                                  : group_rsrc(vhead, vrow_b, vpage_b, key0, 2 * DVT);
+                                                  : group_rsrc(vhead, vrow_b, vpage_b, key0, KEB * DVT);
       dma_blocks<2 * VG>(rsrc, vbuf0 + buf * VTILE + gi * 1024, vdoff);
+    }
+  };
+  // FP8: whole tiles into the staging buffer, 1 KiB (1024 / D rows) per
+  // instruction; a wave's instructions n = w + W i each stay inside one
+  // 16-key group, at the same row offset within it.
+  constexpr int KR8 = 1024 / DQ, VR8 = 1024 / DV;   // rows per instruction
+  const int k8off = (((KR8 * wave_u) & 15) + lane / (DQ / 16)) * (int)krow_b + (lane % (DQ / 16)) * 16;
+  const int v8off = (((VR8 * wave_u) & 15) + lane / (DV / 16)) * (int)vrow_b + (lane % (DV / 16)) * 16;
+  auto dma_fp8 = [&](int tile) {
+#pragma unroll
+    for (int i = 0; i < 64 / KR8 / W; ++i) {
+      const int n = wave_u + W * i;
+      const auto rsrc = group_rsrc(khead, krow_b, kpage_b, tile * PF_BN + ((n * KR8) & ~15), DQ);
+      dma16<0>(rsrc, stk + n * 1024, k8off);
+    }
+#pragma unroll
+    for (int i = 0; i < 64 / VR8 / W; ++i) {
+      const int n = wave_u + W * i;
+      const auto rsrc = group_rsrc(vhead, vrow_b, vpage_b, tile * PF_BN + ((n * VR8) & ~15), DV);
+      dma16<0>(rsrc, stv + n * 1024, v8off);
+    }
+  };
+  // FP8: staging -> tile buffer buf in the 16-bit layouts above (K: key r
+  // at row sigma(r), swizzled 8-dim chunks; V: 32-dim blocks).  Thread t
+  // converts 16-byte chunks t + 64 W i; successive i advance by 1024 W / D
+  // rows (a multiple of 16, so sigma and the swizzle shift by constants).
+  // The addresses derive from an opaque copy of t so that none of them is
+  // held in registers across the main loop.
+  auto widen_tile = [&](int buf) {
+    int t = tid;
+    asm volatile("" : "+v"(t));
+    {
+      constexpr int CPR = DQ / 16, ROWS = 64 * W / CPR;
+      const int r = t / CPR, u = t % CPR, rho = sigma(r), sw = (rho >> 1) & 7, c0 = 2 * (u & 3);
+      char* const row = kbuf0 + buf * KTILE + (u >> 2) * PF_GROUP_BYTES + rho * 128;
+      char* const lo_p = row + (c0 ^ sw) * 16;
+      char* const hi_p = row + ((c0 + 1) ^ sw) * 16;
+      const char* const src = stk + 16 * t;
+#pragma unroll
+      for (int it = 0; it < 4 * DQ / (64 * W); ++it) {
+        u32x4 lo, hi;
+        widen_fp8_16<T>(*(const u32x4*)(src + 1024 * W * it), lo, hi);
+        *(u32x4*)(lo_p + ROWS * 128 * it) = lo;
+        *(u32x4*)(hi_p + ROWS * 128 * it) = hi;
+      }
+    }
+    {
+      constexpr int CPR = DV / 16, ROWS = 64 * W / CPR;
+      const int r = t / CPR, u = t % CPR;
+      char* const dst = vbuf0 + buf * VTILE + (u >> 1) * PF_VBLOCK_BYTES + r * 64 + 32 * (u & 1);
+      const char* const src = stv + 16 * t;
+#pragma unroll
+      for (int it = 0; it < 4 * DV / (64 * W); ++it) {
+        u32x4 lo, hi;
+        widen_fp8_16<T>(*(const u32x4*)(src + 1024 * W * it), lo, hi);
+        *(u32x4*)(dst + ROWS * 64 * it) = lo;
+        *(u32x4*)(dst + ROWS * 64 * it + 16) = hi;
+      }
     }
   };
 
@@ -400,8 +498,14 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   const int vg16 = lane >> 4, vi = lane & 15, va = vi & 3, vt = vi >> 2;
   const int vrd = (8 * (vg16 >> 1) + vt) * 64 + (4 * (vg16 & 1) + va) * 8;
 
-  const float c_scale = a.softmax_scale * LOG2E;          // raw dot -> log2 units
-  const float cap_in = CAP ? 2.0f * LOG2E * a.softmax_scale / a.softcap : 0.0f;
+  // Descales (per request and KV head, 1 when absent): score = scale *
+  // q_descale * k_descale * q.k, output * v_descale
+  // (flash_attn_mps/kernels/attention.metal:47-51, 170-180).
+  const float kdsc = descale_of(a.q_descale, a.q_descale_stride, b, kh) *
+                     descale_of(a.k_descale, a.k_descale_stride, b, kh);
+  const float vdsc = descale_of(a.v_descale, a.v_descale_stride, b, kh);
+  const float c_scale = a.softmax_scale * kdsc * LOG2E;   // raw dot -> log2 units
+  const float cap_in = CAP ? 2.0f * LOG2E * a.softmax_scale * kdsc / a.softcap : 0.0f;
   const float cap_out = a.softcap * LOG2E;
   // A sink logit seeds the running state (max = sink, sum = 1) of every row.
   const float sink2 = a.sinks ? a.sinks[(int64_t)h * a.sink_stride] * LOG2E : -INFINITY;
@@ -548,16 +652,26 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // 32..63 and K(j) rows 0..31; then V(j+1), K(j+1) rows 32..63 and K(j+2)
   // rows 0..31 are issued into the freed buffer halves.  With full_tag
   // true the caller guarantees that those tiles lie inside the request.
+  // FP8: the staging tile holds tile j+1; it is widened into buffer
+  // (j+1) & 1 (free since tile j-1 is done), then refilled with tile j+2.
   auto tile_start = [&](auto full_tag, int st) {
     if ((st & 1) == 0) {
       const int j = st >> 1;
       __builtin_amdgcn_s_waitcnt(0x0F70);
       __syncthreads();
-      if (j + 1 < n_tiles) {
-        dma_v(full_tag, j + 1, (j + 1) & 1);
-        dma_k(full_tag, j + 1, (j + 1) & 1, 1);
+      if constexpr (FP8) {
+        if (j + 1 < n_tiles) {
+          widen_tile((j + 1) & 1);
+          __syncthreads();
+          if (j + 2 < n_tiles) dma_fp8(j + 2);
+        }
+      } else {
+        if (j + 1 < n_tiles) {
+          dma_v(full_tag, j + 1, (j + 1) & 1);
+          dma_k(full_tag, j + 1, (j + 1) & 1, 1);
+        }
+        if (j + 2 < n_tiles) dma_k(full_tag, j + 2, j & 1, 0);
       }
-      if (j + 2 < n_tiles) dma_k(full_tag, j + 2, j & 1, 0);
     }
   };
   // Tiles j + 1 and (if it exists) j + 2 hold 64 keys of the request each.
@@ -608,12 +722,21 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     // Prologue: tile tile0 and K(tile0 + 1) rows 0..31 in LDS; S(st0) and
     // its phase A.
     const std::integral_constant<bool, false> any_tile;
-    dma_k(any_tile, tile0, tile0 & 1, 0);
-    dma_k(any_tile, tile0, tile0 & 1, 1);
-    dma_v(any_tile, tile0, tile0 & 1);
-    if (tile0 + 1 < n_tiles) dma_k(any_tile, tile0 + 1, (tile0 + 1) & 1, 0);
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    __syncthreads();
+    if constexpr (FP8) {
+      dma_fp8(tile0);
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      __syncthreads();
+      widen_tile(tile0 & 1);
+      __syncthreads();
+      if (tile0 + 1 < n_tiles) dma_fp8(tile0 + 1);
+    } else {
+      dma_k(any_tile, tile0, tile0 & 1, 0);
+      dma_k(any_tile, tile0, tile0 & 1, 1);
+      dma_v(any_tile, tile0, tile0 & 1);
+      if (tile0 + 1 < n_tiles) dma_k(any_tile, tile0 + 1, (tile0 + 1) & 1, 0);
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      __syncthreads();
+    }
     f32x16 sa[NB], sb[NB];
     float f[NB];
 #pragma unroll
@@ -657,7 +780,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     const float lt = sum_hh(l_run[nb]);
     const int row = wq0 + 32 * nb + l32;
     if (row < r.q_len) {
-      const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+      const float inv = lt > 0.0f ? vdsc / lt : 0.0f;
       const int64_t tq = (int64_t)r.q_begin + row;
       uint16_t* op = (uint16_t*)a.out + tq * a.out_stride[0] + (int64_t)h * a.out_stride[1] + 4 * hh;
 #pragma unroll
@@ -708,76 +831,92 @@ struct PrefillChoice {
   size_t lds;
 };
 
-template <typename T, int DQ, int DV, bool CAUSAL, typename S, int DQT, int DVT>
+template <typename T, int DQ, int DV, bool CAUSAL, typename S, int DQT, int DVT, typename KT>
 PrefillChoice pick_tile(bool cap, bool win) {
   PrefillChoice c;
   if (win)
-    c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, true, true, DQT, DVT>
-                 : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false, true, DQT, DVT>;
+    c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, true, true, DQT, DVT, KT>
+                 : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false, true, DQT, DVT, KT>;
   else
-    c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, true, false, DQT, DVT>
-                 : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false, false, DQT, DVT>;
+    c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, true, false, DQT, DVT, KT>
+                 : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false, false, DQT, DVT, KT>;
   c.bm = 32 * S::NB * S::W;
   c.threads = 64 * S::W;
-  c.lds = lds_bytes<DQ, DV>();
+  c.lds = lds_bytes<DQ, DV>() + (KT::id == FA_E4M3 ? 64 * (size_t)(DQ + DV) : 0);   // + FP8 staging tile
   return c;
 }
 
-template <typename T, int DQ, int DV, bool CAUSAL, int DQT, int DVT>
+template <typename T, int DQ, int DV, bool CAUSAL, int DQT, int DVT, typename KT>
 PrefillChoice pick_cap(bool cap, bool wide, bool win) {
   if constexpr (PrefillTileWide<DQ, DV>::exists) {
     static_assert(32 * PrefillTileWide<DQ, DV>::NB * PrefillTileWide<DQ, DV>::W ==
                       32 * PrefillTile<DQ, DV>::NB * PrefillTile<DQ, DV>::W,
                   "both tiles cover the same query rows per workgroup");
-    if (wide) return pick_tile<T, DQ, DV, CAUSAL, PrefillTileWide<DQ, DV>, DQT, DVT>(cap, win);
+    if (wide) return pick_tile<T, DQ, DV, CAUSAL, PrefillTileWide<DQ, DV>, DQT, DVT, KT>(cap, win);
   }
-  return pick_tile<T, DQ, DV, CAUSAL, PrefillTile<DQ, DV>, DQT, DVT>(cap, win);
+  return pick_tile<T, DQ, DV, CAUSAL, PrefillTile<DQ, DV>, DQT, DVT, KT>(cap, win);
 }
 
-// (DQ, DV) = the tile; (DQT, DVT) = the tensors' head dims padded into it.
-template <typename T, int DQ, int DV, int DQT = DQ, int DVT = DV>
+// (DQ, DV) = the tile; (DQT, DVT) = the tensors' head dims padded into it;
+// KT = the K/V storage type.
+template <typename T, typename KT, int DQ, int DV, int DQT = DQ, int DVT = DV>
 PrefillChoice pick(bool causal, bool cap, bool wide, bool win) {
-  return causal ? pick_cap<T, DQ, DV, true, DQT, DVT>(cap, wide, win)
-                : pick_cap<T, DQ, DV, false, DQT, DVT>(cap, wide, win);
+  return causal ? pick_cap<T, DQ, DV, true, DQT, DVT, KT>(cap, wide, win)
+                : pick_cap<T, DQ, DV, false, DQT, DVT, KT>(cap, wide, win);
 }
 
 // Head dims of the reference's fast path (flash_attn_mps/_attention.py:149-158:
 // 32, 64, 72, 80, 96, 128, 256) plus DIFFKV 192/128; 32 runs in the 64-dim
-// tile and 72/80/96 in the 128-dim tile.
+// tile and 72/80/96 in the 128-dim tile.  FP8 K/V: 64, 128, 256.
 template <typename T>
-PrefillChoice pick_dims(int64_t dq, int64_t dv, bool causal, bool cap, bool wide, bool win) {
+PrefillChoice pick_dims(int64_t dq, int64_t dv, bool causal, bool cap, bool wide, bool win, bool fp8) {
   if (dq != dv && !(dq == 192 && dv == 128)) return PrefillChoice{nullptr, 0, 0, 0};
+  if (fp8) {
+    if (dq != dv) return PrefillChoice{nullptr, 0, 0, 0};
+    switch (dq) {
+      case 64: return pick<T, E4M3T, 64, 64>(causal, cap, false, win);
+      case 128: return pick<T, E4M3T, 128, 128>(causal, cap, false, win);
+      case 256: return pick<T, E4M3T, 256, 256>(causal, cap, false, win);
+      default: return PrefillChoice{nullptr, 0, 0, 0};
+    }
+  }
   switch (dq) {
-    case 32: return pick<T, 64, 64, 32, 32>(causal, cap, wide, win);
-    case 64: return pick<T, 64, 64>(causal, cap, wide, win);
-    case 72: return pick<T, 128, 128, 72, 72>(causal, cap, wide, win);
-    case 80: return pick<T, 128, 128, 80, 80>(causal, cap, wide, win);
-    case 96: return pick<T, 128, 128, 96, 96>(causal, cap, wide, win);
-    case 128: return pick<T, 128, 128>(causal, cap, wide, win);
-    case 192: return pick<T, 192, 128>(causal, cap, wide, win);
-    case 256: return pick<T, 256, 256>(causal, cap, wide, win);
+    case 32: return pick<T, T, 64, 64, 32, 32>(causal, cap, wide, win);
+    case 64: return pick<T, T, 64, 64>(causal, cap, wide, win);
+    case 72: return pick<T, T, 128, 128, 72, 72>(causal, cap, wide, win);
+    case 80: return pick<T, T, 128, 128, 80, 80>(causal, cap, wide, win);
+    case 96: return pick<T, T, 128, 128, 96, 96>(causal, cap, wide, win);
+    case 128: return pick<T, T, 128, 128>(causal, cap, wide, win);
+    case 192: return pick<T, T, 192, 128>(causal, cap, wide, win);
+    case 256: return pick<T, T, 256, 256>(causal, cap, wide, win);
     default: return PrefillChoice{nullptr, 0, 0, 0};
   }
 }
 
 PrefillChoice select_prefill(const fa_attn_args& a, bool wide) {
-  const bool causal = a.causal != 0, cap = a.softcap > 0.0f;
+  const bool causal = a.causal != 0, cap = a.softcap > 0.0f, fp8 = a.k_dtype == FA_E4M3;
   // A right window bounds nothing under causality.
   const bool win = a.window_left >= 0 || (!causal && a.window_right >= 0);
-  return a.q_dtype == FA_BF16 ? pick_dims<BF16T>(a.head_dim_qk, a.head_dim_v, causal, cap, wide, win)
-                              : pick_dims<F16T>(a.head_dim_qk, a.head_dim_v, causal, cap, wide, win);
+  return a.q_dtype == FA_BF16 ? pick_dims<BF16T>(a.head_dim_qk, a.head_dim_v, causal, cap, wide, win, fp8)
+                              : pick_dims<F16T>(a.head_dim_qk, a.head_dim_v, causal, cap, wide, win, fp8);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 bool prefill_ok(const fa_attn_args& a) {
-  if (!(a.q_dtype == a.k_dtype && a.k_dtype == a.v_dtype && a.v_dtype == a.out_dtype)) return false;
   if (a.q_dtype != FA_BF16 && a.q_dtype != FA_F16) return false;
+  if (a.out_dtype != a.q_dtype || a.k_dtype != a.v_dtype) return false;
+  const bool fp8 = a.k_dtype == FA_E4M3;
+  if (!fp8 && a.k_dtype != a.q_dtype) return false;
   const int64_t dq = a.head_dim_qk, dv = a.head_dim_v;
-  if (!((dq == dv && (dq == 32 || dq == 64 || dq == 72 || dq == 80 || dq == 96 || dq == 128 || dq == 256)) ||
-        (dq == 192 && dv == 128)))
+  if (fp8) {
+    if (!(dq == dv && (dq == 64 || dq == 128 || dq == 256))) return false;
+  } else if (!((dq == dv && (dq == 32 || dq == 64 || dq == 72 || dq == 80 || dq == 96 || dq == 128 || dq == 256)) ||
+               (dq == 192 && dv == 128))) {
     return false;
-  if (a.leftpad_k || a.alibi || a.q_descale || a.k_descale || a.v_descale) return false;
+  }
+  if (a.leftpad_k || a.alibi) return false;
+  const int kb = fp8 ? 1 : 2;   // K/V bytes per element
   if (a.mask_kind != 0 || a.causal_by_batch || a.window_left < -1 || a.window_right < -1) return false;
   if (a.num_splits != 1) return false;
   if (a.q_stride[2] != 1 || a.k_stride[3] != 1 || a.v_stride[3] != 1 || a.out_stride[2] != 1) return false;
@@ -785,15 +924,15 @@ bool prefill_ok(const fa_attn_args& a) {
   for (int i = 0; i < 2; ++i)
     if ((a.q_stride[i] * 2) % 16 || (a.out_stride[i] * 2) % 8) return false;
   for (int i = a.page_size ? 0 : 1; i < 3; ++i)
-    if ((a.k_stride[i] * 2) % 16 || (a.v_stride[i] * 2) % 16) return false;
+    if ((a.k_stride[i] * kb) % 16 || (a.v_stride[i] * kb) % 16) return false;
   // Group-bounded buffer loads need non-overlapping rows and 16-row groups
   // that span less than 2 GiB.
   if (a.k_stride[1] < dq || a.v_stride[1] < dv) return false;
-  if (16 * a.k_stride[1] * 2 >= 0x7fffffffll || 16 * a.v_stride[1] * 2 >= 0x7fffffffll) return false;
+  if (16 * a.k_stride[1] * kb >= 0x7fffffffll || 16 * a.v_stride[1] * kb >= 0x7fffffffll) return false;
   if (a.page_size) {
     if (a.page_size < 16 || (a.page_size & (a.page_size - 1))) return false;
     // Page strides are 32-bit byte counts in the group descriptors.
-    if (2 * a.k_stride[0] >= (1ll << 32) || 2 * a.v_stride[0] >= (1ll << 32)) return false;
+    if (kb * a.k_stride[0] >= (1ll << 32) || kb * a.v_stride[0] >= (1ll << 32)) return false;
   }
   return true;
 }

@@ -117,11 +117,10 @@ def _fast_candidate(q, k, v, out, num_splits, deterministic, causal, window_size
                     s_aux, q_descale, k_descale, v_descale, mask_mod, leftpad_k):
     """Feature gate of the MFMA prefill route (kernel support is asked separately)."""
     return (not deterministic and num_splits in (0, 1)
-            and q.dtype == k.dtype == v.dtype == out.dtype
-            and q.dtype in (torch.float16, torch.bfloat16)
+            and q.dtype == out.dtype and q.dtype in (torch.float16, torch.bfloat16)
+            and k.dtype == v.dtype and k.dtype in (q.dtype, torch.float8_e4m3fn)
             and not isinstance(causal, torch.Tensor)
             and alibi_slopes is None
-            and q_descale is None and k_descale is None and v_descale is None
             and mask_mod is None and leftpad_k is None)
 
 

@@ -1,0 +1,203 @@
+"""MFMA prefill over FP8 (E4M3) K/V caches vs the fp64 oracle.
+
+The vLLM FP8 KV-cache contract (flash_attn_mps/vllm.py:35-70): bf16/fp16
+queries, E4M3 K/V (packed or paged), per-(request, KV head) descales,
+score = scale * q_descale * k_descale * q.k and output * v_descale
+(flash_attn_mps/kernels/attention.metal:47-51, 170-180).  The kernel widens
+the E4M3 codes to the query dtype exactly, so the bars are those of the
+16-bit path: max-abs <= 1e-2 bf16 / 2e-3 fp16, LSE <= 1e-4 (rows that see at
+least 32 keys; all rows within the reference's own tolerance).
+"""
+import pytest
+import torch
+
+from flash_attn_mps_amd import _lib, vllm
+from flash_attn_mps_amd._attention import attention, build_args
+from helpers import assert_north_star, assert_reference_tol, attention_reference, cu_from_lengths
+
+pytestmark = pytest.mark.gpu
+
+E4M3 = torch.float8_e4m3fn
+
+
+def _descales(g, batch, hkv, device, lo=0.02, hi=0.2):
+    return torch.empty(batch, hkv).uniform_(lo, hi, generator=g).to(device)
+
+
+def _quantize(x, scale_per_token_head):
+    """x / scale rounded to E4M3 (the cache holds codes, the descale restores)."""
+    return (x / scale_per_token_head).to(E4M3)
+
+
+def _rows_with_keys(q_lens, k_lens, minimum=32, window=-1):
+    rows, start = [], 0
+    for n, m in zip(q_lens, k_lens):
+        for i in range(n):
+            seen = m - n + i + 1
+            if window >= 0:
+                seen = min(seen, window + 1)
+            if seen >= minimum:
+                rows.append(start + i)
+        start += n
+    return torch.tensor(rows, dtype=torch.long)
+
+
+def _packed(device, dtype, d, hq, hkv, q_lens, k_lens, seed, qscale=0.5):
+    g = torch.Generator().manual_seed(seed)
+    b = len(q_lens)
+    ks, vs = _descales(g, b, hkv, device), _descales(g, b, hkv, device)
+    per_tok = lambda s, lens: torch.cat([s[i].cpu().expand(n, hkv) for i, n in enumerate(lens)])[..., None]
+    q = (torch.randn(sum(q_lens), hq, d, generator=g) * qscale).to(dtype).to(device)
+    k = _quantize(torch.randn(sum(k_lens), hkv, d, generator=g) * 0.5, per_tok(ks, k_lens)).to(device)
+    v = _quantize(torch.randn(sum(k_lens), hkv, d, generator=g), per_tok(vs, k_lens)).to(device)
+    return q, k, v, ks, vs, cu_from_lengths(q_lens, device), cu_from_lengths(k_lens, device)
+
+
+def _mfma_route(q, k, v, **kw):
+    keep = []
+    out = torch.empty(q.shape[0], q.shape[1], v.shape[-1], dtype=q.dtype, device=q.device)
+    lse = torch.empty(q.shape[1], q.shape[0], device=q.device)
+    full = dict(cu_seqlens_q=None, cu_seqlens_k=None, seqused_k=None, max_seqlen_q=1, max_seqlen_k=1,
+                block_table=None, softmax_scale=None, causal=False, window_size=(-1, -1), alibi_slopes=None,
+                softcap=0., s_aux=None, q_descale=None, k_descale=None, v_descale=None, mask_mod=None,
+                aux_tensors=None, leftpad_k=None)
+    full.update(kw)
+    return _lib.supported("fa_prefill_supported", build_args(q, k, v, out, lse, keep=keep, **full))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("causal", [True, False])
+def test_fp8_prefill_packed(device, dtype, d, causal):
+    q_lens, k_lens = [1, 37, 300, 64, 513], [5, 37, 300, 200, 700]
+    q, k, v, ks, vs, cuq, cuk = _packed(device, dtype, d, 8, 2, q_lens, k_lens, seed=d + causal)
+    kw = dict(cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=max(q_lens), max_seqlen_k=max(k_lens),
+              causal=causal, k_descale=ks, v_descale=vs)
+    assert _mfma_route(q, k, v, **kw)
+    out, lse = attention(q, k, v, **kw)
+    ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=causal, k_descale=ks, v_descale=vs)
+    assert_reference_tol(out, lse, ref, ref_lse, dtype)
+    rows = _rows_with_keys(q_lens, k_lens) if causal else None
+    assert_north_star(out, lse, ref, ref_lse, dtype, rows=rows)
+
+
+def test_fp8_prefill_q_descale_and_broadcast_strides(device):
+    """q_descale joins the score scale; descales expanded from [Hkv] (stride 0
+    over requests) and a transposed [B, Hkv] view read through their strides."""
+    q_lens, k_lens = [129, 256, 70], [300, 256, 1000]
+    q, k, v, _, _, cuq, cuk = _packed(device, torch.bfloat16, 128, 16, 4, q_lens, k_lens, seed=5)
+    g = torch.Generator().manual_seed(6)
+    qs = torch.empty(4).uniform_(0.5, 2.0, generator=g).to(device).expand(3, 4)
+    ks = torch.empty(4, 3).uniform_(0.02, 0.2, generator=g).to(device).t()
+    vs = torch.empty(4).uniform_(0.05, 0.1, generator=g).to(device).expand(3, 4)
+    out, lse = attention(q, k, v, cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=256, max_seqlen_k=1000,
+                         causal=True, q_descale=qs, k_descale=ks, v_descale=vs)
+    ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=True, q_descale=qs, k_descale=ks, v_descale=vs)
+    assert_north_star(out, lse, ref, ref_lse, torch.bfloat16, rows=_rows_with_keys(q_lens, k_lens))
+    assert_reference_tol(out, lse, ref, ref_lse, torch.bfloat16)
+
+
+def test_fp8_prefill_without_descales(device):
+    """Absent descales mean 1 (raw E4M3 values)."""
+    q_lens = [200, 64]
+    g = torch.Generator().manual_seed(8)
+    q = (torch.randn(sum(q_lens), 8, 128, generator=g) * 0.1).to(torch.float16).to(device)
+    k = (torch.randn(sum(q_lens), 8, 128, generator=g)).to(E4M3).to(device)
+    v = (torch.randn(sum(q_lens), 8, 128, generator=g)).to(E4M3).to(device)
+    cu = cu_from_lengths(q_lens, device)
+    out, lse = attention(q, k, v, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=200, max_seqlen_k=200, causal=True)
+    ref, ref_lse = attention_reference(q, k, v, cu, cu, causal=True)
+    assert_north_star(out, lse, ref, ref_lse, torch.float16, rows=_rows_with_keys(q_lens, q_lens))
+
+
+@pytest.mark.parametrize("page", [16, 256])
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_fp8_prefill_paged_poisoned_tail(device, page, d):
+    """Paged E4M3 caches through a permuted block table; every slot past a
+    request's length holds the E4M3 NaN code and must never be read."""
+    g = torch.Generator().manual_seed(page + d)
+    hq, hkv = 8, 2
+    q_lens, k_lens = [300, 33, 129, 1], [700, 33, 1029, 517]
+    cols = max((n + page - 1) // page for n in k_lens)
+    pool = cols * len(k_lens) + 2
+    table = torch.randperm(pool, generator=g)[:cols * len(k_lens)].int().reshape(len(k_lens), cols)
+    ks, vs = _descales(g, len(k_lens), hkv, "cpu"), _descales(g, len(k_lens), hkv, "cpu")
+    kc = torch.randn(pool, page, hkv, d, generator=g) * 0.5
+    vc = torch.randn(pool, page, hkv, d, generator=g)
+    kq = torch.full(kc.shape, float("nan")).to(E4M3)
+    vq = torch.full(vc.shape, float("nan")).to(E4M3)
+    for b, n in enumerate(k_lens):
+        for pos in range(n):
+            p, s = table[b, pos // page], pos % page
+            kq[p, s] = (kc[p, s] / ks[b][:, None]).to(E4M3)
+            vq[p, s] = (vc[p, s] / vs[b][:, None]).to(E4M3)
+    kq, vq = kq.to(device), vq.to(device)
+    ks, vs = ks.to(device), vs.to(device)
+    q = (torch.randn(sum(q_lens), hq, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
+    cuq = cu_from_lengths(q_lens, device)
+    used = torch.tensor(k_lens, dtype=torch.int32, device=device)
+    kw = dict(cu_seqlens_q=cuq, seqused_k=used, max_seqlen_q=max(q_lens), max_seqlen_k=cols * page,
+              block_table=table.to(device), causal=True, k_descale=ks, v_descale=vs)
+    assert _mfma_route(q, kq, vq, **kw)
+    out, lse = attention(q, kq, vq, **kw)
+    assert torch.isfinite(out).all()
+    ref, ref_lse = attention_reference(q, kq, vq, cuq, used_k=used, block_table=table, causal=True,
+                                       k_descale=ks, v_descale=vs)
+    assert_reference_tol(out, lse, ref, ref_lse, torch.bfloat16)
+    assert_north_star(out, lse, ref, ref_lse, torch.bfloat16, rows=_rows_with_keys(q_lens, k_lens))
+
+
+@pytest.mark.parametrize("window", [(-1, -1), (127, 0), (40, -1)])
+@pytest.mark.parametrize("cap", [0.0, 30.0])
+def test_fp8_prefill_softcap_window_sinks(device, window, cap):
+    q_lens, k_lens = [3, 129, 300, 64], [40, 129, 300, 600]
+    q, k, v, ks, vs, cuq, cuk = _packed(device, torch.bfloat16, 128, 8, 2, q_lens, k_lens, seed=int(cap) + window[0],
+                                        qscale=2.0)
+    sinks = torch.randn(8, generator=torch.Generator().manual_seed(3)).to(device)
+    kw = dict(cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=max(q_lens), max_seqlen_k=max(k_lens),
+              causal=True, window_size=window, softcap=cap, s_aux=sinks, k_descale=ks, v_descale=vs)
+    assert _mfma_route(q, k, v, **kw)
+    out, lse = attention(q, k, v, **kw)
+    ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=True, window=window, softcap=cap,
+                                       sinks=sinks.cpu(), k_descale=ks, v_descale=vs)
+    assert_reference_tol(out, lse, ref, ref_lse, torch.bfloat16)
+    assert_north_star(out, lse, ref, ref_lse, torch.bfloat16,
+                      rows=_rows_with_keys(q_lens, k_lens, window=window[0]))
+
+
+def test_fp8_vllm_mixed_batch_into_caller_out(device):
+    """Chunked prefill + decode over an FP8 paged cache through the vLLM
+    entry point, written into a caller-owned output."""
+    g = torch.Generator().manual_seed(77)
+    page, hq, hkv, d = 16, 16, 8, 128
+    q_lens = [1, 300, 1, 77, 1, 2]
+    k_lens = [900, 700, 4000, 77, 33, 2]
+    cols = max((n + page - 1) // page for n in k_lens)
+    pool = cols * len(k_lens)
+    table = torch.randperm(pool, generator=g).int().reshape(len(k_lens), cols).to(device)
+    scale = torch.empty(hkv).uniform_(0.02, 0.1, generator=g)
+    kc = (torch.randn(pool, page, hkv, d, generator=g) * 0.5 / scale[:, None]).to(E4M3).to(device)
+    vc = (torch.randn(pool, page, hkv, d, generator=g) / scale[:, None]).to(E4M3).to(device)
+    desc = scale.to(device).expand(len(k_lens), hkv)
+    q = (torch.randn(sum(q_lens), hq, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
+    cuq = cu_from_lengths(q_lens, device)
+    used = torch.tensor(k_lens, dtype=torch.int32, device=device)
+    out = torch.full((sum(q_lens), hq, d), float("nan"), dtype=torch.bfloat16, device=device)
+    vllm.flash_attn_varlen_func(q, kc, vc, max(q_lens), cuq, cols * page, seqused_k=used, block_table=table,
+                                causal=True, k_descale=desc, v_descale=desc, out=out)
+    ref, _ = attention_reference(q, kc, vc, cuq, used_k=used, block_table=table, causal=True,
+                                 k_descale=desc, v_descale=desc)
+    rows = _rows_with_keys(q_lens, k_lens)
+    err = (out.float().cpu()[rows] - ref.float()[rows]).abs().max().item()
+    assert err <= 1e-2, err
+
+
+def test_fp8_prefill_unsupported_dims_fall_back(device):
+    """E4M3 K/V with head dims outside 64/128/256 take the generic kernel."""
+    q, k, v, ks, vs, cuq, cuk = _packed(device, torch.bfloat16, 96, 4, 2, [70], [70], seed=1)
+    kw = dict(cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=70, max_seqlen_k=70, causal=True,
+              k_descale=ks, v_descale=vs)
+    assert not _mfma_route(q, k, v, **kw)
+    out, lse = attention(q, k, v, **kw)
+    ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=True, k_descale=ks, v_descale=vs)
+    assert_reference_tol(out, lse, ref, ref_lse, torch.bfloat16)
