@@ -61,7 +61,9 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 constexpr float PF_RESCALE = 8.0f;        // log2 headroom before the running max moves
 constexpr int PF_BN = 64;                 // keys per tile
 constexpr int PF_GROUP_BYTES = 64 * 128;  // one 64-dim column group of a K tile
-constexpr int PF_VBLOCK_BYTES = 64 * 64;  // one 32-dim block of a V tile
+constexpr int PF_VBLOCK_BYTES = 64 * 64;
+// K/V load modes of the main loop (see dma_k / dma_v).
+constexpr int PF_ANY_TILE = 0, PF_FULL_PACKED = 1, PF_FULL_PAGED = 2;  // one 32-dim block of a V tile
 
 template <typename T> FA_DEV f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c);
 template <> FA_DEV f32x16 mfma32<BF16T>(u32x4 a, u32x4 b, f32x16 c) {
@@ -391,11 +393,11 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     return __builtin_amdgcn_make_buffer_rsrc((void*)g, (short)0, bytes, 0x00020000);
   };
   // The same for a group known to hold 16 keys of the request: scalar
-  // arithmetic only, size = 16 rows.
+  // arithmetic only, size = 16 rows; pg (paged or not) is a compile-time tag.
   const int knrec = 15 * (int)krow_b + KEB * DQT, vnrec = 15 * (int)vrow_b + KEB * DVT;
-  auto full_rsrc = [&](const char* head, uint32_t row_b, uint32_t page_b, int key0, int nrec) {
+  auto full_rsrc = [&](auto pg, const char* head, uint32_t row_b, uint32_t page_b, int key0, int nrec) {
     const char* g;
-    if (paged) {
+    if constexpr (decltype(pg)::value) {
       const uint32_t blk = (uint32_t)load_invariant_i32(trow, (int64_t)(key0 >> lp) * bt1);
       g = head + (uint64_t)blk * page_b + (uint32_t)(key0 & pmask) * row_b;
     } else {
@@ -403,26 +405,32 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     }
     return __builtin_amdgcn_make_buffer_rsrc((void*)g, (short)0, nrec, 0x00020000);
   };
+  auto paged_tag = [](auto mode) { return std::integral_constant<bool, decltype(mode)::value == PF_FULL_PAGED>(); };
+  // Load modes (a compile-time tag): PF_ANY_TILE = any tile, per-group
+  // bounds; PF_FULL_PACKED / PF_FULL_PAGED = tiles known to hold 64 keys of
+  // the request, packed or paged K/V.
   // K rows 32 half .. +32 of a tile (row blocks 4 half .. +4).
-  auto dma_k = [&](auto full_tag, int tile, int buf, int half) {
+  auto dma_k = [&](auto mode, int tile, int buf, int half) {
 #pragma unroll
     for (int i = 0; i < 8 / W; ++i) {
       const int rb = wave_u + W * i;
       if ((rb >> 2) != half) continue;
       const int key0 = tile * PF_BN + 16 * (rb >> 1);
-      const auto rsrc = decltype(full_tag)::value ? full_rsrc(khead, krow_b, kpage_b, key0, knrec)
-                                                  : group_rsrc(khead, krow_b, kpage_b, key0, KEB * DQT);
+      const auto rsrc = decltype(mode)::value == PF_ANY_TILE
+                            ? group_rsrc(khead, krow_b, kpage_b, key0, KEB * DQT)
+                            : full_rsrc(paged_tag(mode), khead, krow_b, kpage_b, key0, knrec);
       dma_columns<KG>(rsrc, kbuf0 + buf * KTILE + rb * 1024, kdoff);
     }
   };
-  auto dma_v = [&](auto full_tag, int tile, int buf) {
+  auto dma_v = [&](auto mode, int tile, int buf) {
 #pragma unroll
     for (int i = 0; i < (4 + W - 1) / W; ++i) {
       const int gi = wave_u + W * i;
       if (gi >= 4) continue;
       const int key0 = tile * PF_BN + 16 * gi;
-      const auto rsrc = decltype(full_tag)::value ? full_rsrc(vhead, vrow_b, vpage_b, key0, vnrec)
-                                                  : group_rsrc(vhead, vrow_b, vpage_b, key0, KEB * DVT);
+      const auto rsrc = decltype(mode)::value == PF_ANY_TILE
+                            ? group_rsrc(vhead, vrow_b, vpage_b, key0, KEB * DVT)
+                            : full_rsrc(paged_tag(mode), vhead, vrow_b, vpage_b, key0, vnrec);
       dma_blocks<2 * VG>(rsrc, vbuf0 + buf * VTILE + gi * 1024, vdoff);
     }
   };
@@ -650,11 +658,11 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // DMAs and barrier, after which V(j), K(j) rows 32..63 and K(j+1) rows
   // 0..31 are resident and every wave is done with V(j-1), K(j-1) rows
   // 32..63 and K(j) rows 0..31; then V(j+1), K(j+1) rows 32..63 and K(j+2)
-  // rows 0..31 are issued into the freed buffer halves.  With full_tag
+  // rows 0..31 are issued into the freed buffer halves.  With a full mode
   // true the caller guarantees that those tiles lie inside the request.
   // FP8: the staging tile holds tile j+1; it is widened into buffer
   // (j+1) & 1 (free since tile j-1 is done), then refilled with tile j+2.
-  auto tile_start = [&](auto full_tag, int st) {
+  auto tile_start = [&](auto mode, int st) {
     if ((st & 1) == 0) {
       const int j = st >> 1;
       __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -667,10 +675,10 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
         }
       } else {
         if (j + 1 < n_tiles) {
-          dma_v(full_tag, j + 1, (j + 1) & 1);
-          dma_k(full_tag, j + 1, (j + 1) & 1, 1);
+          dma_v(mode, j + 1, (j + 1) & 1);
+          dma_k(mode, j + 1, (j + 1) & 1, 1);
         }
-        if (j + 2 < n_tiles) dma_k(full_tag, j + 2, j & 1, 0);
+        if (j + 2 < n_tiles) dma_k(mode, j + 2, j & 1, 0);
       }
     }
   };
@@ -679,8 +687,9 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // Steady state: stage st and st+1 both active, st+1 unmasked.  One
   // straight scheduling region: phase B(st) under the MFMAs of S(st+1),
   // phase A(st+1) under the MFMAs of P.V(st).
-  auto step_hot = [&](int st, f32x16 (&sc)[NB], f32x16 (&sn)[NB], float (&f)[NB]) {
-    tile_start(std::integral_constant<bool, true>(), st);
+  auto step_hot = [&](auto mode, int st, f32x16 (&sc)[NB], f32x16 (&sn)[NB], float (&f)[NB])
+                      __attribute__((always_inline)) {
+    tile_start(mode, st);
     rescale_o(f);
     u32x4 pop[NB][2];
     phase_b(sc, pop);
@@ -695,7 +704,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // With windows, a wave inactive at st (left of its window) but active at
   // st+1 only computes S(st+1).
   auto step_any = [&](int st, f32x16 (&sc)[NB], f32x16 (&sn)[NB], float (&f)[NB]) {
-    tile_start(std::integral_constant<bool, false>(), st);
+    tile_start(std::integral_constant<int, PF_ANY_TILE>(), st);
     const bool act = active(st), act_n = st + 1 < n_stages && active(st + 1);
     u32x4 pop[NB][2];
     if constexpr (WIN) {
@@ -721,7 +730,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   if (st0 < n_stages) {
     // Prologue: tile tile0 and K(tile0 + 1) rows 0..31 in LDS; S(st0) and
     // its phase A.
-    const std::integral_constant<bool, false> any_tile;
+    const std::integral_constant<int, PF_ANY_TILE> any_tile;
     if constexpr (FP8) {
       dma_fp8(tile0);
       __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -748,25 +757,45 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     // Even stage st holds S in sa, odd in sb.  The unmasked two-stage loop
     // runs first; with windows it is re-entered at even stages where this
     // wave is active (its window may start after st0).
+    // The hot loop is instantiated once per K/V layout (packed, paged).
     int st = st0;
     if constexpr (WIN) {
+      auto run_hot = [&](auto mode) {
+        for (; hot(st + 1) && hot(st + 2) && dma_full(st >> 1); st += 2) {
+          step_hot(mode, st, sa, sb, f);
+          step_hot(mode, st + 1, sb, sa, f);
+        }
+      };
       while (st < n_stages) {
-        if (!(st & 1) && active(st))
-          for (; hot(st + 1) && hot(st + 2) && dma_full(st >> 1); st += 2) {
-            step_hot(st, sa, sb, f);
-            step_hot(st + 1, sb, sa, f);
-          }
+        if (!(st & 1) && active(st)) {
+          if (paged) run_hot(std::integral_constant<int, PF_FULL_PAGED>());
+          else run_hot(std::integral_constant<int, PF_FULL_PACKED>());
+        }
         if (st >= n_stages) break;
         if (st & 1) step_any(st, sb, sa, f);
         else step_any(st, sa, sb, f);
         ++st;
       }
     } else {
-      if (active(st))
-        for (; hot(st + 1) && hot(st + 2) && dma_full(st >> 1); st += 2) {
-          step_hot(st, sa, sb, f);
-          step_hot(st + 1, sb, sa, f);
+      // Closed form of hot(st + 1) && hot(st + 2) && dma_full(st / 2) for
+      // even st >= st0 without windows: hot(s) <=> wave_rows && s < hb, and
+      // dma_full(j) <=> j <= jmax (both conditions are prefixes of the
+      // stage / tile range).
+      const int kf = r.k_len / PF_BN;
+      const int jmax = n_tiles <= kf ? kf - 2 : kf - 3;
+      int hb = min(n_stages, r.k_len / 32);
+      if constexpr (CAUSAL) hb = min(hb, max(wave_qabs_lo + 1, 0) / 32);
+      const int lim = wave_rows ? min(hb - 2, 2 * jmax + 1) : INT_MIN;
+      auto run_hot = [&](auto mode) {
+        for (; st < lim; st += 2) {
+          step_hot(mode, st, sa, sb, f);
+          step_hot(mode, st + 1, sb, sa, f);
         }
+      };
+      if (active(st)) {
+        if (paged) run_hot(std::integral_constant<int, PF_FULL_PAGED>());
+        else run_hot(std::integral_constant<int, PF_FULL_PACKED>());
+      }
       for (; st < n_stages; ++st) {
         if (st & 1) step_any(st, sb, sa, f);
         else step_any(st, sa, sb, f);
