@@ -1,0 +1,10 @@
+// BF16T prefill kernel variants, 16-bit K/V with head dims up to 128.
+#include "prefill_kernel.h"
+
+namespace fa_prefill {
+
+PrefillChoice pick_bf16_small(int64_t dq, int64_t dv, bool causal, bool cap, bool wide, bool win) {
+  return pick_dims_small<BF16T>(dq, dv, causal, cap, wide, win);
+}
+
+}  // namespace fa_prefill

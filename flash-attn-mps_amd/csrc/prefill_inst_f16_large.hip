@@ -1,0 +1,10 @@
+// F16T prefill kernel variants, head dims 192/128 and 256 and FP8 K/V.
+#include "prefill_kernel.h"
+
+namespace fa_prefill {
+
+PrefillChoice pick_f16_large(int64_t dq, int64_t dv, bool causal, bool cap, bool wide, bool win, bool fp8) {
+  return pick_dims_large<F16T>(dq, dv, causal, cap, wide, win, fp8);
+}
+
+}  // namespace fa_prefill

@@ -1,933 +1,23 @@
-// MFMA FlashAttention prefill for gfx950 (bf16 / fp16).
-//
-// Semantics follow the reference's fast path (flash_attn_mps/_attention.py:149-158,
-// flash_attn_mps/kernels/attention_fast.metal:103-597) plus the DIFFKV head
-// dims and attention sinks of its tiled path (flash_attn_mps/kernels/
-// attention.metal:60-181): packed or paged K/V, GQA, lower-right causality,
-// optional softcap, left/right sliding windows, a per-head sink logit that joins the softmax
-// denominator only, fp32 softmax and natural-log LSE.  Head dims (Dqk, Dv)
-// in {(32,32), (64,64), (72,72), (80,80), (96,96), (128,128), (256,256),
-// (192,128)}; 32 and 72/80/96 run zero-padded in the 64 and 128 tiles.
-//
-// gfx950 design
-// * A workgroup is W waves; each wave owns 32 query rows of one head.  K/V
-//   tiles of 64 keys live in LDS, two K and two V buffers.
-// * Tiles move global -> LDS with buffer_load ... lds (16 bytes a lane, one
-//   contiguous KiB per instruction): no registers, no VALU.  Every 16-key
-//   group gets a scalar buffer descriptor bounded at the request's last key,
-//   so rows past the end read as zero; lane offsets are loop-invariant.
-// * LDS layout.  K: 64-dim column groups of 64 rows x 128 bytes, the eight
-//   16-byte chunks of a row XOR-swizzled by (row / 2) % 8.  V: 32-dim blocks
-//   of 64 rows x 64 bytes, unswizzled: the eight rows {0..3, 8..11} (+4k)
-//   that one transpose read touches then cover the banks evenly.  Every
-//   operand read is bank-conflict free and addressed as a lane register plus
-//   an immediate.
-// * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16 (A =
-//   K rows from LDS, B = Q^T held in registers for the whole kernel).  A lane
-//   holds 32 keys of ONE query column, so the row max / sum are in-lane plus
-//   one v_permlane32_swap.  K rows are stored at sigma(r) (bits 2 and 3 of r
-//   swapped) so each lane's 8 consecutive accumulators are 8 consecutive
-//   keys: rounded to bf16/fp16 they are directly the B operand of
-//   O^T += V^T P^T.  The V^T operand is read from the row-major V tile with
-//   ds_read_b64_tr_b16 (two per MFMA).
-// * Software pipeline per wave over 32-key stages: while the MFMAs of
-//   S(s+1) = K(s+1) Q^T run, the VALU turns S(s) into P(s) (exp2, pack, row
-//   sums); while the MFMAs of O += V(s) P(s) run, the VALU takes the row max
-//   of S(s+1).  One barrier per 64-key tile; the next tiles' K and V are in
-//   flight meanwhile.
-// * exp2 with softmax_scale*log2(e) folded into one FMA; the running max only
-//   moves (and O is rescaled) when a tile raises it by more than 2^8.
-// * Work is ordered per XCD: each XCD runs whole (request, KV head) pairs one
-//   after another, query blocks heaviest-first within a pair, so resident
-//   workgroups share K/V in their XCD's L2.
-#include "attn_common.h"
-
-#include <climits>
-#include <type_traits>
+// Host side of the MFMA prefill: kernel selection, the support predicate and
+// the C-ABI entry points fa_prefill_supported / fa_prefill_fwd (replacing
+// the reference's `fast_attention` dispatch, flash_attn_mps/_attention.py:
+// 149-158, 170-238).  The kernel itself is in prefill_kernel.h; its variants
+// are instantiated in prefill_inst_*.hip.
+#include "prefill_kernel.h"
 
 namespace {
 
-typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
-typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
-typedef __attribute__((ext_vector_type(16))) float f32x16;
-typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
-typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
-typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
-typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
-typedef __attribute__((ext_vector_type(4))) short s16x4;
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-
-constexpr float PF_RESCALE = 8.0f;        // log2 headroom before the running max moves
-constexpr int PF_BN = 64;                 // keys per tile
-constexpr int PF_GROUP_BYTES = 64 * 128;  // one 64-dim column group of a K tile
-constexpr int PF_VBLOCK_BYTES = 64 * 64;
-// K/V load modes of the main loop (see dma_k / dma_v).
-constexpr int PF_ANY_TILE = 0, PF_FULL_PACKED = 1, PF_FULL_PAGED = 2;  // one 32-dim block of a V tile
-
-template <typename T> FA_DEV f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c);
-template <> FA_DEV f32x16 mfma32<BF16T>(u32x4 a, u32x4 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-}
-template <> FA_DEV f32x16 mfma32<F16T>(u32x4 a, u32x4 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-}
-
-// Two fp32 values -> one word of two 16-bit values (RNE).
-template <typename T> FA_DEV uint32_t pack2(float lo, float hi);
-template <> FA_DEV uint32_t pack2<BF16T>(float lo, float hi) {
-  bf16x2 v;
-  v[0] = (__bf16)lo;
-  v[1] = (__bf16)hi;
-  return __builtin_bit_cast(uint32_t, v);
-}
-template <> FA_DEV uint32_t pack2<F16T>(float lo, float hi) {
-  f16x2 v;
-  v[0] = (_Float16)lo;
-  v[1] = (_Float16)hi;
-  return __builtin_bit_cast(uint32_t, v);
-}
-
-// Two E4M3 codes (bytes 2 HI .. 2 HI + 1 of w) -> two T values, exactly.
-template <typename T, bool HI> FA_DEV uint32_t widen_fp8_pair(uint32_t w);
-template <> FA_DEV uint32_t widen_fp8_pair<BF16T, false>(uint32_t w) {
-  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
-}
-template <> FA_DEV uint32_t widen_fp8_pair<BF16T, true>(uint32_t w) {
-  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true));
-}
-template <> FA_DEV uint32_t widen_fp8_pair<F16T, false>(uint32_t w) {
-  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false));
-}
-template <> FA_DEV uint32_t widen_fp8_pair<F16T, true>(uint32_t w) {
-  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true));
-}
-// 16 E4M3 codes -> 16 T values (dims 0..7 in lo, 8..15 in hi).
-template <typename T>
-FA_DEV void widen_fp8_16(u32x4 w, u32x4& lo, u32x4& hi) {
-  lo = u32x4{widen_fp8_pair<T, false>(w[0]), widen_fp8_pair<T, true>(w[0]), widen_fp8_pair<T, false>(w[1]),
-             widen_fp8_pair<T, true>(w[1])};
-  hi = u32x4{widen_fp8_pair<T, false>(w[2]), widen_fp8_pair<T, true>(w[2]), widen_fp8_pair<T, false>(w[3]),
-             widen_fp8_pair<T, true>(w[3])};
-}
-
-// Swap bits 2 and 3 of a row index (an involution).
-FA_DEV int sigma(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
-
-// x combined with the value of lane ^ 32 (v_permlane32_swap exchanges the
-// wave halves; max / sum of the two results is symmetric in them).
-FA_DEV float max_hh(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-FA_DEV float sum_hh(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-// 16 bytes a lane from a buffer straight into LDS at lds + 16 * lane.  The
-// host compilation pass rejects this builtin (and would drop the kernel
-// stub without a diagnostic), so only the device pass sees the call.
-// IMM is added to both the global and the LDS address.
-template <int IMM>
-FA_DEV void dma16(__amdgpu_buffer_rsrc_t rsrc, char* lds, int voffset) {
-#if __HIP_DEVICE_COMPILE__
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(lds - IMM), 16, voffset, 0, IMM, 0);
-#endif
-}
-
-// One row block (8 rows x 128 bytes) of each of N column groups.
-template <int N, int I = 0>
-FA_DEV void dma_columns(__amdgpu_buffer_rsrc_t rsrc, char* lds, int voffset) {
-  if constexpr (I < N) {
-    dma16<128 * I>(rsrc, lds + I * PF_GROUP_BYTES, voffset);
-    dma_columns<N, I + 1>(rsrc, lds, voffset);
-  }
-}
-
-// One 16-key group (16 rows x 64 bytes) of each of N 32-dim blocks.
-template <int N, int I = 0>
-FA_DEV void dma_blocks(__amdgpu_buffer_rsrc_t rsrc, char* lds, int voffset) {
-  if constexpr (I < N) {
-    dma16<64 * I>(rsrc, lds + I * PF_VBLOCK_BYTES, voffset);
-    dma_blocks<N, I + 1>(rsrc, lds, voffset);
-  }
-}
-
-FA_DEV u32x4 lds_read16(const char* base, int off) { return *(const u32x4*)(base + off); }
-FA_DEV u32x2 lds_read_tr(const char* base, int off) {
-  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + off)));
-}
-
-// The request of rank `rank` when the batch (at most 64 requests) is ordered
-// by decreasing key count, ties by index.  Lane i ranks request i; every
-// wave computes the same answer.
-FA_DEV int64_t request_by_rank(const fa_attn_args& a, int64_t rank, int lane) {
-  const int n = (int)a.batch;
-  int len = -1;
-  if (lane < n) {
-    len = a.seqused_k ? a.seqused_k[lane * a.used_k_stride]
-                      : a.cu_seqlens_k[(lane + 1) * a.cu_k_stride] - a.cu_seqlens_k[lane * a.cu_k_stride];
-  }
-  int r = 0;
-  for (int j = 0; j < n; ++j) {
-    const int lj = __builtin_amdgcn_readlane(len, j);
-    r += (lj > len || (lj == len && j < lane)) ? 1 : 0;
-  }
-  const uint64_t hit = __ballot(lane < n && r == rank);
-  return (int64_t)__builtin_ctzll(hit);
-}
-
-struct PrefillShape {
-  int n_qblocks;
-  int log2_page;   // paged K/V: page size = 1 << log2_page
-  int compact;     // 1: workgroups map onto the compact work list
-};
-
-// One workgroup's share of the compact work list.  XCD x owns KV heads
-// x, x + 8, ... (Hkv a multiple of 8) of every request; requests come in
-// order of decreasing key count (ties by index), and request b contributes
-// m = Hkv / 8 KV heads x ceil(q_len / BM) query blocks x G query heads,
-// ordered KV head, then query block heaviest-first, then query head.  Slots
-// past the end of the list get no item.  Lane i evaluates request i (at
-// most 64 requests); every wave computes the same answer.
-struct WorkItem {
-  int64_t b;
-  int qb, kh, g;
-  RequestInfo r;
-};
-
-template <int BM>
-FA_DEV bool compact_item(const fa_attn_args& a, int slot, int xcd, int lane, int G, WorkItem& w) {
-  const int n = (int)a.batch;
-  int qbeg = 0, qlen = 0, klen = -1, kbase = 0;
-  if (lane < n) {
-    qbeg = a.cu_seqlens_q[lane * a.cu_q_stride];
-    qlen = a.cu_seqlens_q[(lane + 1) * a.cu_q_stride] - qbeg;
-    const int kc = a.cu_seqlens_k ? a.cu_seqlens_k[lane * a.cu_k_stride] : 0;
-    kbase = a.page_size ? 0 : kc;
-    klen = a.seqused_k ? a.seqused_k[lane * a.used_k_stride] : a.cu_seqlens_k[(lane + 1) * a.cu_k_stride] - kc;
-  }
-  const bool skip = (a.flags & FA_FLAG_SKIP_SINGLE_QUERY) && qlen == 1;   // the decode kernel owns it
-  const int nqb = (lane < n && !skip) ? (qlen + BM - 1) / BM : 0;
-  int before = 0;   // query blocks of the requests ranked ahead of this one
-  for (int j = 0; j < n; ++j) {
-    const int lj = __builtin_amdgcn_readlane(klen, j);
-    const int nj = __builtin_amdgcn_readlane(nqb, j);
-    before += (lj > klen || (lj == klen && j < lane)) ? nj : 0;
-  }
-  const int per_block = (int)(a.heads_k / 8) * G;
-  const int lo = before * per_block;
-  const uint64_t hit = __ballot(lane < n && slot >= lo && slot < lo + nqb * per_block);
-  if (hit == 0) return false;
-  const int i = __builtin_ctzll(hit);
-  const int nq = __builtin_amdgcn_readlane(nqb, i);
-  const int t = slot - __builtin_amdgcn_readlane(lo, i);
-  const int t2 = t % (nq * G);
-  w.b = i;
-  w.kh = xcd + 8 * (t / (nq * G));
-  w.qb = nq - 1 - t2 / G;
-  w.g = t2 % G;
-  w.r.q_begin = __builtin_amdgcn_readlane(qbeg, i);
-  w.r.q_len = __builtin_amdgcn_readlane(qlen, i);
-  w.r.k_len = __builtin_amdgcn_readlane(klen, i);
-  w.r.k_base = __builtin_amdgcn_readlane(kbase, i);
-  w.r.left = 0;
-  w.r.causal = a.causal != 0;
-  return true;
-}
-
-// DQ / DV are the tile's head dims (multiples of 64); DQT / DVT <= them are
-// the tensors' own (multiples of 8): the query's extra dims load as zero,
-// their K columns are never multiplied (K-steps past DQT are skipped, a half
-// step is masked), and extra output columns are not stored.
-// WIN: sliding windows (a.window_left / a.window_right); without it they are
-// ignored and the window code folds away.
-// KT: K/V storage type, T or E4M3 (FP8 tiles are staged in LDS and widened
-// exactly to T there; k/v descales scale the scores and the output).
-template <typename T, int DQ, int DV, int W, int NB, int MINB, bool CAUSAL, bool CAP, bool WIN, int DQT = DQ,
-          int DVT = DV, typename KT = T>
-__global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_args a, const PrefillShape shp) {
-  constexpr bool FP8 = KT::id == FA_E4M3;
-  constexpr int KEB = KT::bytes;               // bytes per K/V element
-  static_assert(!FP8 || (DQT == DQ && DVT == DV && DQ == DV && (DQ == 64 || DQ == 128 || DQ == 256)),
-                "FP8 K/V tiles: 64/128/256-dim heads");
-  constexpr int BM = 32 * NB * W;              // query rows per workgroup
-  constexpr int KST = DQ / 16;                 // k-steps of the QK^T MFMA
-  constexpr int KSTT = (DQT + 15) / 16;        // k-steps holding real dims
-  static_assert(DQT % 8 == 0 && DVT % 8 == 0 && DQT <= DQ && DVT <= DV, "true head dims");
-  constexpr int DB = DV / 32;                  // 32-dim blocks of O^T
-  constexpr int KG = DQ / 64, VG = DV / 64;    // 64-dim column groups (K), pairs of 32-dim blocks (V)
-  constexpr int KTILE = KG * PF_GROUP_BYTES, VTILE = VG * PF_GROUP_BYTES;
-  static_assert(DQ % 64 == 0 && DV % 64 == 0, "head dims are multiples of 64");
-  static_assert(W == 2 || W == 4 || W == 8, "wave count");
-
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  char* const kbuf0 = smem;
-  char* const vbuf0 = smem + 2 * KTILE;
-  // FP8: one staging tile of raw K and V rows (64 x DQ and 64 x DV bytes).
-  char* const stk = smem + 2 * KTILE + 2 * VTILE;
-  char* const stv = stk + 64 * DQ;
-
-  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-  const int wave_u = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index as a scalar
-  // Work order.  Workgroups are dispatched round-robin over the 8 XCDs
-  // (XCD = blockIdx % 8), each with its own L2, and every XCD works through
-  // whole (request, KV head) pairs one after another, query blocks
-  // heaviest-first, so the resident workgroups of an XCD share K/V in its L2.
-  // Requests come longest first (batches of up to 64), so the grid ends on
-  // the blocks of short requests rather than on the heavy blocks of a long
-  // one.  Compact mode launches only real work; otherwise XCD x takes the
-  // pairs p = x, x + 8, ... with n_qblocks slots each and skips the slots
-  // past a request's end.
-  const int G = (int)(a.heads_q / a.heads_k);
-  const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
-  WorkItem wi;
-  if (shp.compact) {
-    if (!compact_item<BM>(a, slot, xcd, lane, G, wi)) return;
-  } else {
-    const int per_pair = shp.n_qblocks * G;
-    const int64_t pair = (int64_t)(slot / per_pair) * 8 + xcd;
-    if (pair >= a.batch * a.heads_k) return;
-    const int rem = slot % per_pair;
-    wi.qb = shp.n_qblocks - 1 - rem / G;
-    wi.g = rem % G;
-    wi.b = a.batch > 1 && a.batch <= 64 ? request_by_rank(a, pair / a.heads_k, lane) : pair / a.heads_k;
-    wi.kh = (int)(pair % a.heads_k);
-    wi.r = load_request(a, wi.b);
-    if ((a.flags & FA_FLAG_SKIP_SINGLE_QUERY) && wi.r.q_len == 1) return;   // the decode kernel owns it
-  }
-  const int64_t b = wi.b;
-  const int qb = wi.qb, kh = wi.kh, h = kh * G + wi.g;
-  const RequestInfo r = wi.r;
-  const int q0 = qb * BM;
-  if (q0 >= r.q_len) return;
-  const int off = r.k_len - r.q_len;   // absolute position of query row i is i + off
-  // Row qa sees keys j with qa - WL <= j (WL >= 0), j <= qa (causal) or
-  // j <= qa + WR (WR >= 0, not causal), j < k_len (flash_attn_mps/kernels/
-  // attention.metal:29-45, window kind).  The workgroup's key range follows
-  // from its first and last rows.
-  const int WL = WIN ? a.window_left : -1, WR = (WIN && !CAUSAL) ? a.window_right : -1;
-  const int qa_first = q0 + off, qa_last = min(q0 + BM, r.q_len) - 1 + off;
-  int kv_end = r.k_len;
-  if (CAUSAL) kv_end = min(kv_end, qa_last + 1);
-  else if (WR >= 0) kv_end = min(kv_end, max(qa_last + WR + 1, 0));
-  const int kv_begin = WL >= 0 ? min(max(qa_first - WL, 0), max(kv_end, 0)) : 0;
-  const int n_tiles = kv_end > 0 ? (kv_end + PF_BN - 1) / PF_BN : 0;
-  const int tile0 = kv_begin / PF_BN;   // first tile with a visible key
-
-  // Q^T operands for the whole kernel: block nb, lane holds
-  // Q[wq0 + 32 nb + l32][16 kk + 8 hh .. +8].
-  const int wq0 = q0 + wave_u * 32 * NB;
-  u32x4 qop[NB][KST];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int row = wq0 + 32 * nb + l32;
-    const bool ok = row < r.q_len;
-    const uint16_t* qp = (const uint16_t*)a.q + ((int64_t)r.q_begin + row) * a.q_stride[0] +
-                         (int64_t)h * a.q_stride[1] + 8 * hh;
-#pragma unroll
-    for (int kk = 0; kk < KST; ++kk) {
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (ok && 16 * kk + 8 * hh + 8 <= DQT) v = *(const u32x4*)(qp + 16 * kk);
-      qop[nb][kk] = v;
-    }
-  }
-
-  // Rows past the request's last key are never written by the DMA loads of
-  // some hardware paths; zeroed V buffers keep p * v finite for them.
-  // (FP8: the staging tile, whose rows are converted whole.)
-  if constexpr (FP8) {
-    for (int i = tid; i < 64 * (DQ + DV) / 16; i += 64 * W) {
-      const u32x4 z = {0u, 0u, 0u, 0u};
-      *(u32x4*)(stk + 16 * i) = z;
-    }
-  } else {
-    for (int i = tid; i < 2 * VTILE / 16; i += 64 * W) {
-      const u32x4 z = {0u, 0u, 0u, 0u};
-      *(u32x4*)(vbuf0 + 16 * i) = z;
-    }
-  }
-  __syncthreads();
-
-  // ---- DMA addressing.  A tile is 8 row blocks (8 rows each) per column
-  // group; one instruction moves one row block of one column group.  Lane p
-  // fills LDS row 8 rb + p / 8, 16-byte slot p % 8, which holds chunk
-  // (p % 8) ^ ((row / 2) % 8) of that row; K rows hold key sigma(row).
-  // Offsets are relative to the first key of the row's 16-key group, whose
-  // address the per-group descriptor carries.  Wave w owns K row blocks
-  // rb = w + W i: all have rb % 2 = w % 2, so one lane offset serves them all
-  // and the column group is an immediate.  V: one instruction moves one
-  // 16-key group of one 32-dim block (16 rows x 64 bytes, lane p -> row
-  // p / 4, chunk p % 4); wave w owns the groups w + W i, the block is an
-  // immediate.
-  const bool paged = a.page_size != 0;
-  const int lp = shp.log2_page;
-  const int drow = 8 * (wave_u & 1) + (lane >> 3);   // row within its 16-key group
-  const int kdoff = 2 * (int)(sigma(drow) * a.k_stride[1]) + (((lane & 7) ^ ((drow >> 1) & 7)) * 16);
-  const int vdoff = 2 * (int)((lane >> 2) * a.v_stride[1]) + (lane & 3) * 16;
-  const char* const khead = (const char*)a.k + KEB * (int64_t)kh * a.k_stride[2];
-  const char* const vhead = (const char*)a.v + KEB * (int64_t)kh * a.v_stride[2];
-  const uint32_t krow_b = (uint32_t)(KEB * a.k_stride[1]), vrow_b = (uint32_t)(KEB * a.v_stride[1]);
-  const uint32_t kpage_b = (uint32_t)(KEB * a.k_stride[0]), vpage_b = (uint32_t)(KEB * a.v_stride[0]);
-  const int32_t* const trow = paged ? a.block_table + b * a.bt_stride[0] : nullptr;
-  const int bt1 = (int)a.bt_stride[1];
-  const int pmask = (1 << lp) - 1;
-  // Descriptor of the 16-key group starting at key0: base = that key's row,
-  // size ends at the request's last key (0 bytes for groups past it).
-  auto group_rsrc = [&](const char* head, uint32_t row_b, uint32_t page_b, int key0, int row_bytes) {
-    const int nvalid = min(max(r.k_len - key0, 0), 16);
-    const char* g = head;
-    if (nvalid > 0) {
-      if (paged) {
-        const uint32_t blk = (uint32_t)load_invariant_i32(trow, (int64_t)(key0 >> lp) * bt1);
-        g = head + (uint64_t)blk * page_b + (uint32_t)(key0 & pmask) * row_b;
-      } else {
-        g = head + (uint64_t)(uint32_t)(r.k_base + key0) * row_b;
-      }
-    }
-    // readfirstlane keeps the (uniform) size in an SGPR: a VGPR-held
-    // descriptor field would make the compiler wrap each load in a loop over
-    // distinct descriptors.
-    const int bytes = __builtin_amdgcn_readfirstlane(nvalid > 0 ? (nvalid - 1) * (int)row_b + row_bytes : 0);
-    return __builtin_amdgcn_make_buffer_rsrc((void*)g, (short)0, bytes, 0x00020000);
-  };
-  // The same for a group known to hold 16 keys of the request: scalar
-  // arithmetic only, size = 16 rows; pg (paged or not) is a compile-time tag.
-  const int knrec = 15 * (int)krow_b + KEB * DQT, vnrec = 15 * (int)vrow_b + KEB * DVT;
-  auto full_rsrc = [&](auto pg, const char* head, uint32_t row_b, uint32_t page_b, int key0, int nrec) {
-    const char* g;
-    if constexpr (decltype(pg)::value) {
-      const uint32_t blk = (uint32_t)load_invariant_i32(trow, (int64_t)(key0 >> lp) * bt1);
-      g = head + (uint64_t)blk * page_b + (uint32_t)(key0 & pmask) * row_b;
-    } else {
-      g = head + (uint64_t)(uint32_t)(r.k_base + key0) * row_b;
-    }
-    return __builtin_amdgcn_make_buffer_rsrc((void*)g, (short)0, nrec, 0x00020000);
-  };
-  auto paged_tag = [](auto mode) { return std::integral_constant<bool, decltype(mode)::value == PF_FULL_PAGED>(); };
-  // Load modes (a compile-time tag): PF_ANY_TILE = any tile, per-group
-  // bounds; PF_FULL_PACKED / PF_FULL_PAGED = tiles known to hold 64 keys of
-  // the request, packed or paged K/V.
-  // K rows 32 half .. +32 of a tile (row blocks 4 half .. +4).
-  auto dma_k = [&](auto mode, int tile, int buf, int half) {
-#pragma unroll
-    for (int i = 0; i < 8 / W; ++i) {
-      const int rb = wave_u + W * i;
-      if ((rb >> 2) != half) continue;
-      const int key0 = tile * PF_BN + 16 * (rb >> 1);
-      const auto rsrc = decltype(mode)::value == PF_ANY_TILE
-                            ? group_rsrc(khead, krow_b, kpage_b, key0, KEB * DQT)
-                            : full_rsrc(paged_tag(mode), khead, krow_b, kpage_b, key0, knrec);
-      dma_columns<KG>(rsrc, kbuf0 + buf * KTILE + rb * 1024, kdoff);
-    }
-  };
-  auto dma_v = [&](auto mode, int tile, int buf) {
-#pragma unroll
-    for (int i = 0; i < (4 + W - 1) / W; ++i) {
-      const int gi = wave_u + W * i;
-      if (gi >= 4) continue;
-      const int key0 = tile * PF_BN + 16 * gi;
-      const auto rsrc = decltype(mode)::value == PF_ANY_TILE
-                            ? group_rsrc(vhead, vrow_b, vpage_b, key0, KEB * DVT)
-                            : full_rsrc(paged_tag(mode), vhead, vrow_b, vpage_b, key0, vnrec);
-      dma_blocks<2 * VG>(rsrc, vbuf0 + buf * VTILE + gi * 1024, vdoff);
-    }
-  };
-  // FP8: whole tiles into the staging buffer, 1 KiB (1024 / D rows) per
-  // instruction; a wave's instructions n = w + W i each stay inside one
-  // 16-key group, at the same row offset within it.
-  constexpr int KR8 = 1024 / DQ, VR8 = 1024 / DV;   // rows per instruction
-  const int k8off = (((KR8 * wave_u) & 15) + lane / (DQ / 16)) * (int)krow_b + (lane % (DQ / 16)) * 16;
-  const int v8off = (((VR8 * wave_u) & 15) + lane / (DV / 16)) * (int)vrow_b + (lane % (DV / 16)) * 16;
-  auto dma_fp8 = [&](int tile) {
-#pragma unroll
-    for (int i = 0; i < 64 / KR8 / W; ++i) {
-      const int n = wave_u + W * i;
-      const auto rsrc = group_rsrc(khead, krow_b, kpage_b, tile * PF_BN + ((n * KR8) & ~15), DQ);
-      dma16<0>(rsrc, stk + n * 1024, k8off);
-    }
-#pragma unroll
-    for (int i = 0; i < 64 / VR8 / W; ++i) {
-      const int n = wave_u + W * i;
-      const auto rsrc = group_rsrc(vhead, vrow_b, vpage_b, tile * PF_BN + ((n * VR8) & ~15), DV);
-      dma16<0>(rsrc, stv + n * 1024, v8off);
-    }
-  };
-  // FP8: staging -> tile buffer buf in the 16-bit layouts above (K: key r
-  // at row sigma(r), swizzled 8-dim chunks; V: 32-dim blocks).  Thread t
-  // converts 16-byte chunks t + 64 W i; successive i advance by 1024 W / D
-  // rows (a multiple of 16, so sigma and the swizzle shift by constants).
-  // The addresses derive from an opaque copy of t so that none of them is
-  // held in registers across the main loop.
-  auto widen_tile = [&](int buf) {
-    int t = tid;
-    asm volatile("" : "+v"(t));
-    {
-      constexpr int CPR = DQ / 16, ROWS = 64 * W / CPR;
-      const int r = t / CPR, u = t % CPR, rho = sigma(r), sw = (rho >> 1) & 7, c0 = 2 * (u & 3);
-      char* const row = kbuf0 + buf * KTILE + (u >> 2) * PF_GROUP_BYTES + rho * 128;
-      char* const lo_p = row + (c0 ^ sw) * 16;
-      char* const hi_p = row + ((c0 + 1) ^ sw) * 16;
-      const char* const src = stk + 16 * t;
-#pragma unroll
-      for (int it = 0; it < 4 * DQ / (64 * W); ++it) {
-        u32x4 lo, hi;
-        widen_fp8_16<T>(*(const u32x4*)(src + 1024 * W * it), lo, hi);
-        *(u32x4*)(lo_p + ROWS * 128 * it) = lo;
-        *(u32x4*)(hi_p + ROWS * 128 * it) = hi;
-      }
-    }
-    {
-      constexpr int CPR = DV / 16, ROWS = 64 * W / CPR;
-      const int r = t / CPR, u = t % CPR;
-      char* const dst = vbuf0 + buf * VTILE + (u >> 1) * PF_VBLOCK_BYTES + r * 64 + 32 * (u & 1);
-      const char* const src = stv + 16 * t;
-#pragma unroll
-      for (int it = 0; it < 4 * DV / (64 * W); ++it) {
-        u32x4 lo, hi;
-        widen_fp8_16<T>(*(const u32x4*)(src + 1024 * W * it), lo, hi);
-        *(u32x4*)(dst + ROWS * 64 * it) = lo;
-        *(u32x4*)(dst + ROWS * 64 * it + 16) = hi;
-      }
-    }
-  };
-
-  // ---- Operand read offsets (bytes within a tile buffer).
-  // K (A of S^T): LDS row 32 (st % 2) + l32, chunk 2 kk + hh -> column group
-  // kk / 4, slot (2 (kk % 4) + hh) ^ ((l32 / 2) % 8); kk / 4 is an immediate.
-  int krd[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) krd[s] = l32 * 128 + (((2 * s + hh) ^ ((l32 >> 1) & 7)) * 16);
-  // V^T (A of O^T) through ds_read_b64_tr_b16: in each 16-lane group g, lane
-  // i = a + 4 t' reads row 8 (g / 2) + t' (+ 32 (st % 2) + 16 c + 4 t) of
-  // block db at dims 16 (g % 2) + 4 a .. +4; the hardware hands lane 4 a + e
-  // dim 4 a + e of those four rows, i.e. four consecutive keys of one dim.
-  const int vg16 = lane >> 4, vi = lane & 15, va = vi & 3, vt = vi >> 2;
-  const int vrd = (8 * (vg16 >> 1) + vt) * 64 + (4 * (vg16 & 1) + va) * 8;
-
-  // Descales (per request and KV head, 1 when absent): score = scale *
-  // q_descale * k_descale * q.k, output * v_descale
-  // (flash_attn_mps/kernels/attention.metal:47-51, 170-180).
-  const float kdsc = descale_of(a.q_descale, a.q_descale_stride, b, kh) *
-                     descale_of(a.k_descale, a.k_descale_stride, b, kh);
-  const float vdsc = descale_of(a.v_descale, a.v_descale_stride, b, kh);
-  const float c_scale = a.softmax_scale * kdsc * LOG2E;   // raw dot -> log2 units
-  const float cap_in = CAP ? 2.0f * LOG2E * a.softmax_scale * kdsc / a.softcap : 0.0f;
-  const float cap_out = a.softcap * LOG2E;
-  // A sink logit seeds the running state (max = sink, sum = 1) of every row.
-  const float sink2 = a.sinks ? a.sinks[(int64_t)h * a.sink_stride] * LOG2E : -INFINITY;
-  float m_run[NB], l_run[NB];
-  f32x16 o[NB][DB];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    m_run[nb] = sink2;
-    l_run[nb] = (a.sinks && hh == 0) ? 1.0f : 0.0f;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) o[nb][db][i] = 0.0f;
-  }
-
-  const bool wave_rows = wq0 < r.q_len;
-  const int wave_qabs_lo = wq0 + off;
-  const int wave_qabs_hi = min(wq0 + 32 * NB, r.q_len) - 1 + off;
-  // The pipeline runs over 32-key stages: stage st is half st % 2 of tile
-  // st / 2 (keys 32 st .. +32).
-  const int n_stages = kv_end > 0 ? (kv_end + 31) / 32 : 0;
-  const int st0 = 2 * tile0;
-  // Keys some row of this wave sees: [wave_key_lo, wave_key_hi].
-  const int wave_key_lo = WL >= 0 ? wave_qabs_lo - WL : INT_MIN;
-  const int wave_key_hi = CAUSAL ? wave_qabs_hi : (WR >= 0 ? wave_qabs_hi + WR : INT_MAX);
-  auto active = [&](int st) { return wave_rows && st * 32 <= wave_key_hi && st * 32 + 31 >= wave_key_lo; };
-  auto needs_mask = [&](int st) {
-    const int t0 = st * 32;
-    return (t0 + 32 > r.k_len) || (CAUSAL && t0 + 31 > wave_qabs_lo) ||
-           (WL >= 0 && t0 < wave_qabs_hi - WL) || (WR >= 0 && t0 + 31 > wave_qabs_lo + WR);
-  };
-
-  // S^T of one stage: s[nb][i] = score of key 32 st + 16 (i >> 3) + 8 hh + (i & 7).
-  auto qk = [&](int st, f32x16 (&s)[NB]) {
-    const char* kl = kbuf0 + ((st >> 1) & 1) * KTILE + (st & 1) * 32 * 128;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[nb][i] = 0.0f;
-#pragma unroll
-    for (int kk = 0; kk < KSTT; ++kk) {
-      u32x4 av = lds_read16(kl, krd[kk % 4] + (kk / 4) * PF_GROUP_BYTES);
-      if constexpr (DQT % 16 == 8) {
-        if (kk == KSTT - 1 && hh) av = u32x4{0u, 0u, 0u, 0u};   // dims past DQT: whatever the DMA read
-      }
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) s[nb] = mfma32<T>(av, qop[nb][kk], s[nb]);
-    }
-  };
-  // Phase A: softcap, mask, row max and the lazy rescale of (m, l); fills
-  // O's factors, applied before the stage's P.V.  With commit false (a stage
-  // past this wave's causal range) the running state is left untouched.
-  auto phase_a = [&](auto mask_tag, int st, f32x16 (&s)[NB], bool commit, float (&f)[NB]) {
-    constexpr bool MASK = decltype(mask_tag)::value;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      if constexpr (CAP) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float e = fast_exp2(cap_in * s[nb][i]);
-          s[nb][i] = cap_out * (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f));
-        }
-      }
-      if constexpr (MASK) {
-        // Key t0 + 16 (i >> 3) + 8 hh + (i & 7) is visible iff its offset
-        // 16 (i >> 3) + (i & 7) (an inline constant) <= lim.
-        const int t0 = st * 32, qa = wq0 + 32 * nb + l32 + off;
-        int lim = r.k_len - 1 - t0;
-        if (CAUSAL) lim = min(lim, qa - t0);
-        else if (WR >= 0) lim = min(lim, qa + WR - t0);
-        lim -= 8 * hh;
-        // ... and >= lo (left window).
-        const int lo = WL >= 0 ? qa - WL - t0 - 8 * hh : INT_MIN;
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (16 * (i >> 3) + (i & 7) > lim || 16 * (i >> 3) + (i & 7) < lo) s[nb][i] = -INFINITY;
-      }
-      float mx = fmaxf(s[nb][0], s[nb][1]);
-#pragma unroll
-      for (int i = 2; i < 16; ++i) mx = fmaxf(mx, s[nb][i]);
-      mx = max_hh(mx);
-      const float cand = CAP ? mx : mx * c_scale;
-      const bool need = commit && cand > m_run[nb] + PF_RESCALE;
-      f[nb] = need ? fast_exp2(m_run[nb] - cand) : 1.0f;
-      m_run[nb] = need ? cand : m_run[nb];
-      l_run[nb] *= f[nb];
-    }
-  };
-  // Phase B: probabilities (<= 2^8), row sums, packed B operand of O^T.
-  auto phase_b = [&](f32x16 (&s)[NB], u32x4 (&pop)[NB][2]) {
-    const float sc = CAP ? 1.0f : c_scale;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const float mref = m_run[nb] == -INFINITY ? 0.0f : m_run[nb];
-      float psum = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float p = fast_exp2(fmaf(s[nb][i], sc, -mref));
-        s[nb][i] = p;
-        psum += p;
-      }
-      l_run[nb] += psum;
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        u32x4 w;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) w[q] = pack2<T>(s[nb][8 * c + 2 * q], s[nb][8 * c + 2 * q + 1]);
-        pop[nb][c] = w;
-      }
-    }
-  };
-  auto pv = [&](int st, const u32x4 (&pop)[NB][2]) {
-    const char* vl = vbuf0 + ((st >> 1) & 1) * VTILE + (st & 1) * 32 * 64;
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const int imm = 16 * c * 64 + db * PF_VBLOCK_BYTES;
-        const u32x2 lo = lds_read_tr(vl, vrd + imm);
-        const u32x2 hi = lds_read_tr(vl, vrd + imm + 4 * 64);
-        const u32x4 av = {lo[0], lo[1], hi[0], hi[1]};
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) o[nb][db] = mfma32<T>(av, pop[nb][c], o[nb][db]);
-      }
-  };
-  auto rescale_o = [&](const float (&f)[NB]) {
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      if (__builtin_expect(__any(f[nb] != 1.0f), 0)) {
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) o[nb][db][i] *= f[nb];
-      }
-    }
-  };
-
-  // One pipeline stage: P(st) from S(st), S(st+1), O += V P(st), phase A of
-  // S(st+1); f carries O's pending rescale factors.
-  //
-  // LDS traffic, at the start of tile j (even stages): wait for this wave's
-  // DMAs and barrier, after which V(j), K(j) rows 32..63 and K(j+1) rows
-  // 0..31 are resident and every wave is done with V(j-1), K(j-1) rows
-  // 32..63 and K(j) rows 0..31; then V(j+1), K(j+1) rows 32..63 and K(j+2)
-  // rows 0..31 are issued into the freed buffer halves.  With a full mode
-  // true the caller guarantees that those tiles lie inside the request.
-  // FP8: the staging tile holds tile j+1; it is widened into buffer
-  // (j+1) & 1 (free since tile j-1 is done), then refilled with tile j+2.
-  auto tile_start = [&](auto mode, int st) {
-    if ((st & 1) == 0) {
-      const int j = st >> 1;
-      __builtin_amdgcn_s_waitcnt(0x0F70);
-      __syncthreads();
-      if constexpr (FP8) {
-        if (j + 1 < n_tiles) {
-          widen_tile((j + 1) & 1);
-          __syncthreads();
-          if (j + 2 < n_tiles) dma_fp8(j + 2);
-        }
-      } else {
-        if (j + 1 < n_tiles) {
-          dma_v(mode, j + 1, (j + 1) & 1);
-          dma_k(mode, j + 1, (j + 1) & 1, 1);
-        }
-        if (j + 2 < n_tiles) dma_k(mode, j + 2, j & 1, 0);
-      }
-    }
-  };
-  // Tiles j + 1 and (if it exists) j + 2 hold 64 keys of the request each.
-  auto dma_full = [&](int j) { return PF_BN * (j + 2 < n_tiles ? j + 3 : j + 2) <= r.k_len; };
-  // Steady state: stage st and st+1 both active, st+1 unmasked.  One
-  // straight scheduling region: phase B(st) under the MFMAs of S(st+1),
-  // phase A(st+1) under the MFMAs of P.V(st).
-  auto step_hot = [&](auto mode, int st, f32x16 (&sc)[NB], f32x16 (&sn)[NB], float (&f)[NB])
-                      __attribute__((always_inline)) {
-    tile_start(mode, st);
-    rescale_o(f);
-    u32x4 pop[NB][2];
-    phase_b(sc, pop);
-    qk(st + 1, sn);
-    pv(st, pop);
-    phase_a(std::integral_constant<bool, false>(), st + 1, sn, true, f);
-  };
-  // Any stage: inactive waves only keep the barrier cadence; S(st+1) is
-  // computed even when stage st+1 lies past this wave's causal range (its K
-  // rows hold valid or stale finite data) and its phase A then commits
-  // nothing.
-  // With windows, a wave inactive at st (left of its window) but active at
-  // st+1 only computes S(st+1).
-  auto step_any = [&](int st, f32x16 (&sc)[NB], f32x16 (&sn)[NB], float (&f)[NB]) {
-    tile_start(std::integral_constant<int, PF_ANY_TILE>(), st);
-    const bool act = active(st), act_n = st + 1 < n_stages && active(st + 1);
-    u32x4 pop[NB][2];
-    if constexpr (WIN) {
-      if (!act && !act_n) return;
-      if (act) {
-        rescale_o(f);
-        phase_b(sc, pop);
-      }
-      qk(st + 1, sn);
-      if (act) pv(st, pop);
-    } else {
-      if (!act) return;
-      rescale_o(f);
-      phase_b(sc, pop);
-      qk(st + 1, sn);
-      pv(st, pop);
-    }
-    if (needs_mask(st + 1)) phase_a(std::integral_constant<bool, true>(), st + 1, sn, act_n, f);
-    else phase_a(std::integral_constant<bool, false>(), st + 1, sn, act_n, f);
-  };
-  auto hot = [&](int st) { return st < n_stages && active(st) && !needs_mask(st); };
-
-  if (st0 < n_stages) {
-    // Prologue: tile tile0 and K(tile0 + 1) rows 0..31 in LDS; S(st0) and
-    // its phase A.
-    const std::integral_constant<int, PF_ANY_TILE> any_tile;
-    if constexpr (FP8) {
-      dma_fp8(tile0);
-      __builtin_amdgcn_s_waitcnt(0x0F70);
-      __syncthreads();
-      widen_tile(tile0 & 1);
-      __syncthreads();
-      if (tile0 + 1 < n_tiles) dma_fp8(tile0 + 1);
-    } else {
-      dma_k(any_tile, tile0, tile0 & 1, 0);
-      dma_k(any_tile, tile0, tile0 & 1, 1);
-      dma_v(any_tile, tile0, tile0 & 1);
-      if (tile0 + 1 < n_tiles) dma_k(any_tile, tile0 + 1, (tile0 + 1) & 1, 0);
-      __builtin_amdgcn_s_waitcnt(0x0F70);
-      __syncthreads();
-    }
-    f32x16 sa[NB], sb[NB];
-    float f[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) f[nb] = 1.0f;
-    if (active(st0)) {
-      qk(st0, sa);
-      phase_a(std::integral_constant<bool, true>(), st0, sa, true, f);
-    }
-    // Even stage st holds S in sa, odd in sb.  The unmasked two-stage loop
-    // runs first; with windows it is re-entered at even stages where this
-    // wave is active (its window may start after st0).
-    // The hot loop is instantiated once per K/V layout (packed, paged).
-    int st = st0;
-    if constexpr (WIN) {
-      auto run_hot = [&](auto mode) {
-        for (; hot(st + 1) && hot(st + 2) && dma_full(st >> 1); st += 2) {
-          step_hot(mode, st, sa, sb, f);
-          step_hot(mode, st + 1, sb, sa, f);
-        }
-      };
-      while (st < n_stages) {
-        if (!(st & 1) && active(st)) {
-          if (paged) run_hot(std::integral_constant<int, PF_FULL_PAGED>());
-          else run_hot(std::integral_constant<int, PF_FULL_PACKED>());
-        }
-        if (st >= n_stages) break;
-        if (st & 1) step_any(st, sb, sa, f);
-        else step_any(st, sa, sb, f);
-        ++st;
-      }
-    } else {
-      // Closed form of hot(st + 1) && hot(st + 2) && dma_full(st / 2) for
-      // even st >= st0 without windows: hot(s) <=> wave_rows && s < hb, and
-      // dma_full(j) <=> j <= jmax (both conditions are prefixes of the
-      // stage / tile range).
-      const int kf = r.k_len / PF_BN;
-      const int jmax = n_tiles <= kf ? kf - 2 : kf - 3;
-      int hb = min(n_stages, r.k_len / 32);
-      if constexpr (CAUSAL) hb = min(hb, max(wave_qabs_lo + 1, 0) / 32);
-      const int lim = wave_rows ? min(hb - 2, 2 * jmax + 1) : INT_MIN;
-      auto run_hot = [&](auto mode) {
-        for (; st < lim; st += 2) {
-          step_hot(mode, st, sa, sb, f);
-          step_hot(mode, st + 1, sb, sa, f);
-        }
-      };
-      if (active(st)) {
-        if (paged) run_hot(std::integral_constant<int, PF_FULL_PAGED>());
-        else run_hot(std::integral_constant<int, PF_FULL_PACKED>());
-      }
-      for (; st < n_stages; ++st) {
-        if (st & 1) step_any(st, sb, sa, f);
-        else step_any(st, sa, sb, f);
-      }
-    }
-  }
-
-  // Epilogue: O = O^T / l, LSE = m * ln2 + ln(l).
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const float lt = sum_hh(l_run[nb]);
-    const int row = wq0 + 32 * nb + l32;
-    if (row < r.q_len) {
-      const float inv = lt > 0.0f ? vdsc / lt : 0.0f;
-      const int64_t tq = (int64_t)r.q_begin + row;
-      uint16_t* op = (uint16_t*)a.out + tq * a.out_stride[0] + (int64_t)h * a.out_stride[1] + 4 * hh;
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          if (32 * db + 8 * g + 8 > DVT) continue;   // padding columns
-          uint2 w;
-          w.x = pack2<T>(o[nb][db][4 * g] * inv, o[nb][db][4 * g + 1] * inv);
-          w.y = pack2<T>(o[nb][db][4 * g + 2] * inv, o[nb][db][4 * g + 3] * inv);
-          *(uint2*)(op + 32 * db + 8 * g) = w;
-        }
-      if (hh == 0)
-        a.lse[(int64_t)h * a.lse_stride[0] + tq * a.lse_stride[1]] = lt > 0.0f ? m_run[nb] * LN2 + logf(lt) : -INFINITY;
-    }
-  }
-}
-
-// Waves per workgroup, 32-row query blocks per wave and workgroups per CU
-// per head-dim pair (LDS holds two K and two V tiles per workgroup).
-#ifndef FA_PF128_W
-#define FA_PF128_W 4
-#define FA_PF128_NB 1
-#define FA_PF128_MINB 2
-#endif
-template <int DQ, int DV> struct PrefillTile;
-template <> struct PrefillTile<64, 64> { static constexpr int W = 4, NB = 1, MINB = 2; };
-template <> struct PrefillTile<128, 128> { static constexpr int W = FA_PF128_W, NB = FA_PF128_NB, MINB = FA_PF128_MINB; };
-template <> struct PrefillTile<192, 128> { static constexpr int W = 4, NB = 1, MINB = 1; };
-// Large grids of 192/128 heads: two workgroups per CU (2 x 80 KiB of LDS)
-// trade registers for a second wave per SIMD.  Few-workgroup launches keep
-// one workgroup per CU, whose heavy blocks then run at full speed.
-template <int DQ, int DV> struct PrefillTileWide { static constexpr bool exists = false; };
-template <> struct PrefillTileWide<192, 128> { static constexpr bool exists = true; static constexpr int W = 4, NB = 1, MINB = 2; };
-constexpr int64_t PF_WIDE_MIN_BLOCKS = 2048;
-template <> struct PrefillTile<256, 256> { static constexpr int W = 4, NB = 1, MINB = 1; };
-
-template <int DQ, int DV>
-constexpr size_t lds_bytes() {
-  return 2 * (size_t)(DQ / 64 + DV / 64) * PF_GROUP_BYTES;
-}
-
-using PrefillKernel = void (*)(fa_attn_args, PrefillShape);
-
-struct PrefillChoice {
-  PrefillKernel kern;
-  int bm, threads;
-  size_t lds;
-};
-
-template <typename T, int DQ, int DV, bool CAUSAL, typename S, int DQT, int DVT, typename KT>
-PrefillChoice pick_tile(bool cap, bool win) {
-  PrefillChoice c;
-  if (win)
-    c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, true, true, DQT, DVT, KT>
-                 : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false, true, DQT, DVT, KT>;
-  else
-    c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, true, false, DQT, DVT, KT>
-                 : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false, false, DQT, DVT, KT>;
-  c.bm = 32 * S::NB * S::W;
-  c.threads = 64 * S::W;
-  c.lds = lds_bytes<DQ, DV>() + (KT::id == FA_E4M3 ? 64 * (size_t)(DQ + DV) : 0);   // + FP8 staging tile
-  return c;
-}
-
-template <typename T, int DQ, int DV, bool CAUSAL, int DQT, int DVT, typename KT>
-PrefillChoice pick_cap(bool cap, bool wide, bool win) {
-  if constexpr (PrefillTileWide<DQ, DV>::exists) {
-    static_assert(32 * PrefillTileWide<DQ, DV>::NB * PrefillTileWide<DQ, DV>::W ==
-                      32 * PrefillTile<DQ, DV>::NB * PrefillTile<DQ, DV>::W,
-                  "both tiles cover the same query rows per workgroup");
-    if (wide) return pick_tile<T, DQ, DV, CAUSAL, PrefillTileWide<DQ, DV>, DQT, DVT, KT>(cap, win);
-  }
-  return pick_tile<T, DQ, DV, CAUSAL, PrefillTile<DQ, DV>, DQT, DVT, KT>(cap, win);
-}
-
-// (DQ, DV) = the tile; (DQT, DVT) = the tensors' head dims padded into it;
-// KT = the K/V storage type.
-template <typename T, typename KT, int DQ, int DV, int DQT = DQ, int DVT = DV>
-PrefillChoice pick(bool causal, bool cap, bool wide, bool win) {
-  return causal ? pick_cap<T, DQ, DV, true, DQT, DVT, KT>(cap, wide, win)
-                : pick_cap<T, DQ, DV, false, DQT, DVT, KT>(cap, wide, win);
-}
-
-// Head dims of the reference's fast path (flash_attn_mps/_attention.py:149-158:
-// 32, 64, 72, 80, 96, 128, 256) plus DIFFKV 192/128; 32 runs in the 64-dim
-// tile and 72/80/96 in the 128-dim tile.  FP8 K/V: 64, 128, 256.
-template <typename T>
-PrefillChoice pick_dims(int64_t dq, int64_t dv, bool causal, bool cap, bool wide, bool win, bool fp8) {
-  if (dq != dv && !(dq == 192 && dv == 128)) return PrefillChoice{nullptr, 0, 0, 0};
-  if (fp8) {
-    if (dq != dv) return PrefillChoice{nullptr, 0, 0, 0};
-    switch (dq) {
-      case 64: return pick<T, E4M3T, 64, 64>(causal, cap, false, win);
-      case 128: return pick<T, E4M3T, 128, 128>(causal, cap, false, win);
-      case 256: return pick<T, E4M3T, 256, 256>(causal, cap, false, win);
-      default: return PrefillChoice{nullptr, 0, 0, 0};
-    }
-  }
-  switch (dq) {
-    case 32: return pick<T, T, 64, 64, 32, 32>(causal, cap, wide, win);
-    case 64: return pick<T, T, 64, 64>(causal, cap, wide, win);
-    case 72: return pick<T, T, 128, 128, 72, 72>(causal, cap, wide, win);
-    case 80: return pick<T, T, 128, 128, 80, 80>(causal, cap, wide, win);
-    case 96: return pick<T, T, 128, 128, 96, 96>(causal, cap, wide, win);
-    case 128: return pick<T, T, 128, 128>(causal, cap, wide, win);
-    case 192: return pick<T, T, 192, 128>(causal, cap, wide, win);
-    case 256: return pick<T, T, 256, 256>(causal, cap, wide, win);
-    default: return PrefillChoice{nullptr, 0, 0, 0};
-  }
-}
+using namespace fa_prefill;
 
 PrefillChoice select_prefill(const fa_attn_args& a, bool wide) {
   const bool causal = a.causal != 0, cap = a.softcap > 0.0f, fp8 = a.k_dtype == FA_E4M3;
   // A right window bounds nothing under causality.
   const bool win = a.window_left >= 0 || (!causal && a.window_right >= 0);
-  return a.q_dtype == FA_BF16 ? pick_dims<BF16T>(a.head_dim_qk, a.head_dim_v, causal, cap, wide, win, fp8)
-                              : pick_dims<F16T>(a.head_dim_qk, a.head_dim_v, causal, cap, wide, win, fp8);
+  const int64_t dq = a.head_dim_qk, dv = a.head_dim_v;
+  const bool bf16 = a.q_dtype == FA_BF16;
+  if (!fp8 && dq <= 128)
+    return bf16 ? pick_bf16_small(dq, dv, causal, cap, wide, win) : pick_f16_small(dq, dv, causal, cap, wide, win);
+  return bf16 ? pick_bf16_large(dq, dv, causal, cap, wide, win, fp8) : pick_f16_large(dq, dv, causal, cap, wide, win, fp8);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }

@@ -167,3 +167,37 @@ def test_graph_store_kvcache(device):
         s = slots[ok].long()
         assert torch.equal(kc.view(-1, hkv, d)[s], k[ok]), f"replay {it}"
         assert torch.equal(vc.view(-1, hkv, d)[s], v[ok]), f"replay {it}"
+
+
+def test_graph_fp8_chunked_prefill_mixed_batch(device):
+    """Chunked prefill over an FP8 paged cache (MFMA kernel, staged E4M3
+    tiles) with single-query rows (decode kernel) in one captured call."""
+    gen = torch.Generator().manual_seed(75)
+    ctx = [700, 1, 1300, 64, 1, 2000]
+    q_lens = [300, 1, 129, 64, 1, 2]
+    hq, hkv, d, page = 16, 8, 128, 16
+    scale = torch.empty(hkv).uniform_(0.02, 0.1, generator=gen).to(device)
+    kc, vc, table = paged_cache(ctx, page, hkv, d, d, torch.float8_e4m3fn, device, gen, scale=scale)
+    q = torch.randn(sum(q_lens), hq, d, generator=gen).to(torch.bfloat16).to(device)
+    cuq = torch.tensor([0] + torch.tensor(q_lens).cumsum(0).tolist(), dtype=torch.int32, device=device)
+    used = torch.tensor(ctx, dtype=torch.int32, device=device)
+    desc = scale.expand(len(ctx), hkv)
+    out = torch.empty(sum(q_lens), hq, d, dtype=torch.bfloat16, device=device)
+
+    def call():
+        return vllm.flash_attn_varlen_func(q, kc, vc, max(q_lens), cuq, max(ctx), seqused_k=used, block_table=table,
+                                           causal=True, k_descale=desc, v_descale=desc, out=out)
+
+    graph, _ = capture(call)
+    for it in range(REPLAYS):
+        q.copy_(torch.randn(q.shape, generator=gen).to(torch.bfloat16))
+        call()
+        eager = out.clone()
+        if it == 0:
+            ref, _ = attention_reference(q, kc, vc, cuq, used_k=used, block_table=table, causal=True,
+                                         k_descale=desc, v_descale=desc)
+            assert_attention_close(eager, ref, torch.bfloat16)
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {it}"
