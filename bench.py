@@ -312,7 +312,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one MI355X; --gpus must be 1 "
-                                   "(the kernels run on one GPU's share; see DESIGN.md for sharding)"}))
+                                   "(attention shards by request or KV head, one process per GPU, "
+                                   "and each GPU runs these kernels on its share)"}))
         sys.exit(2)
     import torch
     device = torch.device("cuda", 0)
