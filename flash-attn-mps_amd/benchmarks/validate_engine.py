@@ -25,7 +25,11 @@ likelier than a trained model does; they are reported, not failed).  Cases mirro
 reference's (validate_nanovllm.py:165-171): normal, cross-page, shared-prefix (prefix-cache hits),
 chunked-prefill, preemption.
 
+With --performance it also times greedy generation (batch 1 and 4, 1024-token prompts, 128 new
+tokens) with this package's kernels against per-request torch SDPA.
+
 usage: python flash-attn-mps_amd/benchmarks/validate_engine.py --output report.json [--layers 28] [--case NAME]
+       [--performance]
 """
 import argparse
 import itertools
@@ -120,6 +124,25 @@ def native_attention(q, k, v, k_cache, v_cache, ctx, scale):
                                          ctx.max_k, softmax_scale=scale, causal=True, block_table=ctx.block_tables)
     return fa.flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache, cache_seqlens=ctx.context_lens,
                                       block_table=ctx.block_tables, softmax_scale=scale, causal=True).squeeze(1)
+
+
+def sdpa_attention(q, k, v, k_cache, v_cache, ctx, scale):
+    """Timing baseline: index_copy_ slot writes and per-request torch SDPA (flash / memory-efficient
+    backends, fp16, lower-right causal bias, GQA) over the gathered pages."""
+    from compare_sdpa import sdpa_gqa
+    slots = ctx.slot_mapping.long()
+    k_cache.flatten(0, 1).index_copy_(0, slots, k)
+    v_cache.flatten(0, 1).index_copy_(0, slots, v)
+    outs, start = [], 0
+    tables = ctx.block_tables.long()
+    for b, (ql, kl) in enumerate(zip(ctx.q_lens, ctx.k_lens)):
+        blocks = tables[b, : math.ceil(kl / PAGE)]
+        key = k_cache[blocks].flatten(0, 1)[:kl].transpose(0, 1).unsqueeze(0).contiguous()
+        val = v_cache[blocks].flatten(0, 1)[:kl].transpose(0, 1).unsqueeze(0).contiguous()
+        query = q[start:start + ql].transpose(0, 1).unsqueeze(0).contiguous()
+        outs.append(sdpa_gqa(query, key, val, ql, kl).squeeze(0).transpose(0, 1))
+        start += ql
+    return torch.cat(outs)
 
 
 def reference_attention(q, k, v, k_cache, v_cache, ctx, scale):
@@ -469,16 +492,56 @@ def run_all(cfg, device, only=None):
     return report, failures
 
 
+def performance(cfg, device, prompt_len=1024, generated=128, rounds=3):
+    """Greedy generation throughput of the engine with native vs SDPA attention, batch 1 and 4
+    (the shape of the reference's benchmarks/bench_nanovllm_optimization.py:202-260: 1024-token
+    prompts, 128 new tokens, a warmup generation on prompts that share no cached prefix)."""
+    weights = init_weights(cfg, device)
+    settings = dict(max_num_seqs=4, max_num_batched_tokens=4096, num_blocks=32)
+    pattern = [(7 * i + 3) % 997 + 11 for i in range(41)]
+    rows = []
+
+    def sampler(logits, seqs):
+        return logits.argmax(-1).tolist()
+
+    for batch in (1, 4):
+        prompts = [[pattern[(i + off) % len(pattern)] for i in range(prompt_len)] for off in range(batch)]
+        warm = [[1000 + j] + p[1:] for j, p in enumerate(prompts)]
+        row = {"batch": batch, "prompt_tokens": prompt_len, "generated_tokens": generated}
+        for label, backend in (("sdpa", sdpa_attention), ("native", native_attention)):
+            rates = []
+            for _ in range(rounds):
+                model = Model(cfg, weights, backend, settings["num_blocks"], device)
+                eng = Engine(model, settings["num_blocks"], settings["max_num_seqs"],
+                             settings["max_num_batched_tokens"], device)
+                eng.generate(warm, 16, sampler)
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                outs = eng.generate(prompts, generated, sampler, first_sid=100)
+                torch.cuda.synchronize()
+                rates.append(sum(len(o) for o in outs) / (time.perf_counter() - t0))
+                del model, eng
+            row[label + "_tokens_per_s"] = sorted(rates)[len(rates) // 2]
+        row["speedup"] = row["native_tokens_per_s"] / row["sdpa_tokens_per_s"]
+        print("performance", json.dumps(row), flush=True)
+        rows.append(row)
+    return rows
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--output", type=Path, required=True)
     ap.add_argument("--layers", type=int, default=28)
     ap.add_argument("--case")
+    ap.add_argument("--performance", action="store_true", help="also time generation, native vs SDPA")
     opts = ap.parse_args()
     if not torch.cuda.is_available():
         sys.exit("validate_engine.py needs a GPU")
     cfg = ModelConfig(layers=opts.layers)
     report, failures = run_all(cfg, torch.device("cuda", 0), opts.case)
+    if opts.performance:
+        with torch.inference_mode():
+            report["performance"] = performance(cfg, torch.device("cuda", 0))
     report["device"] = torch.cuda.get_device_name(0)
     report["torch"] = torch.__version__
     opts.output.parent.mkdir(parents=True, exist_ok=True)
