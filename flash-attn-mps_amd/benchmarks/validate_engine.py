@@ -25,8 +25,10 @@ likelier than a trained model does; they are reported, not failed).  Cases mirro
 reference's (validate_nanovllm.py:165-171): normal, cross-page, shared-prefix (prefix-cache hits),
 chunked-prefill, preemption.
 
-With --performance it also times greedy generation (batch 1 and 4, 1024-token prompts, 128 new
-tokens) with this package's kernels against per-request torch SDPA.
+Every case also runs natively with the decode step captured in HIP graphs (one per batch size,
+replayed with the step's inputs in static buffers) and must meet the same criteria.  With
+--performance it also times greedy generation (batch 1 and 4, 1024-token prompts, 128 new tokens):
+this package's kernels eager and graph-captured against per-request torch SDPA.
 
 usage: python flash-attn-mps_amd/benchmarks/validate_engine.py --output report.json [--layers 28] [--case NAME]
        [--performance]
@@ -268,9 +270,65 @@ class BlockManager:
         return True
 
 
+class DecodeGraphs:
+    """Decode steps captured once per batch size (HIP graphs through torch.cuda.CUDAGraph) and
+    replayed with the step's inputs copied into static buffers.  Rows past the real batch are padding:
+    slot -1 (no cache write), length 1, outputs ignored.  The attention calls read no device values
+    on the host, which is what makes the step capturable."""
+
+    def __init__(self, model, max_bs, num_blocks, device):
+        self.model = model
+        self.sizes = [b for b in (1, 2, 4, 8, 16, 32) if b < max_bs] + [max_bs]
+        self.ids = torch.zeros(max_bs, dtype=torch.int64, device=device)
+        self.pos = torch.zeros(max_bs, dtype=torch.int64, device=device)
+        self.slots = torch.full((max_bs,), -1, dtype=torch.int32, device=device)
+        self.tables = torch.zeros(max_bs, num_blocks, dtype=torch.int32, device=device)
+        self.lens = torch.ones(max_bs, dtype=torch.int32, device=device)
+        self.rows = torch.arange(max_bs, device=device)
+        self.graphs, self.out = {}, {}
+
+    def _forward(self, bs):
+        ctx = StepContext(False, self.slots[:bs], self.tables[:bs], context_lens=self.lens[:bs], max_q=1,
+                          max_k=self.tables.shape[1] * PAGE)
+        return self.model.forward(self.ids[:bs], self.pos[:bs], ctx, self.rows[:bs])
+
+    def _capture(self, bs):
+        main = torch.cuda.current_stream()
+        side = torch.cuda.Stream()
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                self._forward(bs)
+        main.wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            self.out[bs] = self._forward(bs)
+        self.graphs[bs] = graph
+
+    def run(self, ids, pos, slots, tables, lens):
+        n = ids.shape[0]
+        bs = next(b for b in self.sizes if b >= n)
+        if bs not in self.graphs:
+            self.slots.fill_(-1)
+            self.lens.fill_(1)
+            self._capture(bs)
+        self.ids[:n] = ids
+        self.pos[:n] = pos
+        self.slots[:n] = slots
+        self.slots[n:bs] = -1
+        self.tables[:n] = 0
+        self.tables[:n, : tables.shape[1]] = tables
+        self.lens[:n] = lens
+        self.lens[n:bs] = 1
+        self.graphs[bs].replay()
+        return self.out[bs][:n]
+
+
 class Engine:
-    def __init__(self, model, num_blocks, max_num_seqs, max_num_batched_tokens, device):
+    def __init__(self, model, num_blocks, max_num_seqs, max_num_batched_tokens, device, graphs=False):
         self.model, self.device = model, device
+        self.graphs = DecodeGraphs(model, max_num_seqs, num_blocks, device) if graphs else None
         self.bm = BlockManager(num_blocks)
         self.max_num_seqs, self.budget = max_num_seqs, max_num_batched_tokens
         self.waiting, self.running = [], []
@@ -358,10 +416,14 @@ class Engine:
         pos = torch.tensor([len(s.tokens) - 1 for s in seqs], device=dev)
         slots = torch.cat([self._slots(s, len(s.tokens) - 1, len(s.tokens)) for s in seqs]).to(dev, torch.int32)
         lens = [len(s.tokens) for s in seqs]
-        ctx = StepContext(False, slots, self._tables(seqs).to(dev),
-                          context_lens=torch.tensor(lens, dtype=torch.int32, device=dev),
-                          q_lens=[1] * len(seqs), k_lens=lens, max_q=1, max_k=max(lens))
-        logits = self.model.forward(ids, pos, ctx, torch.arange(len(seqs), device=dev))
+        tables = self._tables(seqs).to(dev)
+        lens_t = torch.tensor(lens, dtype=torch.int32, device=dev)
+        if self.graphs is not None:
+            logits = self.graphs.run(ids, pos, slots, tables, lens_t)
+        else:
+            ctx = StepContext(False, slots, tables, context_lens=lens_t, q_lens=[1] * len(seqs), k_lens=lens,
+                              max_q=1, max_k=max(lens))
+            logits = self.model.forward(ids, pos, ctx, torch.arange(len(seqs), device=dev))
         for s in seqs:
             s.computed = len(s.tokens)
         for s, tok in zip(seqs, sampler(logits, seqs)):
@@ -389,10 +451,11 @@ def kl_rows(ref, act):
     return (ref_logp.exp() * (ref_logp - act_logp)).sum(-1)
 
 
-def run_case(cfg, weights, settings, batches, backend, device, expected=None):
+def run_case(cfg, weights, settings, batches, backend, device, expected=None, graphs=False):
     """One engine run; with `expected` the sampler is teacher-forced and logits are compared."""
     model = Model(cfg, weights, backend, settings["num_blocks"], device)
-    eng = Engine(model, settings["num_blocks"], settings["max_num_seqs"], settings["max_num_batched_tokens"], device)
+    eng = Engine(model, settings["num_blocks"], settings["max_num_seqs"], settings["max_num_batched_tokens"], device,
+                 graphs=graphs)
     trace, errors = [], []
 
     def sampler(logits, seqs):
@@ -476,7 +539,10 @@ def run_all(cfg, device, only=None):
                 continue
             ref, trace = run_case(cfg, weights, settings, batches, reference_attention, device)
             native, _ = run_case(cfg, weights, settings, batches, native_attention, device, expected=trace)
-            bad = check(name, ref, native, batches)
+            graphed, _ = run_case(cfg, weights, settings, batches, native_attention, device, expected=trace,
+                                  graphs=True)
+            bad = check(name, ref, native, batches) + [f"{b} (graph-captured decode)" for b in
+                                                       check(name, ref, graphed, batches)]
             failures += bad
             report["cases"].append({
                 "name": name, "settings": settings, "counters": native["counters"],
@@ -485,6 +551,7 @@ def run_all(cfg, device, only=None):
                 "logit_max_abs": max((e["max_abs"] for e in native["errors"]), default=0.0),
                 "greedy_matches": all(e["greedy_matches"] for e in native["errors"]),
                 "greedy_mismatches_decided": sum(e["greedy_mismatches_decided"] for e in native["errors"]),
+                "graph_kl_max": max((e["kl_max"] for e in graphed["errors"]), default=0.0),
                 "reference_s": ref["elapsed_s"], "native_s": native["elapsed_s"], "passed": not bad})
             print(name, json.dumps(report["cases"][-1]["counters"]), "kl_max",
                   f"{report['cases'][-1]['kl_max']:.2e}", "PASS" if not bad else "FAIL", flush=True)
@@ -508,12 +575,13 @@ def performance(cfg, device, prompt_len=1024, generated=128, rounds=3):
         prompts = [[pattern[(i + off) % len(pattern)] for i in range(prompt_len)] for off in range(batch)]
         warm = [[1000 + j] + p[1:] for j, p in enumerate(prompts)]
         row = {"batch": batch, "prompt_tokens": prompt_len, "generated_tokens": generated}
-        for label, backend in (("sdpa", sdpa_attention), ("native", native_attention)):
+        for label, backend, graphs in (("sdpa", sdpa_attention, False), ("native", native_attention, False),
+                                       ("native_graph", native_attention, True)):
             rates = []
             for _ in range(rounds):
                 model = Model(cfg, weights, backend, settings["num_blocks"], device)
                 eng = Engine(model, settings["num_blocks"], settings["max_num_seqs"],
-                             settings["max_num_batched_tokens"], device)
+                             settings["max_num_batched_tokens"], device, graphs=graphs)
                 eng.generate(warm, 16, sampler)
                 torch.cuda.synchronize()
                 t0 = time.perf_counter()
@@ -523,6 +591,7 @@ def performance(cfg, device, prompt_len=1024, generated=128, rounds=3):
                 del model, eng
             row[label + "_tokens_per_s"] = sorted(rates)[len(rates) // 2]
         row["speedup"] = row["native_tokens_per_s"] / row["sdpa_tokens_per_s"]
+        row["graph_speedup"] = row["native_graph_tokens_per_s"] / row["sdpa_tokens_per_s"]
         print("performance", json.dumps(row), flush=True)
         rows.append(row)
     return rows

@@ -31,3 +31,14 @@ def test_engine_case(device, weights, name):
         native, _ = ve.run_case(CFG, weights, settings, batches, ve.native_attention, device, expected=trace)
     assert native["errors"], "no sampler calls"
     assert ve.check(name, ref, native, batches) == []
+
+
+@pytest.mark.parametrize("name", ["normal", "preemption"])
+def test_engine_case_graph_captured_decode(device, weights, name):
+    """The decode step captured in HIP graphs (per batch size, padded rows) meets the same bar."""
+    settings, batches = next((s, b) for n, s, b in ve.cases() if n == name)
+    with torch.inference_mode():
+        ref, trace = ve.run_case(CFG, weights, settings, batches, ve.reference_attention, device)
+        native, _ = ve.run_case(CFG, weights, settings, batches, ve.native_attention, device, expected=trace,
+                                graphs=True)
+    assert ve.check(name, ref, native, batches) == []
