@@ -211,8 +211,13 @@ def attention(q, k, v, *, cu_seqlens_q, cu_seqlens_k=None, seqused_k=None, max_s
             and _lib.supported("fa_prefill_supported", args)):
         # Mixed batches (chunked prefill + decode): single-query requests run
         # on the split-KV decode kernel and the MFMA kernel skips them, since a
-        # 128-row query tile would spend one workgroup per head on each.
-        if batch > 1 and _decode_rows(args, batch, heads, kh, dq, dv, max_seqlen_k, q.device, keep):
+        # 128-row query tile would spend one workgroup per head on each.  When
+        # the same offsets describe queries and keys (packed self-attention), a
+        # single-query request has a single key, so the MFMA kernel keeps it
+        # and no decode pass is launched.
+        self_attention = cu_seqlens_k is cu_seqlens_q and seqused_k is None and block_table is None
+        if (batch > 1 and not self_attention
+                and _decode_rows(args, batch, heads, kh, dq, dv, max_seqlen_k, q.device, keep)):
             args.flags |= _lib.FLAG_SKIP_SINGLE_QUERY
         _lib.call("fa_prefill_fwd", args, q.device)
         return out, lse
