@@ -35,7 +35,7 @@ def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--warmup", type=int, default=200)
     p.add_argument("--no-secondary", action="store_true", help="only the headline prefill config")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--only", default="", help="comma list of configs to run (2,3,4,5)")
@@ -61,35 +61,43 @@ def causal_pairs(q_lens, k_lens):
     return total
 
 
-def time_calls(fn, steps, warmup):
-    """Warmup, then `steps` back-to-back calls bracketed by synchronize.
-    Returns (ms per step over the whole region, mean ms per call from per-call
-    events on the launching stream)."""
+def time_calls(fn, steps, warmup, kernel=None):
+    """Warmup, then `steps` back-to-back calls bracketed by synchronize with
+    no other work in between (ms per step = the region over `steps`).  A
+    second pass of `steps` calls then records a HIP event pair around every
+    call, and around every launch of the C-ABI entry point `kernel` when one
+    is named, on the launching stream (event records cost a few microseconds
+    each, so they stay out of the first region).  Returns (ms per step, median
+    ms per call, mean ms per `kernel` launch or None)."""
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     region0 = torch.cuda.Event(enable_timing=True)
     region1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     region0.record()
-    for i in range(steps):
-        starts[i].record()
+    for _ in range(steps):
         fn()
-        ends[i].record()
     region1.record()
     torch.cuda.synchronize()
     total = region0.elapsed_time(region1)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    with launch_events(kernel) as pairs:
+        for i in range(steps):
+            starts[i].record()
+            fn()
+            ends[i].record()
+        torch.cuda.synchronize()
     per_call = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
-    return total / steps, per_call[len(per_call) // 2]
+    kernel_ms = sum(s.elapsed_time(e) for s, e in pairs) / len(pairs) if pairs else None
+    return total / steps, per_call[len(per_call) // 2], kernel_ms
 
 
 class launch_events:
     """Record a HIP event pair on the launching stream around every call of
     one C-ABI entry point (the library's only route to the GPU), so a single
-    kernel's duration is timed inside the benchmark's own timed region."""
+    kernel's duration is timed inside the benchmark; name None records none."""
 
     def __init__(self, name):
         self.name = name
@@ -101,7 +109,7 @@ class launch_events:
         self._lib, self._orig = _lib, _lib.call
 
         def call(name, args, device):
-            if name != self.name:
+            if self.name is None or name != self.name:
                 return self._orig(name, args, device)
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             start.record()
@@ -162,9 +170,7 @@ def config2(device, steps, warmup):
     def step():
         fa.flash_attn_varlen_func(q, k, v, cu, cu, maxlen, maxlen, causal=True, out=out)
 
-    with launch_events("fa_prefill_fwd") as pairs:
-        ms, call_ms = time_calls(step, steps, warmup)
-    kernel_ms = sum(s.elapsed_time(e) for s, e in pairs[-steps:]) / steps
+    ms, call_ms, kernel_ms = time_calls(step, steps, warmup, kernel="fa_prefill_fwd")
     flops = causal_pairs(lengths, lengths) * hq * 2 * (d + d)
     return dict(lengths=lengths, flops=flops, ms=ms, call_ms=call_ms, kernel_ms=kernel_ms,
                 tflops=flops / (ms * 1e-3) / 1e12, call_tflops=flops / (call_ms * 1e-3) / 1e12,
@@ -216,7 +222,7 @@ def config3(device, steps, warmup):
     def step():
         fa.flash_attn_with_kvcache(q, kc, vc, cache_seqlens=lens, block_table=table, causal=True)
 
-    ms, call_ms = time_calls(step, steps, warmup)
+    ms, call_ms, _ = time_calls(step, steps, warmup)
     kv_bytes = sum(ctx) * hkv * 2 * d * 2
     del kc, vc
     return dict(kv_bytes=kv_bytes, ms=ms, call_ms=call_ms, gbs=kv_bytes / (ms * 1e-3) / 1e9,
@@ -243,7 +249,7 @@ def config4(device, steps, warmup):
                                     causal=True, softcap=50.0, window_size=(4095, 0),
                                     k_descale=desc, v_descale=desc, out=out)
 
-    ms, call_ms = time_calls(step, steps, warmup)
+    ms, call_ms, _ = time_calls(step, steps, warmup)
     kv_bytes = sum(min(c, 4096) for c in ctx) * hkv * 2 * d * 1
     del kc, vc
     return dict(kv_bytes=kv_bytes, ms=ms, call_ms=call_ms, gbs=kv_bytes / (ms * 1e-3) / 1e9,
@@ -272,7 +278,7 @@ def config5(device, steps, warmup):
         vllm.flash_attn_varlen_func(q, kc, vc, max(q_lens), cuq, max(k_lens), seqused_k=used,
                                     block_table=table, causal=True, s_aux=sinks, out=out)
 
-    ms, call_ms = time_calls(step, steps, warmup)
+    ms, call_ms, _ = time_calls(step, steps, warmup)
     dec_bytes = sum(dec_ctx) * hkv * (dqk + dv) * 2
     chunk_bytes = sum(k_lens[:8]) * hkv * (dqk + dv) * 2
     flops = causal_pairs(q_lens[:8], k_lens[:8]) * hq * 2 * (dqk + dv)
