@@ -449,6 +449,7 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
 // s0 + j on lane j), and broadcast with readlane; every lane accumulates the
 // dims lane, lane + 64, ... so each partial row is one coalesced read.
 constexpr int MERGE_DIMS = 256 / 64;   // dims per lane: the decode kernels cover Dv <= 256
+constexpr int MERGE_GROUP = 8;         // splits whose loads are in flight together
 
 __global__ __launch_bounds__(256) void decode_merge_kernel(const fa_attn_args a, const int span) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -475,7 +476,26 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const fa_attn_args a,
     const float w = s0 + lane < nv ? expf(plse[s0 + lane] - ref) : 0.0f;
     denom += w;
     const int cnt = min(64, nv - s0);
-    for (int j = 0; j < cnt; ++j) {
+    // Splits in groups of MERGE_GROUP: all their loads are issued before any
+    // is used.  A zero-weight split (empty, its partial never written) is
+    // read like the others but dropped by a select, so its contents never
+    // reach the sum.
+    int j = 0;
+    for (; j + MERGE_GROUP <= cnt; j += MERGE_GROUP) {
+      float ws[MERGE_GROUP], x[MERGE_GROUP][MERGE_DIMS];
+#pragma unroll
+      for (int u = 0; u < MERGE_GROUP; ++u) {
+        ws[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j + u));
+        const float* src = po + (int64_t)(s0 + j + u) * DV;
+#pragma unroll
+        for (int k = 0; k < MERGE_DIMS; ++k) x[u][k] = lane + 64 * k < DV ? src[lane + 64 * k] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < MERGE_GROUP; ++u)
+#pragma unroll
+        for (int k = 0; k < MERGE_DIMS; ++k) acc[k] = ws[u] > 0.0f ? fmaf(ws[u], x[u][k], acc[k]) : acc[k];
+    }
+    for (; j < cnt; ++j) {
       const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
       if (ws > 0.0f) {   // zero-weight splits are never read
         const float* src = po + (int64_t)(s0 + j) * DV;
