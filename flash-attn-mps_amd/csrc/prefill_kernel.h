@@ -185,6 +185,7 @@ struct PrefillShape {
   int n_qblocks;
   int log2_page;   // paged K/V: page size = 1 << log2_page
   int compact;     // 1: workgroups map onto the compact work list
+  int hp;          // query heads per workgroup (1 or 2, dividing the GQA group): W / hp waves per head
 };
 
 // One workgroup's share of the compact work list.  XCD x owns KV heads
@@ -200,7 +201,9 @@ struct WorkItem {
   RequestInfo r;
 };
 
-template <int BM>
+// BMH: query rows per head of a workgroup; G: workgroups per query block and
+// KV head (the GQA group over the heads packed into one workgroup).
+template <int BMH>
 FA_DEV bool compact_item(const fa_attn_args& a, int slot, int xcd, int lane, int G, WorkItem& w) {
   const int n = (int)a.batch;
   int qbeg = 0, qlen = 0, klen = -1, kbase = 0;
@@ -212,7 +215,7 @@ FA_DEV bool compact_item(const fa_attn_args& a, int slot, int xcd, int lane, int
     klen = a.seqused_k ? a.seqused_k[lane * a.used_k_stride] : a.cu_seqlens_k[(lane + 1) * a.cu_k_stride] - kc;
   }
   const bool skip = (a.flags & FA_FLAG_SKIP_SINGLE_QUERY) && qlen == 1;   // the decode kernel owns it
-  const int nqb = (lane < n && !skip) ? (qlen + BM - 1) / BM : 0;
+  const int nqb = (lane < n && !skip) ? (qlen + BMH - 1) / BMH : 0;
   int before = 0;   // query blocks of the requests ranked ahead of this one
   for (int j = 0; j < n; ++j) {
     const int lj = __builtin_amdgcn_readlane(klen, j);
@@ -283,11 +286,14 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // one.  Compact mode launches only real work; otherwise XCD x takes the
   // pairs p = x, x + 8, ... with n_qblocks slots each and skips the slots
   // past a request's end.
-  const int G = (int)(a.heads_q / a.heads_k);
+  // With hp = 2 a workgroup holds BM / 2 rows of two query heads of one KV
+  // head (waves 0 .. W/2-1 the first head), sharing every K/V tile.
+  const int G = (int)(a.heads_q / a.heads_k) / shp.hp;
   const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
   WorkItem wi;
   if (shp.compact) {
-    if (!compact_item<BM>(a, slot, xcd, lane, G, wi)) return;
+    if (!(shp.hp == 2 ? compact_item<BM / 2>(a, slot, xcd, lane, G, wi) : compact_item<BM>(a, slot, xcd, lane, G, wi)))
+      return;
   } else {
     const int per_pair = shp.n_qblocks * G;
     const int64_t pair = (int64_t)(slot / per_pair) * 8 + xcd;
@@ -301,9 +307,11 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     if ((a.flags & FA_FLAG_SKIP_SINGLE_QUERY) && wi.r.q_len == 1) return;   // the decode kernel owns it
   }
   const int64_t b = wi.b;
-  const int qb = wi.qb, kh = wi.kh, h = kh * G + wi.g;
+  const int wph = W / shp.hp;   // waves per head
+  const int bmh = 32 * NB * wph;   // query rows per head
+  const int qb = wi.qb, kh = wi.kh, h = (kh * G + wi.g) * shp.hp + wave_u / wph;
   const RequestInfo r = wi.r;
-  const int q0 = qb * BM;
+  const int q0 = qb * bmh;
   if (q0 >= r.q_len) return;
   const int off = r.k_len - r.q_len;   // absolute position of query row i is i + off
   // Row qa sees keys j with qa - WL <= j (WL >= 0), j <= qa (causal) or
@@ -311,7 +319,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // attention.metal:29-45, window kind).  The workgroup's key range follows
   // from its first and last rows.
   const int WL = WIN ? a.window_left : -1, WR = (WIN && !CAUSAL) ? a.window_right : -1;
-  const int qa_first = q0 + off, qa_last = min(q0 + BM, r.q_len) - 1 + off;
+  const int qa_first = q0 + off, qa_last = min(q0 + bmh, r.q_len) - 1 + off;
   int kv_end = r.k_len;
   if (CAUSAL) kv_end = min(kv_end, qa_last + 1);
   else if (WR >= 0) kv_end = min(kv_end, max(qa_last + WR + 1, 0));
@@ -321,7 +329,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
 
   // Q^T operands for the whole kernel: block nb, lane holds
   // Q[wq0 + 32 nb + l32][16 kk + 8 hh .. +8].
-  const int wq0 = q0 + wave_u * 32 * NB;
+  const int wq0 = q0 + (wave_u % wph) * 32 * NB;
   u32x4 qop[NB][KST];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {

@@ -73,18 +73,22 @@ extern "C" int fa_prefill_fwd(const fa_attn_args* a, void* stream) {
   FA_REQUIRE(a->max_seqlen_q >= 1, "fa_prefill_fwd: max_seqlen_q must be positive");
   PrefillChoice ch = select_prefill(*a, false);
   PrefillShape shp;
-  shp.n_qblocks = (int)fa_ceil_div(a->max_seqlen_q, ch.bm);
+  // Query heads per workgroup: two heads of a KV head share each workgroup's
+  // K/V tiles when the GQA group is even.
+  shp.hp = (a->heads_q / a->heads_k) % 2 == 0 ? 2 : 1;
+  const int64_t bmh = ch.bm / shp.hp;   // query rows per head of a workgroup
+  shp.n_qblocks = (int)fa_ceil_div(a->max_seqlen_q, bmh);
   shp.log2_page = 0;
   if (a->page_size)
     while ((1ll << shp.log2_page) < a->page_size) ++shp.log2_page;
   const int64_t pairs = a->batch * a->heads_k;
-  const int64_t group = a->heads_q / a->heads_k;
+  const int64_t group = a->heads_q / a->heads_k / shp.hp;   // workgroups per query block and KV head
   int64_t blocks = fa_ceil_div(pairs, 8) * 8 * shp.n_qblocks * group;
-  // Compact work list: at most sum ceil(q_len / BM) <= (T + B (BM - 1)) / BM
+  // Compact work list: at most sum ceil(q_len / bmh) <= (T + B (bmh - 1)) / bmh
   // query blocks per request-ordered KV head.
   shp.compact = 0;
   if (a->batch <= 64 && a->heads_k % 8 == 0) {
-    const int64_t qblocks = (a->total_q + a->batch * (ch.bm - 1)) / ch.bm;
+    const int64_t qblocks = (a->total_q + a->batch * (bmh - 1)) / bmh;
     const int64_t compact = 8 * (a->heads_k / 8) * group * qblocks;
     if (compact < blocks) {
       blocks = compact;
