@@ -191,10 +191,14 @@ struct PrefillShape {
 // One workgroup's share of the compact work list.  XCD x owns KV heads
 // x, x + 8, ... (Hkv a multiple of 8) of every request; requests come in
 // order of decreasing key count (ties by index), and request b contributes
-// m = Hkv / 8 KV heads x ceil(q_len / BM) query blocks x G query heads,
+// m = Hkv / 8 KV heads x ceil(q_len / BMH) query blocks x G workgroups,
 // ordered KV head, then query block heaviest-first, then query head.  Slots
-// past the end of the list get no item.  Lane i evaluates request i (at
-// most 64 requests); every wave computes the same answer.
+// past the end of the list get no item.  Lane l evaluates requests
+// l, l + 64, ... (R per lane: at most 64 R requests); the ranking visits
+// only requests with query blocks (a mixed batch's single-query requests
+// have none).  Every wave computes the same answer.
+constexpr int PF_COMPACT_MAX_BATCH = 256;
+
 struct WorkItem {
   int64_t b;
   int qb, kh, g;
@@ -203,44 +207,59 @@ struct WorkItem {
 
 // BMH: query rows per head of a workgroup; G: workgroups per query block and
 // KV head (the GQA group over the heads packed into one workgroup).
-template <int BMH>
+template <int BMH, int R>
 FA_DEV bool compact_item(const fa_attn_args& a, int slot, int xcd, int lane, int G, WorkItem& w) {
   const int n = (int)a.batch;
-  int qbeg = 0, qlen = 0, klen = -1, kbase = 0;
-  if (lane < n) {
-    qbeg = a.cu_seqlens_q[lane * a.cu_q_stride];
-    qlen = a.cu_seqlens_q[(lane + 1) * a.cu_q_stride] - qbeg;
-    const int kc = a.cu_seqlens_k ? a.cu_seqlens_k[lane * a.cu_k_stride] : 0;
-    kbase = a.page_size ? 0 : kc;
-    klen = a.seqused_k ? a.seqused_k[lane * a.used_k_stride] : a.cu_seqlens_k[(lane + 1) * a.cu_k_stride] - kc;
+  int qbeg[R], qlen[R], klen[R], kbase[R], nqb[R], before[R];
+#pragma unroll
+  for (int c = 0; c < R; ++c) {
+    const int i = lane + 64 * c;
+    qbeg[c] = 0, qlen[c] = 0, klen[c] = -1, kbase[c] = 0, before[c] = 0;
+    if (i < n) {
+      qbeg[c] = a.cu_seqlens_q[i * a.cu_q_stride];
+      qlen[c] = a.cu_seqlens_q[(i + 1) * a.cu_q_stride] - qbeg[c];
+      const int kc = a.cu_seqlens_k ? a.cu_seqlens_k[i * a.cu_k_stride] : 0;
+      kbase[c] = a.page_size ? 0 : kc;
+      klen[c] = a.seqused_k ? a.seqused_k[i * a.used_k_stride] : a.cu_seqlens_k[(i + 1) * a.cu_k_stride] - kc;
+    }
+    const bool skip = (a.flags & FA_FLAG_SKIP_SINGLE_QUERY) && qlen[c] == 1;   // the decode kernel owns it
+    nqb[c] = (i < n && !skip) ? (qlen[c] + BMH - 1) / BMH : 0;
   }
-  const bool skip = (a.flags & FA_FLAG_SKIP_SINGLE_QUERY) && qlen == 1;   // the decode kernel owns it
-  const int nqb = (lane < n && !skip) ? (qlen + BMH - 1) / BMH : 0;
-  int before = 0;   // query blocks of the requests ranked ahead of this one
-  for (int j = 0; j < n; ++j) {
-    const int lj = __builtin_amdgcn_readlane(klen, j);
-    const int nj = __builtin_amdgcn_readlane(nqb, j);
-    before += (lj > klen || (lj == klen && j < lane)) ? nj : 0;
+  // Query blocks of the requests ranked ahead of each of this lane's requests.
+#pragma unroll
+  for (int cj = 0; cj < R; ++cj) {
+    for (uint64_t m = __ballot(nqb[cj] > 0); m; m &= m - 1) {
+      const int lj = __builtin_ctzll(m), j = 64 * cj + lj;
+      const int kj = __builtin_amdgcn_readlane(klen[cj], lj);
+      const int nj = __builtin_amdgcn_readlane(nqb[cj], lj);
+#pragma unroll
+      for (int c = 0; c < R; ++c)
+        before[c] += (kj > klen[c] || (kj == klen[c] && j < lane + 64 * c)) ? nj : 0;
+    }
   }
   const int per_block = (int)(a.heads_k / 8) * G;
-  const int lo = before * per_block;
-  const uint64_t hit = __ballot(lane < n && slot >= lo && slot < lo + nqb * per_block);
-  if (hit == 0) return false;
-  const int i = __builtin_ctzll(hit);
-  const int nq = __builtin_amdgcn_readlane(nqb, i);
-  const int t = slot - __builtin_amdgcn_readlane(lo, i);
-  const int t2 = t % (nq * G);
-  w.b = i;
-  w.kh = xcd + 8 * (t / (nq * G));
-  w.qb = nq - 1 - t2 / G;
-  w.g = t2 % G;
-  w.r.q_begin = __builtin_amdgcn_readlane(qbeg, i);
-  w.r.q_len = __builtin_amdgcn_readlane(qlen, i);
-  w.r.k_len = __builtin_amdgcn_readlane(klen, i);
-  w.r.k_base = __builtin_amdgcn_readlane(kbase, i);
-  w.r.left = 0;
-  w.r.causal = a.causal != 0;
-  return true;
+#pragma unroll
+  for (int c = 0; c < R; ++c) {
+    const int lo = before[c] * per_block;
+    const uint64_t hit = __ballot(nqb[c] > 0 && slot >= lo && slot < lo + nqb[c] * per_block);
+    if (hit == 0) continue;
+    const int l = __builtin_ctzll(hit);
+    const int nq = __builtin_amdgcn_readlane(nqb[c], l);
+    const int t = slot - __builtin_amdgcn_readlane(lo, l);
+    const int t2 = t % (nq * G);
+    w.b = 64 * c + l;
+    w.kh = xcd + 8 * (t / (nq * G));
+    w.qb = nq - 1 - t2 / G;
+    w.g = t2 % G;
+    w.r.q_begin = __builtin_amdgcn_readlane(qbeg[c], l);
+    w.r.q_len = __builtin_amdgcn_readlane(qlen[c], l);
+    w.r.k_len = __builtin_amdgcn_readlane(klen[c], l);
+    w.r.k_base = __builtin_amdgcn_readlane(kbase[c], l);
+    w.r.left = 0;
+    w.r.causal = a.causal != 0;
+    return true;
+  }
+  return false;
 }
 
 // DQ / DV are the tile's head dims (multiples of 64); DQT / DVT <= them are
@@ -292,8 +311,13 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
   WorkItem wi;
   if (shp.compact) {
-    if (!(shp.hp == 2 ? compact_item<BM / 2>(a, slot, xcd, lane, G, wi) : compact_item<BM>(a, slot, xcd, lane, G, wi)))
-      return;
+    bool found;
+    if (a.batch <= 64)
+      found = shp.hp == 2 ? compact_item<BM / 2, 1>(a, slot, xcd, lane, G, wi) : compact_item<BM, 1>(a, slot, xcd, lane, G, wi);
+    else
+      found = shp.hp == 2 ? compact_item<BM / 2, PF_COMPACT_MAX_BATCH / 64>(a, slot, xcd, lane, G, wi)
+                          : compact_item<BM, PF_COMPACT_MAX_BATCH / 64>(a, slot, xcd, lane, G, wi);
+    if (!found) return;
   } else {
     const int per_pair = shp.n_qblocks * G;
     const int64_t pair = (int64_t)(slot / per_pair) * 8 + xcd;

@@ -87,7 +87,7 @@ extern "C" int fa_prefill_fwd(const fa_attn_args* a, void* stream) {
   // Compact work list: at most sum ceil(q_len / bmh) <= (T + B (bmh - 1)) / bmh
   // query blocks per request-ordered KV head.
   shp.compact = 0;
-  if (a->batch <= 64 && a->heads_k % 8 == 0) {
+  if (a->batch <= PF_COMPACT_MAX_BATCH && a->heads_k % 8 == 0) {
     const int64_t qblocks = (a->total_q + a->batch * (bmh - 1)) / bmh;
     const int64_t compact = 8 * (a->heads_k / 8) * group * qblocks;
     if (compact < blocks) {

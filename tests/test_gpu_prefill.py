@@ -224,10 +224,10 @@ def test_mixed_batch_routes_single_queries_to_decode(device, dq, dv):
 @pytest.mark.parametrize("batch,hq,hkv", [(64, 16, 8), (65, 16, 8), (7, 16, 16), (33, 48, 24), (20, 12, 4),
                                           (128, 16, 8), (200, 8, 8), (256, 16, 8), (257, 16, 8)])
 def test_prefill_work_list_modes(device, batch, hq, hkv):
-    """Batches of at most 64 requests with a multiple of 8 KV heads launch the
-    compact work list (longest request first); other shapes, including
-    batches of 65-257 requests, the per-pair grid.  Lengths include empty
-    and one-row requests, and q carries spare rows past the last request."""
+    """Batches of at most 256 requests with a multiple of 8 KV heads launch the
+    compact work list (longest request first; one request per lane up to 64,
+    four beyond); other shapes the per-pair grid.  Lengths include empty and
+    one-row requests, and q carries spare rows past the last request."""
     g = torch.Generator().manual_seed(batch * 100 + hkv)
     q_lens = torch.randint(0, 200, (batch,), generator=g)
     q_lens[::9] = 0
