@@ -270,10 +270,14 @@ FA_DEV bool compact_item(const fa_attn_args& a, int slot, int xcd, int lane, int
 // ignored and the window code folds away.
 // KT: K/V storage type, T or E4M3 (FP8 tiles are staged in LDS and widened
 // exactly to T there; k/v descales scale the scores and the output).
+// ALIBI: linear biases -slope[b][h] |q_pos - k_pos| after the softcap
+// (flash_attn_mps/kernels/attention.metal:47-51, 84-87).
 template <typename T, int DQ, int DV, int W, int NB, int MINB, bool CAUSAL, bool CAP, bool WIN, int DQT = DQ,
-          int DVT = DV, typename KT = T>
+          int DVT = DV, typename KT = T, bool ALIBI = false>
 __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_args a, const PrefillShape shp) {
   constexpr bool FP8 = KT::id == FA_E4M3;
+  constexpr bool LOG2S = CAP || ALIBI;         // phase A leaves scores in log2 units
+  static_assert(!(CAP && ALIBI), "the ALiBi bias scales raw dot products, so it excludes softcap");
   constexpr int KEB = KT::bytes;               // bytes per K/V element
   static_assert(!FP8 || (DQT == DQ && DVT == DV && DQ == DV && (DQ == 64 || DQ == 128 || DQ == 256)),
                 "FP8 K/V tiles: 64/128/256-dim heads");
@@ -550,6 +554,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   const float c_scale = a.softmax_scale * kdsc * LOG2E;   // raw dot -> log2 units
   const float cap_in = CAP ? 2.0f * LOG2E * a.softmax_scale * kdsc / a.softcap : 0.0f;
   const float cap_out = a.softcap * LOG2E;
+  const float slope2 = ALIBI ? a.alibi[b * a.alibi_stride[0] + (int64_t)h * a.alibi_stride[1]] * LOG2E : 0.0f;
   // A sink logit seeds the running state (max = sink, sum = 1) of every row.
   const float sink2 = a.sinks ? a.sinks[(int64_t)h * a.sink_stride] * LOG2E : -INFINITY;
   float m_run[NB], l_run[NB];
@@ -612,6 +617,14 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
           s[nb][i] = cap_out * (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f));
         }
       }
+      if constexpr (ALIBI) {
+        // Score of key t0 + 8 hh + u, u = 16 (i >> 3) + (i & 7): scale and
+        // -slope log2(e) |qa - key| (qd = qa - t0 - 8 hh).
+        const float qd = (float)(wq0 + 32 * nb + l32 + off - st * 32 - 8 * hh);
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          s[nb][i] = fmaf(s[nb][i], c_scale, -slope2 * fabsf(qd - (float)(16 * (i >> 3) + (i & 7))));
+      }
       if constexpr (MASK) {
         // Key t0 + 16 (i >> 3) + 8 hh + (i & 7) is visible iff its offset
         // 16 (i >> 3) + (i & 7) (an inline constant) <= lim.
@@ -630,7 +643,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
 #pragma unroll
       for (int i = 2; i < 16; ++i) mx = fmaxf(mx, s[nb][i]);
       mx = max_hh(mx);
-      const float cand = CAP ? mx : mx * c_scale;
+      const float cand = LOG2S ? mx : mx * c_scale;
       const bool need = commit && cand > m_run[nb] + PF_RESCALE;
       f[nb] = need ? fast_exp2(m_run[nb] - cand) : 1.0f;
       m_run[nb] = need ? cand : m_run[nb];
@@ -639,7 +652,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   };
   // Phase B: probabilities (<= 2^8), row sums, packed B operand of O^T.
   auto phase_b = [&](f32x16 (&s)[NB], u32x4 (&pop)[NB][2]) {
-    const float sc = CAP ? 1.0f : c_scale;
+    const float sc = LOG2S ? 1.0f : c_scale;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       const float mref = m_run[nb] == -INFINITY ? 0.0f : m_run[nb];
@@ -895,10 +908,15 @@ struct PrefillChoice {
   size_t lds;
 };
 
+// score: 0 plain, 1 softcap, 2 ALiBi (without window or softcap).
 template <typename T, int DQ, int DV, bool CAUSAL, typename S, int DQT, int DVT, typename KT>
-PrefillChoice pick_tile(bool cap, bool win) {
+PrefillChoice pick_tile(int score, bool win) {
   PrefillChoice c;
-  if (win)
+  const bool cap = score == 1;
+  if (score == 2) {
+    if (win || KT::id == FA_E4M3) return PrefillChoice{nullptr, 0, 0, 0};
+    c.kern = prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false, false, DQT, DVT, KT, true>;
+  } else if (win)
     c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, true, true, DQT, DVT, KT>
                  : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false, true, DQT, DVT, KT>;
   else
@@ -911,22 +929,22 @@ PrefillChoice pick_tile(bool cap, bool win) {
 }
 
 template <typename T, int DQ, int DV, bool CAUSAL, int DQT, int DVT, typename KT>
-PrefillChoice pick_cap(bool cap, bool wide, bool win) {
+PrefillChoice pick_cap(int score, bool wide, bool win) {
   if constexpr (PrefillTileWide<DQ, DV>::exists) {
     static_assert(32 * PrefillTileWide<DQ, DV>::NB * PrefillTileWide<DQ, DV>::W ==
                       32 * PrefillTile<DQ, DV>::NB * PrefillTile<DQ, DV>::W,
                   "both tiles cover the same query rows per workgroup");
-    if (wide) return pick_tile<T, DQ, DV, CAUSAL, PrefillTileWide<DQ, DV>, DQT, DVT, KT>(cap, win);
+    if (wide) return pick_tile<T, DQ, DV, CAUSAL, PrefillTileWide<DQ, DV>, DQT, DVT, KT>(score, win);
   }
-  return pick_tile<T, DQ, DV, CAUSAL, PrefillTile<DQ, DV>, DQT, DVT, KT>(cap, win);
+  return pick_tile<T, DQ, DV, CAUSAL, PrefillTile<DQ, DV>, DQT, DVT, KT>(score, win);
 }
 
 // (DQ, DV) = the tile; (DQT, DVT) = the tensors' head dims padded into it;
 // KT = the K/V storage type.
 template <typename T, typename KT, int DQ, int DV, int DQT = DQ, int DVT = DV>
-PrefillChoice pick(bool causal, bool cap, bool wide, bool win) {
-  return causal ? pick_cap<T, DQ, DV, true, DQT, DVT, KT>(cap, wide, win)
-                : pick_cap<T, DQ, DV, false, DQT, DVT, KT>(cap, wide, win);
+PrefillChoice pick(bool causal, int score, bool wide, bool win) {
+  return causal ? pick_cap<T, DQ, DV, true, DQT, DVT, KT>(score, wide, win)
+                : pick_cap<T, DQ, DV, false, DQT, DVT, KT>(score, wide, win);
 }
 
 // Head dims of the reference's fast path (flash_attn_mps/_attention.py:149-158:
@@ -936,40 +954,40 @@ PrefillChoice pick(bool causal, bool cap, bool wide, bool win) {
 // query dtype and by head dim (16-bit K/V up to 128 / the rest), so that
 // they compile in parallel.
 template <typename T>
-PrefillChoice pick_dims_small(int64_t dq, int64_t dv, bool causal, bool cap, bool wide, bool win) {
+PrefillChoice pick_dims_small(int64_t dq, int64_t dv, bool causal, int score, bool wide, bool win) {
   if (dq != dv) return PrefillChoice{nullptr, 0, 0, 0};
   switch (dq) {
-    case 32: return pick<T, T, 64, 64, 32, 32>(causal, cap, wide, win);
-    case 64: return pick<T, T, 64, 64>(causal, cap, wide, win);
-    case 72: return pick<T, T, 128, 128, 72, 72>(causal, cap, wide, win);
-    case 80: return pick<T, T, 128, 128, 80, 80>(causal, cap, wide, win);
-    case 96: return pick<T, T, 128, 128, 96, 96>(causal, cap, wide, win);
-    case 128: return pick<T, T, 128, 128>(causal, cap, wide, win);
+    case 32: return pick<T, T, 64, 64, 32, 32>(causal, score, wide, win);
+    case 64: return pick<T, T, 64, 64>(causal, score, wide, win);
+    case 72: return pick<T, T, 128, 128, 72, 72>(causal, score, wide, win);
+    case 80: return pick<T, T, 128, 128, 80, 80>(causal, score, wide, win);
+    case 96: return pick<T, T, 128, 128, 96, 96>(causal, score, wide, win);
+    case 128: return pick<T, T, 128, 128>(causal, score, wide, win);
     default: return PrefillChoice{nullptr, 0, 0, 0};
   }
 }
 
 template <typename T>
-PrefillChoice pick_dims_large(int64_t dq, int64_t dv, bool causal, bool cap, bool wide, bool win, bool fp8) {
+PrefillChoice pick_dims_large(int64_t dq, int64_t dv, bool causal, int score, bool wide, bool win, bool fp8) {
   if (fp8) {
     if (dq != dv) return PrefillChoice{nullptr, 0, 0, 0};
     switch (dq) {
-      case 64: return pick<T, E4M3T, 64, 64>(causal, cap, false, win);
-      case 128: return pick<T, E4M3T, 128, 128>(causal, cap, false, win);
-      case 256: return pick<T, E4M3T, 256, 256>(causal, cap, false, win);
+      case 64: return pick<T, E4M3T, 64, 64>(causal, score, false, win);
+      case 128: return pick<T, E4M3T, 128, 128>(causal, score, false, win);
+      case 256: return pick<T, E4M3T, 256, 256>(causal, score, false, win);
       default: return PrefillChoice{nullptr, 0, 0, 0};
     }
   }
-  if (dq == 192 && dv == 128) return pick<T, T, 192, 128>(causal, cap, wide, win);
-  if (dq == 256 && dv == 256) return pick<T, T, 256, 256>(causal, cap, wide, win);
+  if (dq == 192 && dv == 128) return pick<T, T, 192, 128>(causal, score, wide, win);
+  if (dq == 256 && dv == 256) return pick<T, T, 256, 256>(causal, score, wide, win);
   return PrefillChoice{nullptr, 0, 0, 0};
 }
 
 // Defined in prefill_inst_{bf16,f16}_{small,large}.hip.
-PrefillChoice pick_bf16_small(int64_t dq, int64_t dv, bool causal, bool cap, bool wide, bool win);
-PrefillChoice pick_f16_small(int64_t dq, int64_t dv, bool causal, bool cap, bool wide, bool win);
-PrefillChoice pick_bf16_large(int64_t dq, int64_t dv, bool causal, bool cap, bool wide, bool win, bool fp8);
-PrefillChoice pick_f16_large(int64_t dq, int64_t dv, bool causal, bool cap, bool wide, bool win, bool fp8);
+PrefillChoice pick_bf16_small(int64_t dq, int64_t dv, bool causal, int score, bool wide, bool win);
+PrefillChoice pick_f16_small(int64_t dq, int64_t dv, bool causal, int score, bool wide, bool win);
+PrefillChoice pick_bf16_large(int64_t dq, int64_t dv, bool causal, int score, bool wide, bool win, bool fp8);
+PrefillChoice pick_f16_large(int64_t dq, int64_t dv, bool causal, int score, bool wide, bool win, bool fp8);
 
 }  // namespace fa_prefill
 

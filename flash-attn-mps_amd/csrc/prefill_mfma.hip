@@ -9,15 +9,21 @@ namespace {
 
 using namespace fa_prefill;
 
+bool window_set(const fa_attn_args& a) {
+  return a.window_left >= 0 || (a.causal == 0 && a.window_right >= 0);
+}
+
 PrefillChoice select_prefill(const fa_attn_args& a, bool wide) {
-  const bool causal = a.causal != 0, cap = a.softcap > 0.0f, fp8 = a.k_dtype == FA_E4M3;
+  const bool causal = a.causal != 0, fp8 = a.k_dtype == FA_E4M3;
+  const int score = a.alibi ? 2 : a.softcap > 0.0f ? 1 : 0;   // plain / softcap / ALiBi
   // A right window bounds nothing under causality.
-  const bool win = a.window_left >= 0 || (!causal && a.window_right >= 0);
+  const bool win = window_set(a);
   const int64_t dq = a.head_dim_qk, dv = a.head_dim_v;
   const bool bf16 = a.q_dtype == FA_BF16;
   if (!fp8 && dq <= 128)
-    return bf16 ? pick_bf16_small(dq, dv, causal, cap, wide, win) : pick_f16_small(dq, dv, causal, cap, wide, win);
-  return bf16 ? pick_bf16_large(dq, dv, causal, cap, wide, win, fp8) : pick_f16_large(dq, dv, causal, cap, wide, win, fp8);
+    return bf16 ? pick_bf16_small(dq, dv, causal, score, wide, win) : pick_f16_small(dq, dv, causal, score, wide, win);
+  return bf16 ? pick_bf16_large(dq, dv, causal, score, wide, win, fp8)
+              : pick_f16_large(dq, dv, causal, score, wide, win, fp8);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -34,7 +40,9 @@ bool prefill_ok(const fa_attn_args& a) {
                (dq == 192 && dv == 128))) {
     return false;
   }
-  if (a.leftpad_k || a.alibi) return false;
+  if (a.leftpad_k) return false;
+  // ALiBi (per-head or per-request slopes) without softcap, windows or FP8.
+  if (a.alibi && (a.softcap > 0.0f || window_set(a) || fp8)) return false;
   const int kb = fp8 ? 1 : 2;   // K/V bytes per element
   if (a.mask_kind != 0 || a.causal_by_batch || a.window_left < -1 || a.window_right < -1) return false;
   if (a.num_splits != 1) return false;
