@@ -270,14 +270,14 @@ FA_DEV bool compact_item(const fa_attn_args& a, int slot, int xcd, int lane, int
 // ignored and the window code folds away.
 // KT: K/V storage type, T or E4M3 (FP8 tiles are staged in LDS and widened
 // exactly to T there; k/v descales scale the scores and the output).
-// ALIBI: linear biases -slope[b][h] |q_pos - k_pos| after the softcap
+// ALIBI: linear biases -slope[b][h] |q_pos - k_pos| seeded into the score
+// accumulators (instantiated without softcap, which would come first)
 // (flash_attn_mps/kernels/attention.metal:47-51, 84-87).
 template <typename T, int DQ, int DV, int W, int NB, int MINB, bool CAUSAL, bool CAP, bool WIN, int DQT = DQ,
           int DVT = DV, typename KT = T, bool ALIBI = false>
 __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_args a, const PrefillShape shp) {
   constexpr bool FP8 = KT::id == FA_E4M3;
-  constexpr bool LOG2S = CAP || ALIBI;         // phase A leaves scores in log2 units
-  static_assert(!(CAP && ALIBI), "the ALiBi bias scales raw dot products, so it excludes softcap");
+  static_assert(!(CAP && ALIBI), "the ALiBi bias is added before the softcap would apply");
   constexpr int KEB = KT::bytes;               // bytes per K/V element
   static_assert(!FP8 || (DQT == DQ && DVT == DV && DQ == DV && (DQ == 64 || DQ == 128 || DQ == 256)),
                 "FP8 K/V tiles: 64/128/256-dim heads");
@@ -554,7 +554,11 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   const float c_scale = a.softmax_scale * kdsc * LOG2E;   // raw dot -> log2 units
   const float cap_in = CAP ? 2.0f * LOG2E * a.softmax_scale * kdsc / a.softcap : 0.0f;
   const float cap_out = a.softcap * LOG2E;
-  const float slope2 = ALIBI ? a.alibi[b * a.alibi_stride[0] + (int64_t)h * a.alibi_stride[1]] * LOG2E : 0.0f;
+  // ALiBi slope in raw dot-product units: the score's bias -slope |qa - key|
+  // becomes -sl |qa - key| before the scale (the host requires scale > 0).
+  const float sl = ALIBI ? a.alibi[b * a.alibi_stride[0] + (int64_t)h * a.alibi_stride[1]] /
+                               (a.softmax_scale * kdsc)
+                         : 0.0f;
   // A sink logit seeds the running state (max = sink, sum = 1) of every row.
   const float sink2 = a.sinks ? a.sinks[(int64_t)h * a.sink_stride] * LOG2E : -INFINITY;
   float m_run[NB], l_run[NB];
@@ -587,12 +591,25 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   };
 
   // S^T of one stage: s[nb][i] = score of key 32 st + 16 (i >> 3) + 8 hh + (i & 7).
+  // With ALiBi the accumulators start at the key's bias, so the MFMAs add
+  // the dot product onto it: -sl |x| with x = key - qa, which is sl x on
+  // every key a causal row sees (keys past the row are masked later).
   auto qk = [&](int st, f32x16 (&s)[NB]) {
     const char* kl = kbuf0 + ((st >> 1) & 1) * KTILE + (st & 1) * 32 * 128;
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
+    for (int nb = 0; nb < NB; ++nb) {
+      if constexpr (ALIBI) {
+        const float d = (float)(st * 32 + 8 * hh - (wq0 + 32 * nb + l32 + off));
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s[nb][i] = 0.0f;
+        for (int i = 0; i < 16; ++i) {
+          const float x = d + (float)(16 * (i >> 3) + (i & 7));
+          s[nb][i] = CAUSAL ? sl * x : -sl * fabsf(x);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[nb][i] = 0.0f;
+      }
+    }
 #pragma unroll
     for (int kk = 0; kk < KSTT; ++kk) {
       u32x4 av = lds_read16(kl, krd[kk % 4] + (kk / 4) * PF_GROUP_BYTES);
@@ -617,14 +634,6 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
           s[nb][i] = cap_out * (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f));
         }
       }
-      if constexpr (ALIBI) {
-        // Score of key t0 + 8 hh + u, u = 16 (i >> 3) + (i & 7): scale and
-        // -slope log2(e) |qa - key| (qd = qa - t0 - 8 hh).
-        const float qd = (float)(wq0 + 32 * nb + l32 + off - st * 32 - 8 * hh);
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          s[nb][i] = fmaf(s[nb][i], c_scale, -slope2 * fabsf(qd - (float)(16 * (i >> 3) + (i & 7))));
-      }
       if constexpr (MASK) {
         // Key t0 + 16 (i >> 3) + 8 hh + (i & 7) is visible iff its offset
         // 16 (i >> 3) + (i & 7) (an inline constant) <= lim.
@@ -643,7 +652,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
 #pragma unroll
       for (int i = 2; i < 16; ++i) mx = fmaxf(mx, s[nb][i]);
       mx = max_hh(mx);
-      const float cand = LOG2S ? mx : mx * c_scale;
+      const float cand = CAP ? mx : mx * c_scale;
       const bool need = commit && cand > m_run[nb] + PF_RESCALE;
       f[nb] = need ? fast_exp2(m_run[nb] - cand) : 1.0f;
       m_run[nb] = need ? cand : m_run[nb];
@@ -652,7 +661,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   };
   // Phase B: probabilities (<= 2^8), row sums, packed B operand of O^T.
   auto phase_b = [&](f32x16 (&s)[NB], u32x4 (&pop)[NB][2]) {
-    const float sc = LOG2S ? 1.0f : c_scale;
+    const float sc = CAP ? 1.0f : c_scale;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       const float mref = m_run[nb] == -INFINITY ? 0.0f : m_run[nb];
@@ -913,9 +922,12 @@ template <typename T, int DQ, int DV, bool CAUSAL, typename S, int DQT, int DVT,
 PrefillChoice pick_tile(int score, bool win) {
   PrefillChoice c;
   const bool cap = score == 1;
-  if (score == 2) {
-    if (win || KT::id == FA_E4M3) return PrefillChoice{nullptr, 0, 0, 0};
-    c.kern = prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false, false, DQT, DVT, KT, true>;
+  if (score == 2) {   // ALiBi: 16-bit K/V and no window only
+    if constexpr (KT::id == FA_E4M3) return PrefillChoice{nullptr, 0, 0, 0};
+    else {
+      if (win) return PrefillChoice{nullptr, 0, 0, 0};
+      c.kern = prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false, false, DQT, DVT, KT, true>;
+    }
   } else if (win)
     c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, true, true, DQT, DVT, KT>
                  : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false, true, DQT, DVT, KT>;

@@ -42,7 +42,11 @@ bool prefill_ok(const fa_attn_args& a) {
   }
   if (a.leftpad_k) return false;
   // ALiBi (per-head or per-request slopes) without softcap, windows or FP8.
-  if (a.alibi && (a.softcap > 0.0f || window_set(a) || fp8)) return false;
+  // ALiBi folds into the accumulators in raw dot-product units (slope / scale),
+  // so it needs a positive scale and no descale (FP8-only inputs).
+  if (a.alibi && (a.softcap > 0.0f || window_set(a) || fp8 || !(a.softmax_scale > 0.0f) || a.q_descale ||
+                  a.k_descale))
+    return false;
   const int kb = fp8 ? 1 : 2;   // K/V bytes per element
   if (a.mask_kind != 0 || a.causal_by_batch || a.window_left < -1 || a.window_right < -1) return false;
   if (a.num_splits != 1) return false;
