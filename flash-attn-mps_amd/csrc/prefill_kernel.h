@@ -272,7 +272,7 @@ FA_DEV bool compact_item(const fa_attn_args& a, int slot, int xcd, int lane, int
 // exactly to T there; k/v descales scale the scores and the output).
 // ALIBI: linear biases -slope[b][h] |q_pos - k_pos| seeded into the score
 // accumulators (instantiated without softcap, which would come first)
-// (flash_attn_mps/kernels/attention.metal:47-51, 84-87).
+// (flash_attn_mps/kernels/attention.metal:47-51, 87).
 template <typename T, int DQ, int DV, int W, int NB, int MINB, bool CAUSAL, bool CAP, bool WIN, int DQT = DQ,
           int DVT = DV, typename KT = T, bool ALIBI = false>
 __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_args a, const PrefillShape shp) {
