@@ -256,7 +256,7 @@ FA_DEV bool compact_item(const fa_attn_args& a, int slot, int xcd, int lane, int
     w.r.k_len = __builtin_amdgcn_readlane(klen[c], l);
     w.r.k_base = __builtin_amdgcn_readlane(kbase[c], l);
     w.r.left = 0;
-    w.r.causal = a.causal != 0;
+    w.r.causal = a.causal_by_batch ? a.causal_by_batch[w.b * a.causal_stride] != 0 : a.causal != 0;
     return true;
   }
   return false;
@@ -346,7 +346,9 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // j <= qa + WR (WR >= 0, not causal), j < k_len (flash_attn_mps/kernels/
   // attention.metal:29-45, window kind).  The workgroup's key range follows
   // from its first and last rows.
-  const int WL = WIN ? a.window_left : -1, WR = (WIN && !CAUSAL) ? a.window_right : -1;
+  // Per-request causality (a.causal_by_batch) runs in the non-causal WIN
+  // variant: a causal request is the right window 0.
+  const int WL = WIN ? a.window_left : -1, WR = (WIN && !CAUSAL) ? (r.causal ? 0 : a.window_right) : -1;
   const int qa_first = q0 + off, qa_last = min(q0 + bmh, r.q_len) - 1 + off;
   int kv_end = r.k_len;
   if (CAUSAL) kv_end = min(kv_end, qa_last + 1);

@@ -9,8 +9,9 @@ namespace {
 
 using namespace fa_prefill;
 
+// Windows, or per-request causality (run as a right window of 0 per request).
 bool window_set(const fa_attn_args& a) {
-  return a.window_left >= 0 || (a.causal == 0 && a.window_right >= 0);
+  return a.window_left >= 0 || a.causal_by_batch || (a.causal == 0 && a.window_right >= 0);
 }
 
 PrefillChoice select_prefill(const fa_attn_args& a, bool wide) {
@@ -48,7 +49,7 @@ bool prefill_ok(const fa_attn_args& a) {
                   a.k_descale))
     return false;
   const int kb = fp8 ? 1 : 2;   // K/V bytes per element
-  if (a.mask_kind != 0 || a.causal_by_batch || a.window_left < -1 || a.window_right < -1) return false;
+  if (a.mask_kind != 0 || a.window_left < -1 || a.window_right < -1) return false;
   if (a.num_splits != 1) return false;
   if (a.q_stride[2] != 1 || a.k_stride[3] != 1 || a.v_stride[3] != 1 || a.out_stride[2] != 1) return false;
   if (!aligned16(a.q) || !aligned16(a.k) || !aligned16(a.v) || ((uintptr_t)a.out & 7u)) return false;

@@ -7,7 +7,8 @@ shapes, dtypes, strides, feature flags and the caller's maximum lengths:
 1. one query per request, not deterministic, no ALiBi or mask
    -> split-KV decode (``_decode.decode_attention``; _attention.py:134-147);
 2. bf16/fp16 with the feature set compiled into the MFMA prefill kernel
-   (including ALiBi without softcap, windows or FP8 K/V) -> fa_prefill_fwd (the reference's `fast` route, _attention.py:149-158);
+   (including per-request causality, and ALiBi without softcap, windows,
+   per-request causality or FP8 K/V) -> fa_prefill_fwd (the reference's `fast` route, _attention.py:149-158);
    in a batch of several requests, the single-query ones go to the split-KV
    decode kernel first and fa_prefill_fwd skips them
    (FA_FLAG_SKIP_SINGLE_QUERY);
@@ -119,7 +120,6 @@ def _fast_candidate(q, k, v, out, num_splits, deterministic, causal, window_size
     return (not deterministic and num_splits in (0, 1)
             and q.dtype == out.dtype and q.dtype in (torch.float16, torch.bfloat16)
             and k.dtype == v.dtype and k.dtype in (q.dtype, torch.float8_e4m3fn)
-            and not isinstance(causal, torch.Tensor)
             and mask_mod is None and leftpad_k is None)
 
 
