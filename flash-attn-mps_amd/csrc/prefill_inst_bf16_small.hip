@@ -3,8 +3,8 @@
 
 namespace fa_prefill {
 
-PrefillChoice pick_bf16_small(int64_t dq, int64_t dv, bool causal, int score, bool wide, bool win) {
-  return pick_dims_small<BF16T>(dq, dv, causal, score, wide, win);
+PrefillChoice pick_bf16_small(int64_t dq, int64_t dv, bool causal, int score, bool win) {
+  return pick_dims_small<BF16T>(dq, dv, causal, score, win);
 }
 
 }  // namespace fa_prefill

@@ -897,13 +897,10 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
 template <int DQ, int DV> struct PrefillTile;
 template <> struct PrefillTile<64, 64> { static constexpr int W = 4, NB = 1, MINB = 2; };
 template <> struct PrefillTile<128, 128> { static constexpr int W = FA_PF128_W, NB = FA_PF128_NB, MINB = FA_PF128_MINB; };
-template <> struct PrefillTile<192, 128> { static constexpr int W = 4, NB = 1, MINB = 1; };
-// Large grids of 192/128 heads: two workgroups per CU (2 x 80 KiB of LDS)
-// trade registers for a second wave per SIMD.  Few-workgroup launches keep
-// one workgroup per CU, whose heavy blocks then run at full speed.
-template <int DQ, int DV> struct PrefillTileWide { static constexpr bool exists = false; };
-template <> struct PrefillTileWide<192, 128> { static constexpr bool exists = true; static constexpr int W = 4, NB = 1, MINB = 2; };
-constexpr int64_t PF_WIDE_MIN_BLOCKS = 2048;
+// 192/128: two workgroups per CU (2 x 80 KiB of LDS) trade registers for a
+// second wave per SIMD, at every grid size (one workgroup per CU ran 7-48%
+// slower even on 128-workgroup launches).
+template <> struct PrefillTile<192, 128> { static constexpr int W = 4, NB = 1, MINB = 2; };
 template <> struct PrefillTile<256, 256> { static constexpr int W = 4, NB = 1, MINB = 1; };
 
 template <int DQ, int DV>
@@ -942,23 +939,12 @@ PrefillChoice pick_tile(int score, bool win) {
   return c;
 }
 
-template <typename T, int DQ, int DV, bool CAUSAL, int DQT, int DVT, typename KT>
-PrefillChoice pick_cap(int score, bool wide, bool win) {
-  if constexpr (PrefillTileWide<DQ, DV>::exists) {
-    static_assert(32 * PrefillTileWide<DQ, DV>::NB * PrefillTileWide<DQ, DV>::W ==
-                      32 * PrefillTile<DQ, DV>::NB * PrefillTile<DQ, DV>::W,
-                  "both tiles cover the same query rows per workgroup");
-    if (wide) return pick_tile<T, DQ, DV, CAUSAL, PrefillTileWide<DQ, DV>, DQT, DVT, KT>(score, win);
-  }
-  return pick_tile<T, DQ, DV, CAUSAL, PrefillTile<DQ, DV>, DQT, DVT, KT>(score, win);
-}
-
 // (DQ, DV) = the tile; (DQT, DVT) = the tensors' head dims padded into it;
 // KT = the K/V storage type.
 template <typename T, typename KT, int DQ, int DV, int DQT = DQ, int DVT = DV>
-PrefillChoice pick(bool causal, int score, bool wide, bool win) {
-  return causal ? pick_cap<T, DQ, DV, true, DQT, DVT, KT>(score, wide, win)
-                : pick_cap<T, DQ, DV, false, DQT, DVT, KT>(score, wide, win);
+PrefillChoice pick(bool causal, int score, bool win) {
+  return causal ? pick_tile<T, DQ, DV, true, PrefillTile<DQ, DV>, DQT, DVT, KT>(score, win)
+                : pick_tile<T, DQ, DV, false, PrefillTile<DQ, DV>, DQT, DVT, KT>(score, win);
 }
 
 // Head dims of the reference's fast path (flash_attn_mps/_attention.py:149-158:
@@ -968,40 +954,40 @@ PrefillChoice pick(bool causal, int score, bool wide, bool win) {
 // query dtype and by head dim (16-bit K/V up to 128 / the rest), so that
 // they compile in parallel.
 template <typename T>
-PrefillChoice pick_dims_small(int64_t dq, int64_t dv, bool causal, int score, bool wide, bool win) {
+PrefillChoice pick_dims_small(int64_t dq, int64_t dv, bool causal, int score, bool win) {
   if (dq != dv) return PrefillChoice{nullptr, 0, 0, 0};
   switch (dq) {
-    case 32: return pick<T, T, 64, 64, 32, 32>(causal, score, wide, win);
-    case 64: return pick<T, T, 64, 64>(causal, score, wide, win);
-    case 72: return pick<T, T, 128, 128, 72, 72>(causal, score, wide, win);
-    case 80: return pick<T, T, 128, 128, 80, 80>(causal, score, wide, win);
-    case 96: return pick<T, T, 128, 128, 96, 96>(causal, score, wide, win);
-    case 128: return pick<T, T, 128, 128>(causal, score, wide, win);
+    case 32: return pick<T, T, 64, 64, 32, 32>(causal, score, win);
+    case 64: return pick<T, T, 64, 64>(causal, score, win);
+    case 72: return pick<T, T, 128, 128, 72, 72>(causal, score, win);
+    case 80: return pick<T, T, 128, 128, 80, 80>(causal, score, win);
+    case 96: return pick<T, T, 128, 128, 96, 96>(causal, score, win);
+    case 128: return pick<T, T, 128, 128>(causal, score, win);
     default: return PrefillChoice{nullptr, 0, 0, 0};
   }
 }
 
 template <typename T>
-PrefillChoice pick_dims_large(int64_t dq, int64_t dv, bool causal, int score, bool wide, bool win, bool fp8) {
+PrefillChoice pick_dims_large(int64_t dq, int64_t dv, bool causal, int score, bool win, bool fp8) {
   if (fp8) {
     if (dq != dv) return PrefillChoice{nullptr, 0, 0, 0};
     switch (dq) {
-      case 64: return pick<T, E4M3T, 64, 64>(causal, score, false, win);
-      case 128: return pick<T, E4M3T, 128, 128>(causal, score, false, win);
-      case 256: return pick<T, E4M3T, 256, 256>(causal, score, false, win);
+      case 64: return pick<T, E4M3T, 64, 64>(causal, score, win);
+      case 128: return pick<T, E4M3T, 128, 128>(causal, score, win);
+      case 256: return pick<T, E4M3T, 256, 256>(causal, score, win);
       default: return PrefillChoice{nullptr, 0, 0, 0};
     }
   }
-  if (dq == 192 && dv == 128) return pick<T, T, 192, 128>(causal, score, wide, win);
-  if (dq == 256 && dv == 256) return pick<T, T, 256, 256>(causal, score, wide, win);
+  if (dq == 192 && dv == 128) return pick<T, T, 192, 128>(causal, score, win);
+  if (dq == 256 && dv == 256) return pick<T, T, 256, 256>(causal, score, win);
   return PrefillChoice{nullptr, 0, 0, 0};
 }
 
 // Defined in prefill_inst_{bf16,f16}_{small,large}.hip.
-PrefillChoice pick_bf16_small(int64_t dq, int64_t dv, bool causal, int score, bool wide, bool win);
-PrefillChoice pick_f16_small(int64_t dq, int64_t dv, bool causal, int score, bool wide, bool win);
-PrefillChoice pick_bf16_large(int64_t dq, int64_t dv, bool causal, int score, bool wide, bool win, bool fp8);
-PrefillChoice pick_f16_large(int64_t dq, int64_t dv, bool causal, int score, bool wide, bool win, bool fp8);
+PrefillChoice pick_bf16_small(int64_t dq, int64_t dv, bool causal, int score, bool win);
+PrefillChoice pick_f16_small(int64_t dq, int64_t dv, bool causal, int score, bool win);
+PrefillChoice pick_bf16_large(int64_t dq, int64_t dv, bool causal, int score, bool win, bool fp8);
+PrefillChoice pick_f16_large(int64_t dq, int64_t dv, bool causal, int score, bool win, bool fp8);
 
 }  // namespace fa_prefill
 

@@ -14,7 +14,7 @@ bool window_set(const fa_attn_args& a) {
   return a.window_left >= 0 || a.causal_by_batch || (a.causal == 0 && a.window_right >= 0);
 }
 
-PrefillChoice select_prefill(const fa_attn_args& a, bool wide) {
+PrefillChoice select_prefill(const fa_attn_args& a) {
   const bool causal = a.causal != 0, fp8 = a.k_dtype == FA_E4M3;
   const int score = a.alibi ? 2 : a.softcap > 0.0f ? 1 : 0;   // plain / softcap / ALiBi
   // A right window bounds nothing under causality.
@@ -22,9 +22,9 @@ PrefillChoice select_prefill(const fa_attn_args& a, bool wide) {
   const int64_t dq = a.head_dim_qk, dv = a.head_dim_v;
   const bool bf16 = a.q_dtype == FA_BF16;
   if (!fp8 && dq <= 128)
-    return bf16 ? pick_bf16_small(dq, dv, causal, score, wide, win) : pick_f16_small(dq, dv, causal, score, wide, win);
-  return bf16 ? pick_bf16_large(dq, dv, causal, score, wide, win, fp8)
-              : pick_f16_large(dq, dv, causal, score, wide, win, fp8);
+    return bf16 ? pick_bf16_small(dq, dv, causal, score, win) : pick_f16_small(dq, dv, causal, score, win);
+  return bf16 ? pick_bf16_large(dq, dv, causal, score, win, fp8)
+              : pick_f16_large(dq, dv, causal, score, win, fp8);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -84,7 +84,7 @@ extern "C" int fa_prefill_fwd(const fa_attn_args* a, void* stream) {
   }
   if (a->total_q == 0) return FA_OK;
   FA_REQUIRE(a->max_seqlen_q >= 1, "fa_prefill_fwd: max_seqlen_q must be positive");
-  PrefillChoice ch = select_prefill(*a, false);
+  PrefillChoice ch = select_prefill(*a);
   PrefillShape shp;
   // Query heads per workgroup: two heads of a KV head share each workgroup's
   // K/V tiles when the GQA group is even.
@@ -109,9 +109,6 @@ extern "C" int fa_prefill_fwd(const fa_attn_args* a, void* stream) {
     }
   }
   FA_REQUIRE(blocks <= 0x7fffffffll, "fa_prefill_fwd: grid too large");
-  // Workgroups of real work are about Hq x T / BM (empty slots of the grid
-  // and single-query requests of a mixed batch exit at once).
-  if (a->heads_q * fa_ceil_div(a->total_q, ch.bm) >= PF_WIDE_MIN_BLOCKS) ch = select_prefill(*a, true);
   hipError_t err = hipFuncSetAttribute((const void*)ch.kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ch.lds);
   if (err != hipSuccess) {
     fa_set_error("fa_prefill_fwd: cannot reserve %zu bytes of LDS: %s", ch.lds, hipGetErrorString(err));
