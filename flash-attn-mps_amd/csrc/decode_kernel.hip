@@ -523,6 +523,7 @@ using DecodeKernel = void (*)(fa_attn_args, int);
 template <typename CT, typename KT, typename VT, int D, int DV, bool CAP, int DT = D, int DVT = DV>
 DecodeKernel pick_group(int gt) {
   switch (gt) {
+    case 8: if constexpr (D == 128 && DV == 128) return decode_kernel<CT, KT, VT, D, DV, 8, CAP, DT, DVT>; else return nullptr;
     case 4: if constexpr (4 * (D + DV) <= 64 * 16) return decode_kernel<CT, KT, VT, D, DV, 4, CAP, DT, DVT>; else return nullptr;
     case 2: if constexpr (2 * (D + DV) <= 64 * 16) return decode_kernel<CT, KT, VT, D, DV, 2, CAP, DT, DVT>; else return nullptr;
     case 1: return decode_kernel<CT, KT, VT, D, DV, 1, CAP, DT, DVT>;
@@ -566,10 +567,14 @@ DecodeKernel pick_dims(int64_t d, int64_t dv, int gt, bool cap) {
 int elem_size(int dt) { return dt == FA_F32 ? 4 : dt == FA_E4M3 ? 1 : 2; }
 
 // Largest query-head group sharing one KV head that keeps q + accumulators
-// within 64 fp32 registers per lane.
+// within 64 fp32 registers per lane.  128-dim tiles also take a group of 8
+// (128 registers): as two groups of 4, each workgroup reads the KV head
+// again (Hq/Hkv = 64/8 at d128: 3.5 -> 4.4 TB/s).  64-dim tiles keep 4: at 8
+// the occupancy halves and decode slows by 15%.
 int decode_group_tile(const fa_attn_args& a) {
   const int64_t group = a.heads_q / a.heads_k;
   const int64_t per = (decode_tile_dim(a.head_dim_qk) + decode_tile_dim(a.head_dim_v)) / 16;
+  if (per == 16 && group % 8 == 0) return 8;
   for (int gt = 4; gt >= 1; gt >>= 1)
     if (group % gt == 0 && gt * per <= 64) return gt;
   return 1;

@@ -43,6 +43,8 @@ def decode_group_tile(heads, kvheads, dq, dv):
     """Query heads per workgroup; must match decode_group_tile() in decode_kernel.hip."""
     group = heads // kvheads
     per = (_tile_dim(dq) + _tile_dim(dv)) // 16
+    if per == 16 and group % 8 == 0:
+        return 8
     for gt in (4, 2, 1):
         if group % gt == 0 and gt * per <= 64:
             return gt

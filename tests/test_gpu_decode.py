@@ -4,7 +4,7 @@ Ports flash_attn_mps tests/test_decode.py:8-174: packed dims, paged +
 leftpad + strided views + poisoned tails for several split counts and page
 sizes, GQA/MQA, empty queries/KV, independent dtypes with broadcast
 descales, paged FP8 with sinks/windows/softcap, sinks counted once, growing
-KV and large split counts.
+KV and large split counts; groups of 8 and 16 query heads per KV head.
 """
 import pytest
 import torch
@@ -286,3 +286,42 @@ def test_decode_padded_head_dims(device, d, dtype, splits):
     torch.testing.assert_close(actual.cpu().double(), expected, atol=2e-3 if qdt == torch.float16 else 1e-2, rtol=0)
     torch.testing.assert_close(lse.cpu().double(), el, atol=1e-4, rtol=0)
     assert torch.all(ost[..., d:] == 7.0)
+
+
+@pytest.mark.parametrize("d", [80, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("heads,kvheads", [(64, 8), (32, 2)])
+@pytest.mark.parametrize("splits", [0, 1])
+def test_decode_group_of_eight(device, d, dtype, heads, kvheads, splits):
+    """128-dim tiles run 8 query heads of one KV head per workgroup (groups of
+    16 take two such workgroups): paged, NaN-poisoned spare pages, sinks,
+    softcap, FP8 descales, empty and single-key requests."""
+    from flash_attn_mps_amd._decode import decode_group_tile
+    assert decode_group_tile(heads, kvheads, d, d) == 8
+    g = torch.Generator().manual_seed(heads + d + splits)
+    lengths = [1, 300, 2049, 0, 77]
+    page = 16
+    cols = max((n + page - 1) // page for n in lengths) + 1
+    pool = len(lengths) * cols + 1
+    table = torch.randperm(pool - 1, generator=g)[:len(lengths) * cols].int().reshape(len(lengths), cols)
+    table[:, -1] = pool - 1
+    kc = torch.randn(pool, page, kvheads, d, generator=g)
+    vc = torch.randn(pool, page, kvheads, d, generator=g)
+    kc[pool - 1] = float("nan")
+    vc[pool - 1] = float("nan")
+    kc, vc = kc.to(dtype).to(device), vc.to(dtype).to(device)
+    q = torch.randn(len(lengths), heads, d, generator=g).to(torch.bfloat16).to(device)
+    cq = torch.arange(len(lengths) + 1, device=device, dtype=torch.int32)
+    used = torch.tensor(lengths, device=device, dtype=torch.int32)
+    table = table.to(device)
+    sinks = torch.linspace(-2, 2, heads, device=device)
+    fp8 = dtype == torch.float8_e4m3fn
+    ks = torch.rand(len(lengths), kvheads, generator=g).add(0.5).to(device) if fp8 else None
+    vs = torch.rand(len(lengths), kvheads, generator=g).add(0.5).to(device) if fp8 else None
+    out, lse = decode_attention(q, kc, vc, cu_seqlens_q=cq, seqused_k=used, max_seqlen_k=cols * page,
+                                block_table=table, num_splits=splits, softcap=20.0, s_aux=sinks,
+                                k_descale=ks, v_descale=vs)
+    expected, el = attention_reference(q, kc, vc, cq, used_k=used, block_table=table, sinks=sinks,
+                                       softcap=20.0, k_descale=ks, v_descale=vs)
+    assert_attention_close(out, expected, torch.bfloat16)
+    torch.testing.assert_close(lse.cpu().double(), el, atol=1e-4, rtol=2e-5)
