@@ -208,8 +208,11 @@ int fa_rotary(const fa_rotary_args* args, void* stream);
 int fa_decode_supported(const fa_attn_args* args);
 int fa_decode_fwd(const fa_attn_args* args, void* stream);
 
-/* MFMA prefill (bf16/fp16).  fa_prefill_supported() says whether the
- * argument combination is compiled in.  With FA_FLAG_SKIP_SINGLE_QUERY in
+/* MFMA prefill (bf16/fp16 queries; bf16/fp16 or FP8 E4M3 K/V with
+ * descales; causal, per-request causal, windows, softcap, sinks, and ALiBi
+ * without softcap, windows, per-request causality or FP8; head dims 32-256
+ * and 192/128).  fa_prefill_supported() says whether the argument
+ * combination is compiled in.  With FA_FLAG_SKIP_SINGLE_QUERY in
  * args->flags, requests with one query row are left untouched for
  * fa_decode_fwd (no reference counterpart: the reference runs such rows
  * through its prefill tile, flash_attn_mps/_attention.py:149-158). */
