@@ -188,12 +188,15 @@ struct PrefillShape {
   int hp;          // query heads per workgroup (1 or 2, dividing the GQA group): W / hp waves per head
 };
 
-// One workgroup's share of the compact work list.  XCD x owns KV heads
-// x, x + 8, ... (Hkv a multiple of 8) of every request; requests come in
-// order of decreasing key count (ties by index), and request b contributes
-// m = Hkv / 8 KV heads x ceil(q_len / BMH) query blocks x G workgroups,
-// ordered KV head, then query block heaviest-first, then query head.  Slots
-// past the end of the list get no item.  Lane l evaluates requests
+// One workgroup's share of the compact work list.  With Hkv a multiple of 8,
+// XCD x owns KV heads x, x + 8, ... of every request; with Hkv dividing 8,
+// S = 8 / Hkv XCDs share KV head x % Hkv and XCD x takes every S-th query
+// block of it (counted from the heaviest, phase x / Hkv), so every XCD still
+// sees every request.  Requests come in order of decreasing key count (ties
+// by index), and request b contributes m = max(Hkv / 8, 1) KV heads x the
+// XCD's query blocks x G workgroups, ordered KV head, then query block
+// heaviest-first, then query head.  Slots past the end of the list get no
+// item.  Lane l evaluates requests
 // l, l + 64, ... (R per lane: at most 64 R requests); the ranking visits
 // only requests with query blocks (a mixed batch's single-query requests
 // have none).  Every wave computes the same answer.
@@ -210,7 +213,8 @@ struct WorkItem {
 template <int BMH, int R>
 FA_DEV bool compact_item(const fa_attn_args& a, int slot, int xcd, int lane, int G, WorkItem& w) {
   const int n = (int)a.batch;
-  int qbeg[R], qlen[R], klen[R], kbase[R], nqb[R], before[R];
+  const int S = a.heads_k % 8 == 0 ? 1 : 8 / (int)a.heads_k, ph = xcd / (8 / S);   // XCDs per KV head, phase
+  int qbeg[R], qlen[R], klen[R], kbase[R], nqb[R], nqx[R], before[R];
 #pragma unroll
   for (int c = 0; c < R; ++c) {
     const int i = lane + 64 * c;
@@ -224,32 +228,33 @@ FA_DEV bool compact_item(const fa_attn_args& a, int slot, int xcd, int lane, int
     }
     const bool skip = (a.flags & FA_FLAG_SKIP_SINGLE_QUERY) && qlen[c] == 1;   // the decode kernel owns it
     nqb[c] = (i < n && !skip) ? (qlen[c] + BMH - 1) / BMH : 0;
+    nqx[c] = nqb[c] > ph ? (nqb[c] - ph + S - 1) / S : 0;   // this XCD's blocks of the request
   }
   // Query blocks of the requests ranked ahead of each of this lane's requests.
 #pragma unroll
   for (int cj = 0; cj < R; ++cj) {
-    for (uint64_t m = __ballot(nqb[cj] > 0); m; m &= m - 1) {
+    for (uint64_t m = __ballot(nqx[cj] > 0); m; m &= m - 1) {
       const int lj = __builtin_ctzll(m), j = 64 * cj + lj;
       const int kj = __builtin_amdgcn_readlane(klen[cj], lj);
-      const int nj = __builtin_amdgcn_readlane(nqb[cj], lj);
+      const int nj = __builtin_amdgcn_readlane(nqx[cj], lj);
 #pragma unroll
       for (int c = 0; c < R; ++c)
         before[c] += (kj > klen[c] || (kj == klen[c] && j < lane + 64 * c)) ? nj : 0;
     }
   }
-  const int per_block = (int)(a.heads_k / 8) * G;
+  const int per_block = (S == 1 ? (int)(a.heads_k / 8) : 1) * G;
 #pragma unroll
   for (int c = 0; c < R; ++c) {
     const int lo = before[c] * per_block;
-    const uint64_t hit = __ballot(nqb[c] > 0 && slot >= lo && slot < lo + nqb[c] * per_block);
+    const uint64_t hit = __ballot(nqx[c] > 0 && slot >= lo && slot < lo + nqx[c] * per_block);
     if (hit == 0) continue;
     const int l = __builtin_ctzll(hit);
-    const int nq = __builtin_amdgcn_readlane(nqb[c], l);
+    const int nq = __builtin_amdgcn_readlane(nqb[c], l), nx = __builtin_amdgcn_readlane(nqx[c], l);
     const int t = slot - __builtin_amdgcn_readlane(lo, l);
-    const int t2 = t % (nq * G);
+    const int t2 = t % (nx * G);
     w.b = 64 * c + l;
-    w.kh = xcd + 8 * (t / (nq * G));
-    w.qb = nq - 1 - t2 / G;
+    w.kh = S == 1 ? xcd + 8 * (t / (nx * G)) : xcd % (int)a.heads_k;
+    w.qb = nq - 1 - (ph + S * (t2 / G));
     w.g = t2 % G;
     w.r.q_begin = __builtin_amdgcn_readlane(qbeg[c], l);
     w.r.q_len = __builtin_amdgcn_readlane(qlen[c], l);

@@ -98,11 +98,15 @@ extern "C" int fa_prefill_fwd(const fa_attn_args* a, void* stream) {
   const int64_t group = a->heads_q / a->heads_k / shp.hp;   // workgroups per query block and KV head
   int64_t blocks = fa_ceil_div(pairs, 8) * 8 * shp.n_qblocks * group;
   // Compact work list: at most sum ceil(q_len / bmh) <= (T + B (bmh - 1)) / bmh
-  // query blocks per request-ordered KV head.
+  // query blocks per request-ordered KV head; with Hkv dividing 8, an XCD
+  // takes every S-th block of one KV head: at most sum ceil(n_b / S)
+  // <= (qblocks + B (S - 1)) / S of them.
   shp.compact = 0;
-  if (a->batch <= PF_COMPACT_MAX_BATCH && a->heads_k % 8 == 0) {
+  if (a->batch <= PF_COMPACT_MAX_BATCH && (a->heads_k % 8 == 0 || 8 % a->heads_k == 0)) {
     const int64_t qblocks = (a->total_q + a->batch * (bmh - 1)) / bmh;
-    const int64_t compact = 8 * (a->heads_k / 8) * group * qblocks;
+    const int64_t S = a->heads_k % 8 == 0 ? 1 : 8 / a->heads_k;
+    const int64_t per_xcd = S == 1 ? (a->heads_k / 8) * qblocks : (qblocks + a->batch * (S - 1)) / S;
+    const int64_t compact = 8 * group * per_xcd;
     if (compact < blocks) {
       blocks = compact;
       shp.compact = 1;
