@@ -188,14 +188,14 @@ struct PrefillShape {
   int hp;          // query heads per workgroup (1 or 2, dividing the GQA group): W / hp waves per head
 };
 
-// One workgroup's share of the compact work list.  With Hkv a multiple of 8,
-// XCD x owns KV heads x, x + 8, ... of every request; with Hkv dividing 8,
-// S = 8 / Hkv XCDs share KV head x % Hkv and XCD x takes every S-th query
-// block of it (counted from the heaviest, phase x / Hkv), so every XCD still
-// sees every request.  Requests come in order of decreasing key count (ties
-// by index), and request b contributes m = max(Hkv / 8, 1) KV heads x the
-// XCD's query blocks x G workgroups, ordered KV head, then query block
-// heaviest-first, then query head.  Slots past the end of the list get no
+// One workgroup's share of the compact work list.  With g = gcd(Hkv, 8),
+// XCD x owns the m = Hkv / g KV heads congruent to x mod g of every request,
+// and the S = 8 / g XCDs that share those heads take every S-th query block
+// of each (counted from the heaviest, phase x / g): Hkv a multiple of 8
+// gives heads x, x + 8, ... and S = 1; every XCD sees every request.
+// Requests come in order of decreasing key count (ties by index), and
+// request b contributes m KV heads x the XCD's query blocks x G workgroups,
+// ordered KV head, then query block heaviest-first, then query head.  Slots past the end of the list get no
 // item.  Lane l evaluates requests
 // l, l + 64, ... (R per lane: at most 64 R requests); the ranking visits
 // only requests with query blocks (a mixed batch's single-query requests
@@ -213,7 +213,8 @@ struct WorkItem {
 template <int BMH, int R>
 FA_DEV bool compact_item(const fa_attn_args& a, int slot, int xcd, int lane, int G, WorkItem& w) {
   const int n = (int)a.batch;
-  const int S = a.heads_k % 8 == 0 ? 1 : 8 / (int)a.heads_k, ph = xcd / (8 / S);   // XCDs per KV head, phase
+  const int hk = (int)a.heads_k, gk = hk % 8 == 0 ? 8 : hk % 4 == 0 ? 4 : hk % 2 == 0 ? 2 : 1;   // gcd(Hkv, 8)
+  const int S = 8 / gk, ph = xcd / gk;   // XCDs sharing a KV head, this XCD's phase
   int qbeg[R], qlen[R], klen[R], kbase[R], nqb[R], nqx[R], before[R];
 #pragma unroll
   for (int c = 0; c < R; ++c) {
@@ -242,7 +243,7 @@ FA_DEV bool compact_item(const fa_attn_args& a, int slot, int xcd, int lane, int
         before[c] += (kj > klen[c] || (kj == klen[c] && j < lane + 64 * c)) ? nj : 0;
     }
   }
-  const int per_block = (S == 1 ? (int)(a.heads_k / 8) : 1) * G;
+  const int per_block = (hk / gk) * G;
 #pragma unroll
   for (int c = 0; c < R; ++c) {
     const int lo = before[c] * per_block;
@@ -253,7 +254,7 @@ FA_DEV bool compact_item(const fa_attn_args& a, int slot, int xcd, int lane, int
     const int t = slot - __builtin_amdgcn_readlane(lo, l);
     const int t2 = t % (nx * G);
     w.b = 64 * c + l;
-    w.kh = S == 1 ? xcd + 8 * (t / (nx * G)) : xcd % (int)a.heads_k;
+    w.kh = xcd % gk + gk * (t / (nx * G));
     w.qb = nq - 1 - (ph + S * (t2 / G));
     w.g = t2 % G;
     w.r.q_begin = __builtin_amdgcn_readlane(qbeg[c], l);

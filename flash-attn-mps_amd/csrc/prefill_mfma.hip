@@ -97,15 +97,16 @@ extern "C" int fa_prefill_fwd(const fa_attn_args* a, void* stream) {
   const int64_t pairs = a->batch * a->heads_k;
   const int64_t group = a->heads_q / a->heads_k / shp.hp;   // workgroups per query block and KV head
   int64_t blocks = fa_ceil_div(pairs, 8) * 8 * shp.n_qblocks * group;
-  // Compact work list: at most sum ceil(q_len / bmh) <= (T + B (bmh - 1)) / bmh
-  // query blocks per request-ordered KV head; with Hkv dividing 8, an XCD
-  // takes every S-th block of one KV head: at most sum ceil(n_b / S)
-  // <= (qblocks + B (S - 1)) / S of them.
+  // Compact work list: requests hold at most sum ceil(q_len / bmh) <=
+  // (T + B (bmh - 1)) / bmh query blocks per KV head; an XCD owns Hkv / g KV
+  // heads (g = gcd(Hkv, 8)) and every S-th block of each (S = 8 / g): at most
+  // sum ceil(n_b / S) <= (qblocks + B (S - 1)) / S blocks per head.
   shp.compact = 0;
-  if (a->batch <= PF_COMPACT_MAX_BATCH && (a->heads_k % 8 == 0 || 8 % a->heads_k == 0)) {
+  if (a->batch <= PF_COMPACT_MAX_BATCH) {
     const int64_t qblocks = (a->total_q + a->batch * (bmh - 1)) / bmh;
-    const int64_t S = a->heads_k % 8 == 0 ? 1 : 8 / a->heads_k;
-    const int64_t per_xcd = S == 1 ? (a->heads_k / 8) * qblocks : (qblocks + a->batch * (S - 1)) / S;
+    const int64_t hk = a->heads_k, gk = hk % 8 == 0 ? 8 : hk % 4 == 0 ? 4 : hk % 2 == 0 ? 2 : 1;
+    const int64_t S = 8 / gk;
+    const int64_t per_xcd = (hk / gk) * ((qblocks + a->batch * (S - 1)) / S);
     const int64_t compact = 8 * group * per_xcd;
     if (compact < blocks) {
       blocks = compact;

@@ -228,12 +228,13 @@ def test_mixed_batch_routes_single_queries_to_decode(device, dq, dv):
 
 @pytest.mark.parametrize("batch,hq,hkv", [(64, 16, 8), (65, 16, 8), (7, 16, 16), (33, 48, 24), (20, 12, 4),
                                           (128, 16, 8), (200, 8, 8), (256, 16, 8), (257, 16, 8), (50, 16, 2),
-                                          (9, 8, 1), (100, 28, 4), (257, 8, 2), (33, 12, 3)])
+                                          (9, 8, 1), (100, 28, 4), (257, 8, 2), (33, 12, 3), (45, 36, 12),
+                                          (21, 30, 6)])
 def test_prefill_work_list_modes(device, batch, hq, hkv):
-    """Batches of at most 256 requests with a multiple of 8 KV heads, or 1, 2
-    or 4 KV heads (8 / Hkv XCDs share a KV head, each taking every
-    (8 / Hkv)-th query block), launch the compact work list (longest request
-    first; one request per lane up to 64, four beyond); other shapes the
+    """Batches of at most 256 requests launch the compact work list (longest
+    request first; one request per lane up to 64, four beyond): with
+    g = gcd(Hkv, 8), each XCD owns Hkv / g KV heads and 8 / g XCDs share
+    them, each taking every (8 / g)-th query block.  Larger batches take the
     per-pair grid.  Lengths include empty and
     one-row requests, and q carries spare rows past the last request."""
     g = torch.Generator().manual_seed(batch * 100 + hkv)
