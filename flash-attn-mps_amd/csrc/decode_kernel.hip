@@ -161,9 +161,12 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, rg = lane >> 4, l16 = lane & 15;
   const RequestInfo r = load_request(a, b);
   if (r.q_len != 1) return;
-  const int group = (int)(a.heads_q / a.heads_k);
-  const int h0 = blockIdx.x * GT;
-  const int kh = h0 / group;
+  // Workgroup x holds query heads t GT .. t GT + GT - 1 of KV head kh's group
+  // (t = x % tiles, tiles = ceil(group / GT)); a last tile past the group
+  // recomputes its last real head in the spare slots and stores nothing there.
+  const int group = (int)(a.heads_q / a.heads_k), tiles = (group + GT - 1) / GT;
+  const int kh = blockIdx.x / tiles, t0 = (blockIdx.x % tiles) * GT;
+  const int h0 = kh * group + t0, nreal = min(GT, group - t0);
   const int vis_begin = decode_vis_begin(a, r.k_len);
   const int begin = vis_begin + split * span;
   const int end = min(r.k_len, begin + span);
@@ -180,7 +183,7 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
   uint32_t qp[GT][EK / 2];
 #pragma unroll
   for (int g = 0; g < GT; ++g) {
-    const int64_t q0 = tq * a.q_stride[0] + (int64_t)(h0 + g) * a.q_stride[1];
+    const int64_t q0 = tq * a.q_stride[0] + (int64_t)(h0 + min(g, nreal - 1)) * a.q_stride[1];
     if (a.q_stride[2] == 1) {
       load_words<EK * 2>((const char*)a.q + (q0 + min(l16, LK - 1) * EK) * 2, qp[g]);
     } else {
@@ -200,7 +203,7 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
   const bool seed = a.sinks && split == 0 && wave == 0 && rg == 0;
 #pragma unroll
   for (int g = 0; g < GT; ++g) {
-    m[g] = seed ? a.sinks[(int64_t)(h0 + g) * a.sink_stride] * LOG2E : -INFINITY;
+    m[g] = seed ? a.sinks[(int64_t)(h0 + min(g, nreal - 1)) * a.sink_stride] * LOG2E : -INFINITY;
     l[g] = seed ? 1.0f : 0.0f;
 #pragma unroll
     for (int e = 0; e < EV; ++e) acc[g][e] = 0.0f;
@@ -415,7 +418,7 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
     }
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < GT * DVT; idx += DEC_THREADS) {
+  for (int idx = threadIdx.x; idx < nreal * DVT; idx += DEC_THREADS) {
     const int g = idx / DVT, d = idx - g * DVT;
     float M = sm_m[0][g];
 #pragma unroll
@@ -566,18 +569,22 @@ DecodeKernel pick_dims(int64_t d, int64_t dv, int gt, bool cap) {
 
 int elem_size(int dt) { return dt == FA_F32 ? 4 : dt == FA_E4M3 ? 1 : 2; }
 
-// Largest query-head group sharing one KV head that keeps q + accumulators
-// within 64 fp32 registers per lane.  128-dim tiles also take a group of 8
-// (128 registers): as two groups of 4, each workgroup reads the KV head
-// again (Hq/Hkv = 64/8 at d128: 3.5 -> 4.4 TB/s).  64-dim tiles keep 4: at 8
-// the occupancy halves and decode slows by 15%.
+// Query heads per workgroup (GT).  Every workgroup of a KV head reads it
+// again, so GT is the smallest power of two that reaches the fewest
+// workgroups per KV head, ceil(group / gmax), where gmax keeps q +
+// accumulators within 64 fp32 registers per lane, or 128 for 128-dim tiles
+// (GT = 8: Hq/Hkv = 64/8 at d128 went 3.5 -> 4.4 TB/s; 64-dim tiles at 8
+// halve the occupancy and run 15% slower).  A group that GT does not divide
+// ends in a partial tile.
 int decode_group_tile(const fa_attn_args& a) {
   const int64_t group = a.heads_q / a.heads_k;
   const int64_t per = (decode_tile_dim(a.head_dim_qk) + decode_tile_dim(a.head_dim_v)) / 16;
-  if (per == 16 && group % 8 == 0) return 8;
-  for (int gt = 4; gt >= 1; gt >>= 1)
-    if (group % gt == 0 && gt * per <= 64) return gt;
-  return 1;
+  int gmax = per == 16 ? 8 : 1;
+  while (gmax < 4 && 2 * gmax * per <= 64) gmax *= 2;
+  const int64_t tiles = (group + gmax - 1) / gmax;
+  int gt = 1;
+  while ((group + gt - 1) / gt > tiles) gt *= 2;
+  return gt;
 }
 
 bool chunk_aligned(const void* p, const int64_t* st, int nstrides, int esz, int bytes_per_lane) {
@@ -643,7 +650,7 @@ extern "C" int fa_decode_fwd(const fa_attn_args* a, void* stream) {
   FA_REQUIRE(a->split_span >= 1, "fa_decode_fwd: split_span must be positive");
   FA_REQUIRE(a->num_splits == 1 || (a->partial_out && a->partial_lse), "fa_decode_fwd: splits need partial buffers");
   FA_REQUIRE(a->batch <= 65535, "fa_decode_fwd: batch exceeds the grid limit");
-  const int64_t head_groups = a->heads_q / gt;
+  const int64_t head_groups = a->heads_k * fa_ceil_div(a->heads_q / a->heads_k, gt);
   FA_REQUIRE(a->num_splits <= 65535, "fa_decode_fwd: too many splits");
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)head_groups, (unsigned)a->num_splits, (unsigned)a->batch);

@@ -128,8 +128,8 @@ def _decode_rows(args, batch, heads, kvheads, dq, dv, max_seqlen_k, device, keep
     mixed batch (it skips every other request); True if it ran."""
     if not _lib.supported("fa_decode_supported", args):
         return False
-    from ._decode import decode_group_tile, split_plan
-    groups = heads // decode_group_tile(heads, kvheads, dq, dv)
+    from ._decode import decode_workgroups_per_token, split_plan
+    groups = decode_workgroups_per_token(heads, kvheads, dq, dv)
     splits, span = split_plan(batch, groups, max_seqlen_k, 0)
     args.num_splits, args.split_span = splits, span
     if splits > 1:

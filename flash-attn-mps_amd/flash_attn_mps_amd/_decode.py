@@ -43,12 +43,19 @@ def decode_group_tile(heads, kvheads, dq, dv):
     """Query heads per workgroup; must match decode_group_tile() in decode_kernel.hip."""
     group = heads // kvheads
     per = (_tile_dim(dq) + _tile_dim(dv)) // 16
-    if per == 16 and group % 8 == 0:
-        return 8
-    for gt in (4, 2, 1):
-        if group % gt == 0 and gt * per <= 64:
-            return gt
-    return 1
+    gmax = 8 if per == 16 else 1
+    while gmax < 4 and 2 * gmax * per <= 64:
+        gmax *= 2
+    tiles = -(-group // gmax)
+    gt = 1
+    while -(-group // gt) > tiles:
+        gt *= 2
+    return gt
+
+
+def decode_workgroups_per_token(heads, kvheads, dq, dv):
+    """Workgroups per (request, split): KV heads x ceil(group / GT)."""
+    return kvheads * -(-(heads // kvheads) // decode_group_tile(heads, kvheads, dq, dv))
 
 
 def decode_attention(q, k, v, *, cu_seqlens_q, cu_seqlens_k=None, seqused_k=None,
@@ -83,7 +90,7 @@ def decode_attention(q, k, v, *, cu_seqlens_q, cu_seqlens_k=None, seqused_k=None
                       q_descale=q_descale, k_descale=k_descale, v_descale=v_descale,
                       mask_mod=None, aux_tensors=None, leftpad_k=leftpad_k, keep=keep)
     if _lib.supported("fa_decode_supported", args):
-        groups = heads // decode_group_tile(heads, kvheads, dq, dv)
+        groups = decode_workgroups_per_token(heads, kvheads, dq, dv)
         splits, span = split_plan(batch, groups, effective_max, num_splits)
         args.num_splits, args.split_span = splits, span
         if splits > 1:

@@ -4,7 +4,8 @@ Ports flash_attn_mps tests/test_decode.py:8-174: packed dims, paged +
 leftpad + strided views + poisoned tails for several split counts and page
 sizes, GQA/MQA, empty queries/KV, independent dtypes with broadcast
 descales, paged FP8 with sinks/windows/softcap, sinks counted once, growing
-KV and large split counts; groups of 8 and 16 query heads per KV head.
+KV and large split counts; query-head groups of 4 to 16 per KV head,
+including groups the head tile does not divide.
 """
 import pytest
 import torch
@@ -288,16 +289,17 @@ def test_decode_padded_head_dims(device, d, dtype, splits):
     assert torch.all(ost[..., d:] == 7.0)
 
 
-@pytest.mark.parametrize("d", [80, 128])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
-@pytest.mark.parametrize("heads,kvheads", [(64, 8), (32, 2)])
+@pytest.mark.parametrize("heads,kvheads,d,gt", [(64, 8, 128, 8), (32, 2, 80, 8), (40, 8, 128, 8), (28, 4, 96, 8),
+                                                (12, 2, 128, 8), (14, 2, 64, 4), (10, 2, 64, 4), (24, 8, 128, 4)])
 @pytest.mark.parametrize("splits", [0, 1])
-def test_decode_group_of_eight(device, d, dtype, heads, kvheads, splits):
-    """128-dim tiles run 8 query heads of one KV head per workgroup (groups of
-    16 take two such workgroups): paged, NaN-poisoned spare pages, sinks,
-    softcap, FP8 descales, empty and single-key requests."""
+def test_decode_head_tiles(device, dtype, heads, kvheads, d, gt, splits):
+    """GT query heads of one KV head per workgroup: 8 for 128-dim tiles and 4
+    for 64-dim ones; groups of 16 take two workgroups, groups of 5, 6 or 7 end
+    in a partial tile whose spare slots store nothing.  Paged, NaN-poisoned
+    spare pages, sinks, softcap, FP8 descales, empty and single-key requests."""
     from flash_attn_mps_amd._decode import decode_group_tile
-    assert decode_group_tile(heads, kvheads, d, d) == 8
+    assert decode_group_tile(heads, kvheads, d, d) == gt
     g = torch.Generator().manual_seed(heads + d + splits)
     lengths = [1, 300, 2049, 0, 77]
     page = 16
@@ -318,10 +320,12 @@ def test_decode_group_of_eight(device, d, dtype, heads, kvheads, splits):
     fp8 = dtype == torch.float8_e4m3fn
     ks = torch.rand(len(lengths), kvheads, generator=g).add(0.5).to(device) if fp8 else None
     vs = torch.rand(len(lengths), kvheads, generator=g).add(0.5).to(device) if fp8 else None
+    storage = torch.full((len(lengths), heads + 8, d), 7.0, device=device, dtype=torch.bfloat16)
     out, lse = decode_attention(q, kc, vc, cu_seqlens_q=cq, seqused_k=used, max_seqlen_k=cols * page,
                                 block_table=table, num_splits=splits, softcap=20.0, s_aux=sinks,
-                                k_descale=ks, v_descale=vs)
+                                k_descale=ks, v_descale=vs, out=storage[:, :heads])
     expected, el = attention_reference(q, kc, vc, cq, used_k=used, block_table=table, sinks=sinks,
                                        softcap=20.0, k_descale=ks, v_descale=vs)
     assert_attention_close(out, expected, torch.bfloat16)
     torch.testing.assert_close(lse.cpu().double(), el, atol=1e-4, rtol=2e-5)
+    assert torch.all(storage[:, heads:] == 7.0), "a spare head slot was stored"
