@@ -141,7 +141,8 @@ FA_DEV int decode_vis_begin(const fa_attn_args& a, int k_len) {
 // past the real dims read the row's last real chunk (always in bounds), with
 // a zero query there, so they add nothing to Q.K; their V columns are never
 // stored.
-template <typename CT, typename KT, typename VT, int D, int DV, int GT, bool CAP, int DT = D, int DVT = DV>
+template <typename CT, typename KT, typename VT, int D, int DV, int GT, bool CAP, int DT = D, int DVT = DV,
+          bool ALIBI = false>
 __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const fa_attn_args a, const int span) {
   constexpr int EK = D / 16, EV = DV / 16;
   constexpr int LK = DT / EK, LV = DVT / EV;   // lanes of a 16-lane row holding real dims
@@ -178,6 +179,20 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
                        descale_of(a.k_descale, a.k_descale_stride, b, kh) * (CAP ? 1.0f : LOG2E);
   const float cap_in = CAP ? 2.0f * LOG2E / a.softcap : 0.0f, cap_out = a.softcap * LOG2E;
   const float vscale = descale_of(a.v_descale, a.v_descale_stride, b, kh);
+  // ALiBi: -slope |q_pos - key| in log2 units after the softcap
+  // (flash_attn_mps/kernels/attention.metal:47-51); the query sits at key
+  // position k_len - 1, storage row qrow, so the bias is slope (row - qrow).
+  // The slopes are wave-uniform: kept in scalar registers.  A template flag,
+  // so kernels without ALiBi keep their registers (a runtime test cost the
+  // eight-head tiles 7%).
+  float slope2[GT];
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    const float sl =
+        ALIBI ? a.alibi[b * a.alibi_stride[0] + (int64_t)(h0 + min(g, nreal - 1)) * a.alibi_stride[1]] * LOG2E : 0.0f;
+    slope2[g] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sl)));
+  }
+  const int qrow = r.k_base + r.left + r.k_len - 1;
 
   // Query pairs of this lane's dims (l16 * EK ..), unscaled, in the compute type.
   uint32_t qp[GT][EK / 2];
@@ -327,6 +342,7 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
       for (int i = 0; i < NT; ++i) {
         float v = row16_sum(s[g][i]) * sscale;
         if constexpr (CAP) v = cap_out * (1.0f - 2.0f * __builtin_amdgcn_rcpf(fast_exp2(v * cap_in) + 1.0f));
+        if constexpr (ALIBI) v = fmaf(slope2[g], (float)(rp + i - qrow), v);
         s[g][i] = v;
       }
     if (!full) {
@@ -523,30 +539,30 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const fa_attn_args a,
 
 using DecodeKernel = void (*)(fa_attn_args, int);
 
-template <typename CT, typename KT, typename VT, int D, int DV, bool CAP, int DT = D, int DVT = DV>
+template <typename CT, typename KT, typename VT, int D, int DV, bool CAP, bool ALIBI, int DT = D, int DVT = DV>
 DecodeKernel pick_group(int gt) {
   switch (gt) {
-    case 8: if constexpr (D == 128 && DV == 128) return decode_kernel<CT, KT, VT, D, DV, 8, CAP, DT, DVT>; else return nullptr;
-    case 4: if constexpr (4 * (D + DV) <= 64 * 16) return decode_kernel<CT, KT, VT, D, DV, 4, CAP, DT, DVT>; else return nullptr;
-    case 2: if constexpr (2 * (D + DV) <= 64 * 16) return decode_kernel<CT, KT, VT, D, DV, 2, CAP, DT, DVT>; else return nullptr;
-    case 1: return decode_kernel<CT, KT, VT, D, DV, 1, CAP, DT, DVT>;
+    case 8: if constexpr (D == 128 && DV == 128) return decode_kernel<CT, KT, VT, D, DV, 8, CAP, DT, DVT, ALIBI>; else return nullptr;
+    case 4: if constexpr (4 * (D + DV) <= 64 * 16) return decode_kernel<CT, KT, VT, D, DV, 4, CAP, DT, DVT, ALIBI>; else return nullptr;
+    case 2: if constexpr (2 * (D + DV) <= 64 * 16) return decode_kernel<CT, KT, VT, D, DV, 2, CAP, DT, DVT, ALIBI>; else return nullptr;
+    case 1: return decode_kernel<CT, KT, VT, D, DV, 1, CAP, DT, DVT, ALIBI>;
     default: return nullptr;
   }
 }
 
 // Head dims 32 and 72/80/96 (dq == dv) run in the 64- and 128-dim tiles.
-template <typename CT, typename KT, typename VT, bool CAP>
+template <typename CT, typename KT, typename VT, bool CAP, bool ALIBI>
 DecodeKernel pick_dims_cap(int64_t d, int64_t dv, int gt) {
-  if (d == 192 && dv == 128) return pick_group<CT, KT, VT, 192, 128, CAP>(gt);
+  if (d == 192 && dv == 128) return pick_group<CT, KT, VT, 192, 128, CAP, ALIBI>(gt);
   if (d != dv) return nullptr;
   switch (d) {
-    case 32: return pick_group<CT, KT, VT, 64, 64, CAP, 32, 32>(gt);
-    case 64: return pick_group<CT, KT, VT, 64, 64, CAP>(gt);
-    case 72: return pick_group<CT, KT, VT, 128, 128, CAP, 72, 72>(gt);
-    case 80: return pick_group<CT, KT, VT, 128, 128, CAP, 80, 80>(gt);
-    case 96: return pick_group<CT, KT, VT, 128, 128, CAP, 96, 96>(gt);
-    case 128: return pick_group<CT, KT, VT, 128, 128, CAP>(gt);
-    case 256: return pick_group<CT, KT, VT, 256, 256, CAP>(gt);
+    case 32: return pick_group<CT, KT, VT, 64, 64, CAP, ALIBI, 32, 32>(gt);
+    case 64: return pick_group<CT, KT, VT, 64, 64, CAP, ALIBI>(gt);
+    case 72: return pick_group<CT, KT, VT, 128, 128, CAP, ALIBI, 72, 72>(gt);
+    case 80: return pick_group<CT, KT, VT, 128, 128, CAP, ALIBI, 80, 80>(gt);
+    case 96: return pick_group<CT, KT, VT, 128, 128, CAP, ALIBI, 96, 96>(gt);
+    case 128: return pick_group<CT, KT, VT, 128, 128, CAP, ALIBI>(gt);
+    case 256: return pick_group<CT, KT, VT, 256, 256, CAP, ALIBI>(gt);
     default: return nullptr;
   }
 }
@@ -563,8 +579,10 @@ int64_t decode_tile_dim(int64_t d) {
 }
 
 template <typename CT, typename KT, typename VT>
-DecodeKernel pick_dims(int64_t d, int64_t dv, int gt, bool cap) {
-  return cap ? pick_dims_cap<CT, KT, VT, true>(d, dv, gt) : pick_dims_cap<CT, KT, VT, false>(d, dv, gt);
+DecodeKernel pick_dims(int64_t d, int64_t dv, int gt, bool cap, bool alibi) {
+  // ALiBi variants exist without softcap only (softcap + ALiBi: generic kernel).
+  if (alibi) return cap ? nullptr : pick_dims_cap<CT, KT, VT, false, true>(d, dv, gt);
+  return cap ? pick_dims_cap<CT, KT, VT, true, false>(d, dv, gt) : pick_dims_cap<CT, KT, VT, false, false>(d, dv, gt);
 }
 
 int elem_size(int dt) { return dt == FA_F32 ? 4 : dt == FA_E4M3 ? 1 : 2; }
@@ -597,7 +615,7 @@ bool chunk_aligned(const void* p, const int64_t* st, int nstrides, int esz, int 
 
 DecodeKernel select_decode(const fa_attn_args& a, int* gt_out) {
   if (a.k_dtype != a.v_dtype) return nullptr;
-  if (a.mask_kind != 0 || a.alibi) return nullptr;
+  if (a.mask_kind != 0) return nullptr;
   if (a.page_size && a.page_size % DEC_PAGE_ALIGN) return nullptr;
   // Page and row strides are 32-bit byte counts in the kernel's addressing.
   for (int i = 0; i < 3; ++i)
@@ -618,13 +636,13 @@ DecodeKernel select_decode(const fa_attn_args& a, int* gt_out) {
   if (a.q_stride[2] == 1 && !chunk_aligned(a.q, a.q_stride, 2, 2, (int)(tq / 16) * 2)) return nullptr;
   const int gt = decode_group_tile(a);
   *gt_out = gt;
-  const bool qbf = a.q_dtype == FA_BF16, cap = a.softcap > 0.0f;
+  const bool qbf = a.q_dtype == FA_BF16, cap = a.softcap > 0.0f, alibi = a.alibi != nullptr;
   const int64_t dq = a.head_dim_qk, dv = a.head_dim_v;
   switch (a.k_dtype) {
-    case FA_BF16: return qbf ? pick_dims<BF16T, BF16T, BF16T>(dq, dv, gt, cap) : nullptr;
-    case FA_F16: return qbf ? nullptr : pick_dims<F16T, F16T, F16T>(dq, dv, gt, cap);
+    case FA_BF16: return qbf ? pick_dims<BF16T, BF16T, BF16T>(dq, dv, gt, cap, alibi) : nullptr;
+    case FA_F16: return qbf ? nullptr : pick_dims<F16T, F16T, F16T>(dq, dv, gt, cap, alibi);
     case FA_E4M3:
-      return qbf ? pick_dims<BF16T, E4M3T, E4M3T>(dq, dv, gt, cap) : pick_dims<F16T, E4M3T, E4M3T>(dq, dv, gt, cap);
+      return qbf ? pick_dims<BF16T, E4M3T, E4M3T>(dq, dv, gt, cap, alibi) : pick_dims<F16T, E4M3T, E4M3T>(dq, dv, gt, cap, alibi);
     default: return nullptr;
   }
 }

@@ -4,8 +4,9 @@ score tensor, no read of device values.
 Counterpart of flash_attn_mps/_attention.py:88-238.  The route depends only on
 shapes, dtypes, strides, feature flags and the caller's maximum lengths:
 
-1. one query per request, not deterministic, no ALiBi or mask
-   -> split-KV decode (``_decode.decode_attention``; _attention.py:134-147);
+1. one query per request, not deterministic, no mask -> split-KV decode
+   (``_decode.decode_attention``; _attention.py:134-147, which also keeps
+   ALiBi off that route);
 2. bf16/fp16 with the feature set compiled into the MFMA prefill kernel
    (including per-request causality, and ALiBi without softcap, windows,
    per-request causality or FP8 K/V) -> fa_prefill_fwd (the reference's `fast` route, _attention.py:149-158);
@@ -187,7 +188,7 @@ def attention(q, k, v, *, cu_seqlens_q, cu_seqlens_k=None, seqused_k=None, max_s
     batch = cu_seqlens_q.numel() - 1
     if batch < 1:
         raise ValueError("cu_seqlens_q must contain at least two offsets")
-    if (max_seqlen_q == 1 and not deterministic and alibi_slopes is None and mask_mod is None):
+    if max_seqlen_q == 1 and not deterministic and mask_mod is None:
         # A single right-aligned query has no future keys, whatever `causal` says.
         from ._decode import decode_attention
         return decode_attention(
@@ -195,7 +196,7 @@ def attention(q, k, v, *, cu_seqlens_q, cu_seqlens_k=None, seqused_k=None, max_s
             seqused_k=seqused_k, max_seqlen_k=max_seqlen_k, block_table=block_table,
             softmax_scale=softmax_scale, out=out, leftpad_k=leftpad_k, num_splits=num_splits,
             s_aux=s_aux, q_descale=q_descale, k_descale=k_descale, v_descale=v_descale,
-            window_size=window_size, softcap=softcap,
+            window_size=window_size, softcap=softcap, alibi_slopes=alibi_slopes,
         )
     lse = torch.empty((heads, tokens), device=q.device, dtype=torch.float32)
     keep = []

@@ -61,12 +61,14 @@ def decode_workgroups_per_token(heads, kvheads, dq, dv):
 def decode_attention(q, k, v, *, cu_seqlens_q, cu_seqlens_k=None, seqused_k=None,
                      max_seqlen_k, block_table=None, softmax_scale=None, out=None,
                      leftpad_k=None, num_splits=0, s_aux=None, q_descale=None,
-                     k_descale=None, v_descale=None, window_size=(-1, -1), softcap=0.):
+                     k_descale=None, v_descale=None, window_size=(-1, -1), softcap=0.,
+                     alibi_slopes=None):
     """Attend one query per nonempty request, returning output and natural LSE.
 
     The caller supplies valid GPU sequence metadata with cu_seqlens_q
     differences in {0, 1}.  K/V are packed or paged, head dimensions lie in
     1..512.  FP8 descales, sinks, left windows and softcap run in the kernel.
+    ALiBi slopes ([Hq] or [B, Hq]) add -slope |k_len - 1 - key| in the kernel.
     Public validation belongs to interface._run and the attention dispatcher.
     """
     tokens, heads, dq = q.shape
@@ -86,7 +88,7 @@ def decode_attention(q, k, v, *, cu_seqlens_q, cu_seqlens_k=None, seqused_k=None
     args = build_args(q, k, v, out, lse, cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_seqlens_k,
                       seqused_k=seqused_k, max_seqlen_q=1, max_seqlen_k=max_seqlen_k,
                       block_table=block_table, softmax_scale=softmax_scale, causal=False,
-                      window_size=window_size, alibi_slopes=None, softcap=softcap, s_aux=s_aux,
+                      window_size=window_size, alibi_slopes=alibi_slopes, softcap=softcap, s_aux=s_aux,
                       q_descale=q_descale, k_descale=k_descale, v_descale=v_descale,
                       mask_mod=None, aux_tensors=None, leftpad_k=leftpad_k, keep=keep)
     if _lib.supported("fa_decode_supported", args):

@@ -5,7 +5,7 @@ leftpad + strided views + poisoned tails for several split counts and page
 sizes, GQA/MQA, empty queries/KV, independent dtypes with broadcast
 descales, paged FP8 with sinks/windows/softcap, sinks counted once, growing
 KV and large split counts; query-head groups of 4 to 16 per KV head,
-including groups the head tile does not divide.
+including groups the head tile does not divide; ALiBi slopes.
 """
 import pytest
 import torch
@@ -329,3 +329,44 @@ def test_decode_head_tiles(device, dtype, heads, kvheads, d, gt, splits):
     assert_attention_close(out, expected, torch.bfloat16)
     torch.testing.assert_close(lse.cpu().double(), el, atol=1e-4, rtol=2e-5)
     assert torch.all(storage[:, heads:] == 7.0), "a spare head slot was stored"
+
+
+@pytest.mark.parametrize("heads,kvheads,d", [(32, 8, 128), (40, 8, 128), (14, 2, 64), (16, 8, 256)])
+@pytest.mark.parametrize("per_request", [False, True])
+@pytest.mark.parametrize("splits", [0, 1])
+def test_decode_alibi(device, heads, kvheads, d, per_request, splits):
+    """ALiBi on the decode kernel: the single query sits at key k_len - 1, so
+    key j gets -slope (k_len - 1 - j); [Hq] or [B, Hq] slopes, with leftpad,
+    a left window, sinks and split counts, through the public route
+    (attention -> decode_attention).  ALiBi with softcap stays on the generic
+    kernel."""
+    from flash_attn_mps_amd._attention import attention, build_args
+    g = torch.Generator().manual_seed(heads + d + per_request)
+    lengths, left = [1, 300, 2049, 0, 77], [0, 5, 0, 0, 3]
+    page = 16
+    cols = max((n + page - 1) // page for n in lengths) + 1
+    pool = len(lengths) * cols
+    table = torch.randperm(pool, generator=g).int().reshape(len(lengths), cols).to(device)
+    kc = torch.randn(pool, page, kvheads, d, generator=g).to(torch.bfloat16).to(device)
+    vc = torch.randn(pool, page, kvheads, d, generator=g).to(torch.bfloat16).to(device)
+    q = torch.randn(len(lengths), heads, d, generator=g).to(torch.bfloat16).to(device)
+    cq = torch.arange(len(lengths) + 1, device=device, dtype=torch.int32)
+    used = torch.tensor([n + p for n, p in zip(lengths, left)], device=device, dtype=torch.int32)
+    lp = torch.tensor(left, device=device, dtype=torch.int32)
+    shape = (len(lengths), heads) if per_request else (heads,)
+    slopes = (torch.rand(shape, generator=g) * 0.2).to(device)
+    sinks = torch.linspace(-1, 1, heads, device=device)
+    kw = dict(cu_seqlens_q=cq, seqused_k=used, max_seqlen_q=1, max_seqlen_k=cols * page, block_table=table,
+              alibi_slopes=slopes, softcap=0.0, window_size=(1000, 0), s_aux=sinks, leftpad_k=lp,
+              num_splits=splits)
+    keep = []
+    probe = build_args(q, kc, vc, torch.empty_like(q), torch.empty(heads, len(lengths), device=device), keep=keep,
+                       causal=False, softmax_scale=None, q_descale=None, k_descale=None, v_descale=None,
+                       mask_mod=None, aux_tensors=None, cu_seqlens_k=None,
+                       **{k: v for k, v in kw.items() if k not in ("s_aux", "num_splits")}, s_aux=sinks)
+    assert _lib.supported("fa_decode_supported", probe)
+    out, lse = attention(q, kc, vc, causal=True, **kw)
+    expected, el = attention_reference(q, kc, vc, cq, used_k=used, block_table=table, leftpad=left,
+                                       alibi=slopes, window=(1000, 0), sinks=sinks)
+    assert_attention_close(out, expected, torch.bfloat16)
+    torch.testing.assert_close(lse.cpu().double(), el, atol=1e-4, rtol=2e-5)
