@@ -1,0 +1,521 @@
+// Single-query split-KV decode over packed or paged K/V, plus the split merge.
+//
+// Semantics follow flash_attn_mps/_decode.py:40-99 and
+// flash_attn_mps/kernels/attention_decode.metal:18-207: one query per request,
+// keys [vis_begin, len) with vis_begin = len - window_left - 1 under a left
+// window, scores scaled by softmax_scale * q_descale * k_descale, softcap on
+// the scaled score, the sink seeding (max, sum) = (sink, 1) of split 0 only,
+// the output multiplied by v_descale, fp32 partial states merged by
+// log-sum-exp.
+//
+// gfx950 layout.  A workgroup (4 waves) owns one (request, group of GT query
+// heads sharing a KV head, split of `span` keys).  Every 16-lane row of a wave
+// owns NT consecutive key positions per step and spreads the head dimension
+// over its 16 lanes, so a 256-byte K or V head row is one coalesced 16-lane
+// access of 16-byte loads.  A wave step covers 4 rows x NT positions; the
+// wave's next step is STEP * 4 positions further (the 4 waves interleave).
+// * The K/V loads of step t+1 are issued before step t is computed (two
+//   register buffers), so every wave keeps one step of K/V in flight while
+//   it does arithmetic.
+// * Block-table entries for 64 steps are loaded once per wave into lanes
+//   (lane 4u + row holds the page of step u's row) and handed to the rows
+//   with ds_bpermute: no dependent table load inside the loop.
+// * Loads are unconditional: positions outside the split clamp to the row's
+//   first/last valid position (rows with none read the split's first key),
+//   and their scores are masked to -inf, so V is finite and p = 0.
+// * Q.K runs on packed pairs with v_dot2_f32_bf16 / v_dot2_f32_f16 (FP8 K
+//   converts exactly to the query's 16-bit type with v_cvt_scalef32_pk_*);
+//   the softmax scale is applied to the reduced score.  P.V is fp32 FMA.
+// * exp2 online softmax per row whose running max moves only when a step
+//   raises it by more than 2^8 (probabilities stay <= 256); rows combine
+//   with lane shuffles and waves through LDS at the end.
+#pragma once
+#include "attn_common.h"
+
+namespace fa_decode {
+
+constexpr int DEC_THREADS = 256;
+constexpr int DEC_PAGE_ALIGN = 8;   // paged K/V needs P % 8 == 0
+#ifndef FA_DEC_MINB
+#define FA_DEC_MINB 2
+#endif
+constexpr float DEC_RESCALE = 8.0f;
+
+typedef __attribute__((ext_vector_type(2))) __bf16 dec_bf16x2;
+typedef __attribute__((ext_vector_type(2))) _Float16 dec_f16x2;
+
+// Positions per 16-lane row per step: 4, or 2 for K+V row pairs of 64 bytes
+// per lane or more (keeps two register buffers within budget).
+template <int KB, int VB>
+struct DecodeRows {
+  static constexpr int value = KB + VB >= 64 ? 2 : 4;
+};
+
+template <int BYTES>
+struct LoadChunk {
+  static constexpr int value = BYTES % 16 == 0 ? 16 : BYTES % 8 == 0 ? 8 : 4;
+};
+
+template <int BYTES>
+FA_DEV void load_words(const char* p, uint32_t (&w)[BYTES / 4]) {
+  constexpr int C = LoadChunk<BYTES>::value;
+#pragma unroll
+  for (int c = 0; c < BYTES / C; ++c) {
+    if constexpr (C == 16) {
+      const uint4 v = *(const uint4*)(p + 16 * c);
+      w[4 * c] = v.x; w[4 * c + 1] = v.y; w[4 * c + 2] = v.z; w[4 * c + 3] = v.w;
+    } else if constexpr (C == 8) {
+      const uint2 v = *(const uint2*)(p + 8 * c);
+      w[2 * c] = v.x; w[2 * c + 1] = v.y;
+    } else {
+      w[c] = *(const uint32_t*)(p + 4 * c);
+    }
+  }
+}
+
+template <typename T, int N>
+FA_DEV void words_to_f32(const uint32_t* w, float* f) {
+  if constexpr (T::id == FA_BF16) {
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+      f[2 * i] = __uint_as_float(w[i] << 16);
+      f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  } else if constexpr (T::id == FA_F16) {
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+      f[2 * i] = f16_bits_to_f32(w[i] & 0xffffu);
+      f[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
+    }
+  } else {
+    static_assert(T::id == FA_E4M3, "V element type");
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], false);
+      const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], true);
+      f[4 * i] = lo[0]; f[4 * i + 1] = lo[1]; f[4 * i + 2] = hi[0]; f[4 * i + 3] = hi[1];
+    }
+  }
+}
+
+// c + a.lo * b.lo + a.hi * b.hi on packed 16-bit pairs, fp32 result.
+template <typename CT> FA_DEV float dot2(uint32_t a, uint32_t b, float c);
+template <> FA_DEV float dot2<BF16T>(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(dec_bf16x2, a), __builtin_bit_cast(dec_bf16x2, b), c, false);
+}
+template <> FA_DEV float dot2<F16T>(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(dec_f16x2, a), __builtin_bit_cast(dec_f16x2, b), c, false);
+}
+
+// K row words -> EK/2 packed pairs of the compute type (FP8 widens exactly).
+template <typename CT, typename KT, int EK>
+FA_DEV void k_pairs(const uint32_t* w, uint32_t* p) {
+  if constexpr (KT::id == FA_E4M3) {
+#pragma unroll
+    for (int i = 0; i < EK / 4; ++i) {
+      if constexpr (CT::id == FA_BF16) {
+        p[2 * i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[i], 1.0f, false));
+        p[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[i], 1.0f, true));
+      } else {
+        p[2 * i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[i], 1.0f, false));
+        p[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[i], 1.0f, true));
+      }
+    }
+  } else {
+    static_assert(KT::id == CT::id, "16-bit K must match the compute type");
+#pragma unroll
+    for (int i = 0; i < EK / 2; ++i) p[i] = w[i];
+  }
+}
+
+template <typename CT>
+FA_DEV uint32_t pack_pair_bits(float lo, float hi) {
+  if constexpr (CT::id == FA_BF16) return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+  else return (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
+}
+
+FA_DEV int decode_vis_begin(const fa_attn_args& a, int k_len) {
+  return a.window_left >= 0 ? max(0, k_len - a.window_left - 1) : 0;
+}
+
+// D / DV: the tile's head dims; DT / DVT <= them: the tensors' own.  Lanes
+// past the real dims read the row's last real chunk (always in bounds), with
+// a zero query there, so they add nothing to Q.K; their V columns are never
+// stored.
+template <typename CT, typename KT, typename VT, int D, int DV, int GT, bool CAP, int DT = D, int DVT = DV,
+          bool ALIBI = false>
+__global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const fa_attn_args a, const int span) {
+  constexpr int EK = D / 16, EV = DV / 16;
+  constexpr int LK = DT / EK, LV = DVT / EV;   // lanes of a 16-lane row holding real dims
+  static_assert(DT % EK == 0 && DVT % EV == 0 && DT <= D && DVT <= DV, "true head dims fill whole lane chunks");
+  constexpr int KB = EK * KT::bytes, VB = EV * VT::bytes;
+  constexpr int NT = DecodeRows<KB, VB>::value;
+  constexpr int STEP = 4 * NT;          // positions of one wave step
+  constexpr int WSTRIDE = 4 * STEP;     // positions between a wave's consecutive steps
+  static_assert(EK % 4 == 0 && EV % 4 == 0 && KB % 4 == 0 && VB % 4 == 0, "decode tile shape");
+  __shared__ float sm_m[4][GT], sm_l[4][GT];
+  __shared__ float sm_acc[4][GT][DV];
+
+  // Head groups are the fastest grid dimension: the workgroups of one
+  // (request, split) run together and read whole token rows of the same pages.
+  const int split = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, rg = lane >> 4, l16 = lane & 15;
+  const RequestInfo r = load_request(a, b);
+  if (r.q_len != 1) return;
+  // Workgroup x holds query heads t GT .. t GT + GT - 1 of KV head kh's group
+  // (t = x % tiles, tiles = ceil(group / GT)); a last tile past the group
+  // recomputes its last real head in the spare slots and stores nothing there.
+  const int group = (int)(a.heads_q / a.heads_k), tiles = (group + GT - 1) / GT;
+  const int kh = blockIdx.x / tiles, t0 = (blockIdx.x % tiles) * GT;
+  const int h0 = kh * group + t0, nreal = min(GT, group - t0);
+  const int vis_begin = decode_vis_begin(a, r.k_len);
+  const int begin = vis_begin + split * span;
+  const int end = min(r.k_len, begin + span);
+  if (split > 0 && begin >= end) return;
+  const int64_t tq = r.q_begin;
+  const int S = a.num_splits;
+
+  const float sscale = a.softmax_scale * descale_of(a.q_descale, a.q_descale_stride, b, kh) *
+                       descale_of(a.k_descale, a.k_descale_stride, b, kh) * (CAP ? 1.0f : LOG2E);
+  const float cap_in = CAP ? 2.0f * LOG2E / a.softcap : 0.0f, cap_out = a.softcap * LOG2E;
+  const float vscale = descale_of(a.v_descale, a.v_descale_stride, b, kh);
+  // ALiBi: -slope |q_pos - key| in log2 units after the softcap
+  // (flash_attn_mps/kernels/attention.metal:47-51); the query sits at key
+  // position k_len - 1, storage row qrow, so the bias is slope (row - qrow).
+  // The slopes are wave-uniform: kept in scalar registers.  A template flag,
+  // so kernels without ALiBi keep their registers (a runtime test cost the
+  // eight-head tiles 7%).
+  float slope2[GT];
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    const float sl =
+        ALIBI ? a.alibi[b * a.alibi_stride[0] + (int64_t)(h0 + min(g, nreal - 1)) * a.alibi_stride[1]] * LOG2E : 0.0f;
+    slope2[g] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sl)));
+  }
+  const int qrow = r.k_base + r.left + r.k_len - 1;
+
+  // Query pairs of this lane's dims (l16 * EK ..), unscaled, in the compute type.
+  uint32_t qp[GT][EK / 2];
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    const int64_t q0 = tq * a.q_stride[0] + (int64_t)(h0 + min(g, nreal - 1)) * a.q_stride[1];
+    if (a.q_stride[2] == 1) {
+      load_words<EK * 2>((const char*)a.q + (q0 + min(l16, LK - 1) * EK) * 2, qp[g]);
+    } else {
+      const int lq = min(l16, LK - 1);
+#pragma unroll
+      for (int j = 0; j < EK / 2; ++j)
+        qp[g][j] = pack_pair_bits<CT>(load_elem<CT>(a.q, q0 + (int64_t)(lq * EK + 2 * j) * a.q_stride[2]),
+                                      load_elem<CT>(a.q, q0 + (int64_t)(lq * EK + 2 * j + 1) * a.q_stride[2]));
+    }
+    if (LK < 16 && l16 >= LK) {
+#pragma unroll
+      for (int j = 0; j < EK / 2; ++j) qp[g][j] = 0u;   // padding dims: no contribution to Q.K
+    }
+  }
+
+  float m[GT], l[GT], acc[GT][EV];
+  const bool seed = a.sinks && split == 0 && wave == 0 && rg == 0;
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    m[g] = seed ? a.sinks[(int64_t)(h0 + min(g, nreal - 1)) * a.sink_stride] * LOG2E : -INFINITY;
+    l[g] = seed ? 1.0f : 0.0f;
+#pragma unroll
+    for (int e = 0; e < EV; ++e) acc[g][e] = 0.0f;
+  }
+
+  // Storage positions [plo, phi) of this split (packed rows or paged slots).
+  const int plo = r.k_base + r.left + begin, phi = r.k_base + r.left + end;
+  const int P = (int)a.page_size;
+  const int sb0 = (plo & ~(STEP - 1)) + STEP * wave;
+  const int nsteps = (begin < end && sb0 < phi) ? (phi - 1 - sb0) / WSTRIDE + 1 : 0;
+
+  // Byte addressing.  Row r of page blk of KV head kh, dims from l16 * E:
+  // base + blk * page_stride + r * row_stride + kh * head_stride + l16 * E * bytes.
+  const uint32_t kpage_b = (uint32_t)(a.k_stride[0] * KT::bytes), vpage_b = (uint32_t)(a.v_stride[0] * VT::bytes);
+  const uint32_t krow_b = (uint32_t)(a.k_stride[1] * KT::bytes), vrow_b = (uint32_t)(a.v_stride[1] * VT::bytes);
+  const char* kbase = (const char*)a.k + (int64_t)kh * a.k_stride[2] * KT::bytes + min(l16, LK - 1) * KB;
+  const char* vbase = (const char*)a.v + (int64_t)kh * a.v_stride[2] * VT::bytes + min(l16, LV - 1) * VB;
+
+  // Address of the split's first key: the read target of rows with no valid position.
+  const char* ksafe = kbase;
+  const char* vsafe = vbase;
+  if (nsteps > 0) {
+    if (P) {
+      const uint32_t blk = (uint32_t)load_invariant_i32(a.block_table, b * a.bt_stride[0] + (int64_t)(plo / P) * a.bt_stride[1]);
+      ksafe += (uint64_t)blk * kpage_b + (uint64_t)(plo % P) * krow_b;
+      vsafe += (uint64_t)blk * vpage_b + (uint64_t)(plo % P) * vrow_b;
+    } else {
+      ksafe += (uint64_t)plo * krow_b;
+      vsafe += (uint64_t)plo * vrow_b;
+    }
+  }
+
+  // Block-table window: tab[c] of lane 4u + row holds the page of that row at
+  // step t0 + 16c + u (0 for rows outside the split).
+  int tab[4] = {0, 0, 0, 0};
+  auto load_tab = [&](int t0) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int tt = t0 + 16 * c + (lane >> 2);
+      const int rp = sb0 + WSTRIDE * tt + NT * (lane & 3);
+      const bool ok = tt < nsteps && rp + NT > plo && rp < phi;
+      tab[c] = ok ? a.block_table[b * a.bt_stride[0] + (int64_t)(rp / P) * a.bt_stride[1]] : 0;
+    }
+  };
+
+  // Row state advanced once per issued step: paged -> row index inside the
+  // page (and its byte offsets); packed -> byte offsets of the row itself.
+  const int rp0 = sb0 + NT * rg;
+  int inr = P ? rp0 % P : 0;
+  const int wrap = P ? WSTRIDE % P : 0;
+  uint64_t kin = P ? (uint64_t)inr * krow_b : (uint64_t)rp0 * krow_b;
+  uint64_t vin = P ? (uint64_t)inr * vrow_b : (uint64_t)rp0 * vrow_b;
+  const uint64_t kstep_packed = (uint64_t)WSTRIDE * krow_b, vstep_packed = (uint64_t)WSTRIDE * vrow_b;
+
+  auto issue = [&](int t, uint32_t (&kw)[NT][KB / 4], uint32_t (&vw)[NT][VB / 4]) {
+    const int sbt = sb0 + WSTRIDE * t;
+    const bool full = sbt >= plo && sbt + STEP <= phi;   // every position of the wave step is in the split
+    const char* krow = kbase + kin;
+    const char* vrow = vbase + vin;
+    if (P) {
+      const int u = t & 63, c = u >> 4;
+      const int e = c == 0 ? tab[0] : c == 1 ? tab[1] : c == 2 ? tab[2] : tab[3];
+      const uint32_t blk = (uint32_t)__builtin_amdgcn_ds_bpermute((((u & 15) << 2) + rg) << 2, e);
+      krow += (uint64_t)blk * kpage_b;
+      vrow += (uint64_t)blk * vpage_b;
+    }
+    if (full) {
+#pragma unroll
+      for (int i = 0; i < NT; ++i) load_words<KB>(krow + i * krow_b, kw[i]);
+#pragma unroll
+      for (int i = 0; i < NT; ++i) load_words<VB>(vrow + i * vrow_b, vw[i]);
+    } else {
+      const int rp = rp0 + WSTRIDE * t;
+      const bool row_ok = rp + NT > plo && rp < phi;
+      const int lo_i = row_ok ? max(plo - rp, 0) : 0;
+      const int hi_i = row_ok ? min(phi - rp, NT) - 1 : 0;
+      if (!row_ok) {
+        krow = ksafe;
+        vrow = vsafe;
+      }
+#pragma unroll
+      for (int i = 0; i < NT; ++i) load_words<KB>(krow + min(max(i, lo_i), hi_i) * krow_b, kw[i]);
+#pragma unroll
+      for (int i = 0; i < NT; ++i) load_words<VB>(vrow + min(max(i, lo_i), hi_i) * vrow_b, vw[i]);
+    }
+    if (P) {
+      inr += wrap;
+      kin += (uint64_t)wrap * krow_b;
+      vin += (uint64_t)wrap * vrow_b;
+      if (inr >= P) {
+        inr -= P;
+        kin -= (uint64_t)P * krow_b;
+        vin -= (uint64_t)P * vrow_b;
+      }
+    } else {
+      kin += kstep_packed;
+      vin += vstep_packed;
+    }
+  };
+
+  auto compute = [&](int t, const uint32_t (&kw)[NT][KB / 4], const uint32_t (&vw)[NT][VB / 4]) {
+    const int sbt = sb0 + WSTRIDE * t;
+    const bool full = sbt >= plo && sbt + STEP <= phi;
+    const int rp = rp0 + WSTRIDE * t;
+    float s[GT][NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+      uint32_t kp[EK / 2];
+      k_pairs<CT, KT, EK>(kw[i], kp);
+#pragma unroll
+      for (int g = 0; g < GT; ++g) {
+        float dot = 0.0f;
+#pragma unroll
+        for (int j = 0; j < EK / 2; ++j) dot = dot2<CT>(qp[g][j], kp[j], dot);
+        s[g][i] = dot;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < GT; ++g)
+#pragma unroll
+      for (int i = 0; i < NT; ++i) {
+        float v = row16_sum(s[g][i]) * sscale;
+        if constexpr (CAP) v = cap_out * (1.0f - 2.0f * __builtin_amdgcn_rcpf(fast_exp2(v * cap_in) + 1.0f));
+        if constexpr (ALIBI) v = fmaf(slope2[g], (float)(rp + i - qrow), v);
+        s[g][i] = v;
+      }
+    if (!full) {
+#pragma unroll
+      for (int i = 0; i < NT; ++i) {
+        const bool ok = rp + i >= plo && rp + i < phi;
+#pragma unroll
+        for (int g = 0; g < GT; ++g) s[g][i] = ok ? s[g][i] : -INFINITY;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      float mx = s[g][0];
+#pragma unroll
+      for (int i = 1; i < NT; ++i) mx = fmaxf(mx, s[g][i]);
+      const bool need = mx > m[g] + DEC_RESCALE;
+      if (__builtin_expect(__any(need), 0)) {
+        const float f = need ? fast_exp2(m[g] - mx) : 1.0f;
+        if (need) m[g] = mx;
+        l[g] *= f;
+#pragma unroll
+        for (int e = 0; e < EV; ++e) acc[g][e] *= f;
+      }
+      const float ref = m[g] == -INFINITY ? 0.0f : m[g];
+      float sum = 0.0f;
+#pragma unroll
+      for (int i = 0; i < NT; ++i) {
+        s[g][i] = fast_exp2(s[g][i] - ref);
+        sum += s[g][i];
+      }
+      l[g] += sum;
+    }
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+      float vf[EV];
+      words_to_f32<VT, EV>(vw[i], vf);
+#pragma unroll
+      for (int g = 0; g < GT; ++g)
+#pragma unroll
+        for (int e = 0; e < EV; ++e) acc[g][e] = fmaf(s[g][i], vf[e], acc[g][e]);
+    }
+  };
+
+  if (nsteps > 0) {
+    uint32_t kwa[NT][KB / 4], vwa[NT][VB / 4], kwb[NT][KB / 4], vwb[NT][VB / 4];
+    if (P) load_tab(0);
+    issue(0, kwa, vwa);
+    for (int t = 0;; t += 2) {
+      if (t + 1 < nsteps) {
+        if (P && ((t + 1) & 63) == 0) load_tab(t + 1);
+        issue(t + 1, kwb, vwb);
+      }
+      compute(t, kwa, vwa);
+      if (t + 1 >= nsteps) break;
+      if (t + 2 < nsteps) {
+        if (P && ((t + 2) & 63) == 0) load_tab(t + 2);
+        issue(t + 2, kwa, vwa);
+      }
+      compute(t + 1, kwb, vwb);
+      if (t + 2 >= nsteps) break;
+    }
+  }
+
+  // Combine the four 16-lane rows of the wave (same l16 <-> same dims).
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+#pragma unroll
+    for (int mask = 16; mask <= 32; mask <<= 1) {
+      const float mo = shfl_xor_f(m[g], mask);
+      const float lo = shfl_xor_f(l[g], mask);
+      const float mn = fmaxf(m[g], mo);
+      const float ref = mn == -INFINITY ? 0.0f : mn;
+      const float fa = fast_exp2(m[g] - ref), fb = fast_exp2(mo - ref);
+      l[g] = l[g] * fa + lo * fb;
+#pragma unroll
+      for (int e = 0; e < EV; ++e) acc[g][e] = acc[g][e] * fa + shfl_xor_f(acc[g][e], mask) * fb;
+      m[g] = mn;
+    }
+  }
+  if (rg == 0) {
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      if (l16 == 0) {
+        sm_m[wave][g] = m[g];
+        sm_l[wave][g] = l[g];
+      }
+#pragma unroll
+      for (int e = 0; e < EV; ++e) sm_acc[wave][g][l16 * EV + e] = acc[g][e];
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < nreal * DVT; idx += DEC_THREADS) {
+    const int g = idx / DVT, d = idx - g * DVT;
+    float M = sm_m[0][g];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) M = fmaxf(M, sm_m[w][g]);
+    const float ref = M == -INFINITY ? 0.0f : M;
+    float L = 0.0f, O = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float f = fast_exp2(sm_m[w][g] - ref);
+      L += sm_l[w][g] * f;
+      O += sm_acc[w][g][d] * f;
+    }
+    const float norm = L > 0.0f ? vscale / L : 0.0f;
+    const float lse = L > 0.0f ? M * LN2 + logf(L) : -INFINITY;
+    const int h = h0 + g;
+    if (S == 1) {
+      store_any(a.out, tq * a.out_stride[0] + (int64_t)h * a.out_stride[1] + (int64_t)d * a.out_stride[2], a.out_dtype,
+                O * norm);
+      if (d == 0) a.lse[(int64_t)h * a.lse_stride[0] + tq * a.lse_stride[1]] = lse;
+    } else {
+      const int64_t row = (b * a.heads_q + h) * S + split;
+      a.partial_out[row * DVT + d] = O * norm;
+      if (d == 0) a.partial_lse[row] = lse;
+    }
+  }
+}
+
+using DecodeKernel = void (*)(fa_attn_args, int);
+
+template <typename CT, typename KT, typename VT, int D, int DV, bool CAP, bool ALIBI, int DT = D, int DVT = DV>
+DecodeKernel pick_group(int gt) {
+  switch (gt) {
+    case 8: if constexpr (D == 128 && DV == 128) return decode_kernel<CT, KT, VT, D, DV, 8, CAP, DT, DVT, ALIBI>; else return nullptr;
+    case 4: if constexpr (4 * (D + DV) <= 64 * 16) return decode_kernel<CT, KT, VT, D, DV, 4, CAP, DT, DVT, ALIBI>; else return nullptr;
+    case 2: if constexpr (2 * (D + DV) <= 64 * 16) return decode_kernel<CT, KT, VT, D, DV, 2, CAP, DT, DVT, ALIBI>; else return nullptr;
+    case 1: return decode_kernel<CT, KT, VT, D, DV, 1, CAP, DT, DVT, ALIBI>;
+    default: return nullptr;
+  }
+}
+
+// Head dims 32 and 72/80/96 (dq == dv) run in the 64- and 128-dim tiles.
+template <typename CT, typename KT, typename VT, bool CAP, bool ALIBI>
+DecodeKernel pick_dims_cap(int64_t d, int64_t dv, int gt) {
+  if (d == 192 && dv == 128) return pick_group<CT, KT, VT, 192, 128, CAP, ALIBI>(gt);
+  if (d != dv) return nullptr;
+  switch (d) {
+    case 32: return pick_group<CT, KT, VT, 64, 64, CAP, ALIBI, 32, 32>(gt);
+    case 64: return pick_group<CT, KT, VT, 64, 64, CAP, ALIBI>(gt);
+    case 72: return pick_group<CT, KT, VT, 128, 128, CAP, ALIBI, 72, 72>(gt);
+    case 80: return pick_group<CT, KT, VT, 128, 128, CAP, ALIBI, 80, 80>(gt);
+    case 96: return pick_group<CT, KT, VT, 128, 128, CAP, ALIBI, 96, 96>(gt);
+    case 128: return pick_group<CT, KT, VT, 128, 128, CAP, ALIBI>(gt);
+    case 256: return pick_group<CT, KT, VT, 256, 256, CAP, ALIBI>(gt);
+    default: return nullptr;
+  }
+}
+
+// The tile head dim a tensor head dim runs in (0: none).
+inline int64_t decode_tile_dim(int64_t d) {
+  switch (d) {
+    case 32: case 64: return 64;
+    case 72: case 80: case 96: case 128: return 128;
+    case 192: return 192;
+    case 256: return 256;
+    default: return 0;
+  }
+}
+
+template <typename CT, typename KT, typename VT>
+DecodeKernel pick_dims(int64_t d, int64_t dv, int gt, bool cap, bool alibi) {
+  // ALiBi variants exist without softcap only (softcap + ALiBi: generic kernel).
+  if (alibi) return cap ? nullptr : pick_dims_cap<CT, KT, VT, false, true>(d, dv, gt);
+  return cap ? pick_dims_cap<CT, KT, VT, true, false>(d, dv, gt) : pick_dims_cap<CT, KT, VT, false, false>(d, dv, gt);
+}
+
+// Variants by (query, K/V) types, instantiated in decode_inst_*.hip so they
+// compile in parallel.
+DecodeKernel pick_decode_bf16(int64_t d, int64_t dv, int gt, bool cap, bool alibi);
+DecodeKernel pick_decode_f16(int64_t d, int64_t dv, int gt, bool cap, bool alibi);
+DecodeKernel pick_decode_fp8_bf16(int64_t d, int64_t dv, int gt, bool cap, bool alibi);
+DecodeKernel pick_decode_fp8_f16(int64_t d, int64_t dv, int gt, bool cap, bool alibi);
+
+}  // namespace fa_decode
