@@ -210,6 +210,13 @@ __global__ __launch_bounds__(256) void rotary_kernel(const RotaryParams p) {
       other = second ? d - p.half : d + p.half;
     }
     const int64_t pos = (int64_t)p.lengths[b] + (p.advance ? j : 0);
+    // Lengths live on the device, so the host cannot check them against the
+    // table: a position with no cos/sin row rotates to NaN instead of
+    // reading past the table.
+    if (pos < 0 || pos >= p.rows) {
+      store_elem<XT>(p.out, i, __builtin_nanf(""));
+      continue;
+    }
     const float c = p.cos_t[pos * p.half + pair], s = p.sin_t[pos * p.half + pair];
     const float x = load_elem<XT>(p.x, src);
     const float y = load_elem<XT>(p.x, b * p.xs[0] + j * p.xs[1] + h * p.xs[2] + other * p.xs[3]);

@@ -85,6 +85,13 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const fa_attn_args a,
 
 int elem_size(int dt) { return dt == FA_F32 ? 4 : dt == FA_E4M3 ? 1 : 2; }
 
+// Most keys one request can see: max_seqlen_k, clipped by a left window
+// (the query sits at the last key, so it sees window_left + 1 keys).
+int64_t decode_visible_max(const fa_attn_args& a) {
+  const int64_t m = a.max_seqlen_k > 0 ? a.max_seqlen_k : 0;
+  return a.window_left >= 0 && a.window_left + 1 < m ? a.window_left + 1 : m;
+}
+
 // Query heads per workgroup (GT).  Every workgroup of a KV head reads it
 // again, so GT is the smallest power of two that reaches the fewest
 // workgroups per KV head, ceil(group / gmax), where gmax keeps q +
@@ -163,7 +170,11 @@ extern "C" int fa_decode_fwd(const fa_attn_args* a, void* stream) {
     return FA_ERR_UNSUPPORTED;
   }
   if (a->total_q == 0) return FA_OK;
-  FA_REQUIRE(a->split_span >= 1, "fa_decode_fwd: split_span must be positive");
+  FA_REQUIRE(a->split_span >= 1 && a->num_splits >= 1, "fa_decode_fwd: num_splits and split_span must be positive");
+  // Keys past num_splits * split_span would be dropped without a trace.
+  FA_REQUIRE((int64_t)a->num_splits * a->split_span >= decode_visible_max(*a),
+             "fa_decode_fwd: num_splits * split_span = %lld does not cover the %lld visible keys",
+             (long long)a->num_splits * a->split_span, (long long)decode_visible_max(*a));
   FA_REQUIRE(a->num_splits == 1 || (a->partial_out && a->partial_lse), "fa_decode_fwd: splits need partial buffers");
   FA_REQUIRE(a->batch <= 65535, "fa_decode_fwd: batch exceeds the grid limit");
   const int64_t head_groups = a->heads_k * fa_ceil_div(a->heads_q / a->heads_k, gt);

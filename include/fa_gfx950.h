@@ -157,9 +157,14 @@ typedef struct fa_attn_args {
   const float* v_descale; int64_t v_descale_stride[2];
 
   int32_t num_splits;                /* >= 1 */
-  int32_t split_span;                /* decode: keys per split (multiple of 128) */
-  float* partial_out;                /* workspace, see fa_*_workspace_floats */
-  float* partial_lse;
+  int32_t split_span;                /* fa_decode_fwd: keys per split (>= 1); the splits
+                                        must cover every visible key:
+                                        num_splits * split_span >= min(max_seqlen_k,
+                                        window_left + 1) (window_left < 0: max_seqlen_k) */
+  float* partial_out;                /* num_splits > 1: caller-owned fp32 workspace,
+                                        fa_decode_fwd [batch, Hq, S, Dv] contiguous,
+                                        fa_attn_fwd [S, total_q, Hq, Dv] contiguous */
+  float* partial_lse;                /* fa_decode_fwd [batch, Hq, S], fa_attn_fwd [S, Hq, total_q] */
 
   int32_t flags;                     /* FA_FLAG_* bits */
   int32_t _pad1;
