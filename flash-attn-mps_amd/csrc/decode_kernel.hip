@@ -1,8 +1,17 @@
 // Split-KV decode: the merge kernel, kernel selection and the C-ABI entry
-// points fa_decode_supported / fa_decode_fwd (flash_attn_mps/_decode.py:40-99).
-// The decode kernel itself is in decode_kernel.h; its variants are
-// instantiated in decode_inst_*.hip.
+// points fa_decode_supported / fa_decode_fwd (flash_attn_mps/_decode.py:40-99)
+// and fa_decode_fwd_noalloc (no reference counterpart).  The decode kernel
+// itself is in decode_kernel.h; its variants are instantiated in
+// decode_inst_*.hip.
+#include <mutex>
+
 #include "decode_kernel.h"
+
+// Split partials of fa_decode_fwd_noalloc, one copy per GPU, held until the
+// process ends.  In host code this name is only a stand-in for the symbol:
+// the device address comes from hipGetSymbolAddress (scratch_of_device) and
+// is the only thing ever handed to a kernel.
+static __device__ __align__(256) float scratch[FA_DECODE_SCRATCH_BYTES / sizeof(float)];
 
 namespace {
 
@@ -160,31 +169,137 @@ extern "C" int fa_decode_supported(const fa_attn_args* a) {
   return select_decode(*a, &gt) != nullptr;
 }
 
-extern "C" int fa_decode_fwd(const fa_attn_args* a, void* stream) {
-  int rc = fa_validate_attn(a, "fa_decode_fwd");
-  if (rc) return rc;
+namespace {
+
+// Launch the decode kernel (and the merge when there are several splits) for
+// arguments that passed fa_validate_attn.
+int decode_launch(const fa_attn_args* a, void* stream, const char* who) {
   int gt = 1;
   const DecodeKernel kern = select_decode(*a, &gt);
   if (!kern) {
-    fa_set_error("fa_decode_fwd: unsupported dtype/head-dim/stride combination");
+    fa_set_error("%s: unsupported dtype/head-dim/stride combination", who);
     return FA_ERR_UNSUPPORTED;
   }
   if (a->total_q == 0) return FA_OK;
-  FA_REQUIRE(a->split_span >= 1 && a->num_splits >= 1, "fa_decode_fwd: num_splits and split_span must be positive");
+  FA_REQUIRE(a->split_span >= 1 && a->num_splits >= 1, "%s: num_splits and split_span must be positive", who);
   // Keys past num_splits * split_span would be dropped without a trace.
   FA_REQUIRE((int64_t)a->num_splits * a->split_span >= decode_visible_max(*a),
-             "fa_decode_fwd: num_splits * split_span = %lld does not cover the %lld visible keys",
+             "%s: num_splits * split_span = %lld does not cover the %lld visible keys", who,
              (long long)a->num_splits * a->split_span, (long long)decode_visible_max(*a));
-  FA_REQUIRE(a->num_splits == 1 || (a->partial_out && a->partial_lse), "fa_decode_fwd: splits need partial buffers");
-  FA_REQUIRE(a->batch <= 65535, "fa_decode_fwd: batch exceeds the grid limit");
+  FA_REQUIRE(a->num_splits == 1 || (a->partial_out && a->partial_lse), "%s: splits need partial buffers", who);
+  FA_REQUIRE(a->batch <= 65535, "%s: batch exceeds the grid limit", who);
   const int64_t head_groups = a->heads_k * fa_ceil_div(a->heads_q / a->heads_k, gt);
-  FA_REQUIRE(a->num_splits <= 65535, "fa_decode_fwd: too many splits");
+  FA_REQUIRE(a->num_splits <= 65535, "%s: too many splits", who);
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)head_groups, (unsigned)a->num_splits, (unsigned)a->batch);
   hipLaunchKernelGGL(kern, grid, dim3(DEC_THREADS), 0, s, *a, (int)a->split_span);
-  rc = fa_check_launch("fa_decode_fwd");
+  int rc = fa_check_launch(who);
   if (rc || a->num_splits == 1) return rc;
   const int64_t rows = a->batch * a->heads_q;
   hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)fa_ceil_div(rows, 4)), dim3(256), 0, s, *a, (int)a->split_span);
-  return fa_check_launch("fa_decode_fwd merge");
+  return fa_check_launch(who);
+}
+
+// Floats of the partial rows; the LSE rows start at the next 256-byte boundary.
+int64_t partial_out_floats(const fa_attn_args& a, int64_t splits) {
+  return fa_ceil_div(a.batch * a.heads_q * splits * a.head_dim_v, 64) * 64;
+}
+
+int64_t partial_floats(const fa_attn_args& a, int64_t splits) {
+  return partial_out_floats(a, splits) + a.batch * a.heads_q * splits;
+}
+
+// The split plan of the Python host layer (flash_attn_mps_amd/_decode.py
+// split_plan with num_splits == 0): spans of 2048 keys halving down to 128
+// until the grid holds 2048 workgroups.  Then the split count is reduced
+// until the partials fit in `cap_floats` (one split needs no partials).
+void plan_splits(const fa_attn_args& a, int gt, int64_t cap_floats, int32_t* splits_out, int32_t* span_out) {
+  const int64_t vis = decode_visible_max(a);
+  if (vis <= 0) {
+    *splits_out = 1;
+    *span_out = 32;
+    return;
+  }
+  const int64_t groups = a.heads_k * fa_ceil_div(a.heads_q / a.heads_k, gt);
+  int64_t span = 2048;
+  while (span > 128 && a.batch * groups * fa_ceil_div(vis, span) < 2048) span /= 2;
+  int64_t splits = fa_ceil_div(vis, span);
+  while (splits > 1 && partial_floats(a, splits) > cap_floats) {
+    span = fa_ceil_div(fa_ceil_div(vis, fa_ceil_div(splits, 2)), 32) * 32;
+    splits = fa_ceil_div(vis, span);
+  }
+  *splits_out = (int32_t)splits;
+  *span_out = (int32_t)(span < INT32_MAX ? span : INT32_MAX);
+}
+
+constexpr int SCRATCH_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[SCRATCH_MAX_DEVICES] = {};
+
+// Device address of this GPU's scratch array: looked up once per device, with
+// that device current, and kept.
+int scratch_of_device(void* stream, float** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= SCRATCH_MAX_DEVICES) {
+    fa_set_error("fa_decode_fwd_noalloc: no current HIP device");
+    return FA_ERR_LAUNCH;
+  }
+  if (stream) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice((hipStream_t)stream, &sdev) != hipSuccess || sdev != dev) {
+      fa_set_error("fa_decode_fwd_noalloc: the stream does not belong to the current device %d", dev);
+      return FA_ERR_INVALID;
+    }
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || p == nullptr) {
+      fa_set_error("fa_decode_fwd_noalloc: hipGetSymbolAddress failed: %s", hipGetErrorString(err));
+      return FA_ERR_LAUNCH;
+    }
+    g_scratch_ptr[dev] = (float*)p;
+  }
+  *out = g_scratch_ptr[dev];
+  return FA_OK;
+}
+
+}  // namespace
+
+extern "C" int fa_decode_fwd(const fa_attn_args* a, void* stream) {
+  const int rc = fa_validate_attn(a, "fa_decode_fwd");
+  return rc ? rc : decode_launch(a, stream, "fa_decode_fwd");
+}
+
+extern "C" int fa_decode_fwd_noalloc(const fa_attn_args* in, void* stream) {
+  FA_REQUIRE(in != nullptr, "fa_decode_fwd_noalloc: null args");
+  FA_REQUIRE(in->partial_out == nullptr && in->partial_lse == nullptr,
+             "fa_decode_fwd_noalloc: partial buffers are library-owned; pass NULL");
+  FA_REQUIRE(in->num_splits >= 0, "fa_decode_fwd_noalloc: num_splits must be >= 0");
+  fa_attn_args a = *in;
+  constexpr int64_t cap = FA_DECODE_SCRATCH_BYTES / (int64_t)sizeof(float);
+  if (a.num_splits == 0) {
+    int gt = 1;
+    if (!select_decode(a, &gt)) {
+      fa_set_error("fa_decode_fwd_noalloc: unsupported dtype/head-dim/stride combination");
+      return FA_ERR_UNSUPPORTED;
+    }
+    FA_REQUIRE(a.batch >= 1 && a.heads_k >= 1 && a.heads_q % a.heads_k == 0,
+               "fa_decode_fwd_noalloc: bad batch/head counts");
+    plan_splits(a, gt, cap, &a.num_splits, &a.split_span);
+  }
+  int rc = fa_validate_attn(&a, "fa_decode_fwd_noalloc");
+  if (rc) return rc;
+  if (a.num_splits > 1) {
+    FA_REQUIRE(partial_floats(a, a.num_splits) <= cap,
+               "fa_decode_fwd_noalloc: %d splits need %lld bytes of partials; the limit is %lld", a.num_splits,
+               (long long)partial_floats(a, a.num_splits) * 4, (long long)FA_DECODE_SCRATCH_BYTES);
+    float* base = nullptr;
+    rc = scratch_of_device(stream, &base);
+    if (rc) return rc;
+    a.partial_out = base;
+    a.partial_lse = base + partial_out_floats(a, a.num_splits);
+  }
+  return decode_launch(&a, stream, "fa_decode_fwd_noalloc");
 }

@@ -115,6 +115,7 @@ ENTRY_POINTS = {
     "fa_rotary": (RotaryArgs, ctypes.c_int),
     "fa_decode_supported": (AttnArgs, ctypes.c_int),
     "fa_decode_fwd": (AttnArgs, ctypes.c_int),
+    "fa_decode_fwd_noalloc": (AttnArgs, ctypes.c_int),
     "fa_prefill_supported": (AttnArgs, ctypes.c_int),
     "fa_prefill_fwd": (AttnArgs, ctypes.c_int),
     "fa_attn_fwd": (AttnArgs, ctypes.c_int),
@@ -124,6 +125,7 @@ ENTRY_POINTS = {
 
 ABI_VERSION = 2
 FLAG_SKIP_SINGLE_QUERY = 1
+DECODE_SCRATCH_BYTES = 32 << 20   # FA_DECODE_SCRATCH_BYTES
 _lib = None
 
 

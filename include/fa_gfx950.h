@@ -213,6 +213,25 @@ int fa_rotary(const fa_rotary_args* args, void* stream);
 int fa_decode_supported(const fa_attn_args* args);
 int fa_decode_fwd(const fa_attn_args* args, void* stream);
 
+/* fa_decode_fwd that allocates nothing.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops and harnesses that forbid hipMalloc).  The split
+ * partials live in a library-owned device array of FA_DECODE_SCRATCH_BYTES
+ * per GPU, held until the process ends; args->partial_out/partial_lse must
+ * be NULL.  num_splits == 0 lets the library plan the splits (spans start at
+ * 2048 keys and halve down to 128 until the grid holds at least 2048
+ * workgroups -- the plan of the Python host layer -- then the split count is
+ * reduced until the partials fit; one split needs none); otherwise the
+ * caller's num_splits/split_span are used and
+ * batch * Hq * num_splits * (Dv + 1) * 4 bytes must fit, else FA_ERR_INVALID.
+ * Every call on one GPU shares that GPU's array and the array keeps the last
+ * call's partials (nothing in it needs clearing: each split writes its own
+ * rows before the merge reads them); calls that overlap in time on one GPU
+ * (two streams, two threads) race.  The stream must belong to the current
+ * device. */
+#define FA_DECODE_SCRATCH_BYTES (32ll << 20)
+int fa_decode_fwd_noalloc(const fa_attn_args* args, void* stream);
+
 /* MFMA prefill (bf16/fp16 queries; bf16/fp16 or FP8 E4M3 K/V with
  * descales; causal, per-request causal, windows, softcap, sinks, and ALiBi
  * without softcap, windows, per-request causality or FP8; head dims 32-256

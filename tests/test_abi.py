@@ -53,6 +53,20 @@ def test_null_arguments_are_rejected_before_launch(name, struct):
     assert lib.fa_last_error().decode().startswith(name)
 
 
+def test_noalloc_decode_rejects_bad_arguments_before_any_hip_call():
+    lib = _lib.load()
+    assert lib.fa_decode_fwd_noalloc(None, None) == 1
+    a = _lib.AttnArgs()
+    a.num_splits = 1                        # explicit plan: NULL tensors fail validation
+    assert lib.fa_decode_fwd_noalloc(ctypes.byref(a), None) == 1
+    assert lib.fa_last_error().decode().startswith("fa_decode_fwd_noalloc")
+    a.partial_out = 4096                    # partials are library-owned
+    assert lib.fa_decode_fwd_noalloc(ctypes.byref(a), None) == 1
+    assert b"library-owned" in lib.fa_last_error()
+    a.partial_out, a.num_splits = None, 0   # library plan: unsupported layout
+    assert lib.fa_decode_fwd_noalloc(ctypes.byref(a), None) == 2
+
+
 def test_supported_queries_reject_unsupported_combinations():
     a = _lib.AttnArgs()
     a.k_dtype = a.v_dtype = _lib.F32
