@@ -153,9 +153,9 @@ def measured_traffic():
     return None
 
 
-def config2(device, steps, warmup):
+def config2_inputs(device):
+    """Config 2: 16 sequences, lengths U[256, 4096], 0.5*N(0,1) bf16 Q/K/V, Hq/Hkv 16/8, d 128."""
     import torch
-    import flash_attn_mps_amd as fa
     g = torch.Generator().manual_seed(123 + 2)
     lengths = torch.randint(256, 4097, (16,), generator=g).tolist()
     total = sum(lengths)
@@ -163,15 +163,22 @@ def config2(device, steps, warmup):
     q = (torch.randn(total, hq, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
     k = (torch.randn(total, hkv, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
     v = (torch.randn(total, hkv, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
-    cu = cu_lengths(lengths, device)
+    return dict(lengths=lengths, q=q, k=k, v=v, cu=cu_lengths(lengths, device), heads=hq, kv_heads=hkv, dim=d)
+
+
+def config2(device, steps, warmup):
+    import torch
+    import flash_attn_mps_amd as fa
+    c = config2_inputs(device)
+    q, k, v, cu, lengths = c["q"], c["k"], c["v"], c["cu"], c["lengths"]
     maxlen = max(lengths)
-    out = torch.empty(total, hq, d, dtype=torch.bfloat16, device=device)
+    out = torch.empty_like(q)
 
     def step():
         fa.flash_attn_varlen_func(q, k, v, cu, cu, maxlen, maxlen, causal=True, out=out)
 
     ms, call_ms, kernel_ms = time_calls(step, steps, warmup, kernel="fa_prefill_fwd")
-    flops = causal_pairs(lengths, lengths) * hq * 2 * (d + d)
+    flops = causal_pairs(lengths, lengths) * c["heads"] * 2 * (c["dim"] + c["dim"])
     return dict(lengths=lengths, flops=flops, ms=ms, call_ms=call_ms, kernel_ms=kernel_ms,
                 tflops=flops / (ms * 1e-3) / 1e12, call_tflops=flops / (call_ms * 1e-3) / 1e12,
                 kernel_tflops=flops / (kernel_ms * 1e-3) / 1e12, tensors=(q, k, v, cu))
@@ -209,56 +216,78 @@ def paged_cache(ctx, page, hkv, d, dtype, device, gen_seed, scale=None, dv=None)
     return kc, vc, table.to(device), slots
 
 
-def config3(device, steps, warmup):
+def config3_inputs(device):
+    """Config 3: 64 requests, contexts U[512, 32768], Hq/Hkv 32/8, d 128, bf16 cache in
+    16-token pages written by store_kvcache through a permuted block table."""
     import torch
-    import flash_attn_mps_amd as fa
     g = torch.Generator().manual_seed(123 + 3)
     ctx = torch.randint(512, 32769, (64,), generator=g).tolist()
     hq, hkv, d, page = 32, 8, 128, 16
-    kc, vc, table, _ = paged_cache(ctx, page, hkv, d, torch.bfloat16, device, 123 + 3)
+    kc, vc, table, slots = paged_cache(ctx, page, hkv, d, torch.bfloat16, device, 123 + 3)
     q = torch.randn(64, 1, hq, d, generator=g).to(torch.bfloat16).to(device)
-    lens = torch.tensor(ctx, dtype=torch.int32, device=device)
+    return dict(ctx=ctx, q=q, k_cache=kc, v_cache=vc, table=table, slots=slots,
+                lengths=torch.tensor(ctx, dtype=torch.int32, device=device), heads=hq, kv_heads=hkv, dim=d,
+                page=page, kv_bytes=sum(ctx) * hkv * 2 * d * 2)
+
+
+def config3(device, steps, warmup):
+    import flash_attn_mps_amd as fa
+    c = config3_inputs(device)
 
     def step():
-        fa.flash_attn_with_kvcache(q, kc, vc, cache_seqlens=lens, block_table=table, causal=True)
+        fa.flash_attn_with_kvcache(c["q"], c["k_cache"], c["v_cache"], cache_seqlens=c["lengths"],
+                                   block_table=c["table"], causal=True)
 
-    ms, call_ms, _ = time_calls(step, steps, warmup)
-    kv_bytes = sum(ctx) * hkv * 2 * d * 2
-    del kc, vc
-    return dict(kv_bytes=kv_bytes, ms=ms, call_ms=call_ms, gbs=kv_bytes / (ms * 1e-3) / 1e9,
+    ms, call_ms, kernel_ms = time_calls(step, steps, warmup, kernel="fa_decode_fwd")
+    kv_bytes = c["kv_bytes"]
+    del c
+    return dict(kv_bytes=kv_bytes, ms=ms, call_ms=call_ms, kernel_ms=kernel_ms, gbs=kv_bytes / (ms * 1e-3) / 1e9,
                 call_gbs=kv_bytes / (call_ms * 1e-3) / 1e9)
+
+
+def config4_inputs(device):
+    """Config 4: 128 requests, contexts U[1024, 8192], Hq/Hkv 16/8, d 256, E4M3 cache with
+    per-KV-head scales U[0.01, 0.1] (descales [B, Hkv] as a stride-0 view), softcap 50,
+    window (4095, 0)."""
+    import torch
+    g = torch.Generator().manual_seed(123 + 4)
+    ctx = torch.randint(1024, 8193, (128,), generator=g).tolist()
+    hq, hkv, d, page = 16, 8, 256, 16
+    scale = torch.empty(hkv).uniform_(0.01, 0.1, generator=g)
+    kc, vc, table, slots = paged_cache(ctx, page, hkv, d, torch.float8_e4m3fn, device, 123 + 4,
+                                       scale=scale.to(device))
+    q = torch.randn(128, hq, d, generator=g).to(torch.bfloat16).to(device)
+    return dict(ctx=ctx, q=q, k_cache=kc, v_cache=vc, table=table, slots=slots, scale=scale,
+                cu_q=torch.arange(129, dtype=torch.int32, device=device),
+                lengths=torch.tensor(ctx, dtype=torch.int32, device=device),
+                descale=scale.to(device).expand(128, hkv), heads=hq, kv_heads=hkv, dim=d, page=page,
+                softcap=50.0, window=(4095, 0), kv_bytes=sum(min(c, 4096) for c in ctx) * hkv * 2 * d * 1)
 
 
 def config4(device, steps, warmup):
     import torch
     from flash_attn_mps_amd import vllm
-    g = torch.Generator().manual_seed(123 + 4)
-    ctx = torch.randint(1024, 8193, (128,), generator=g).tolist()
-    hq, hkv, d, page = 16, 8, 256, 16
-    scale = torch.empty(hkv).uniform_(0.01, 0.1, generator=g)
-    kc, vc, table, _ = paged_cache(ctx, page, hkv, d, torch.float8_e4m3fn, device, 123 + 4,
-                                   scale=scale.to(device))
-    q = torch.randn(128, hq, d, generator=g).to(torch.bfloat16).to(device)
-    cuq = torch.arange(129, dtype=torch.int32, device=device)
-    used = torch.tensor(ctx, dtype=torch.int32, device=device)
-    desc = scale.to(device).expand(128, hkv)
-    out = torch.empty(128, hq, d, dtype=torch.bfloat16, device=device)
+    c = config4_inputs(device)
+    out = torch.empty(128, c["heads"], c["dim"], dtype=torch.bfloat16, device=device)
 
     def step():
-        vllm.flash_attn_varlen_func(q, kc, vc, 1, cuq, max(ctx), seqused_k=used, block_table=table,
-                                    causal=True, softcap=50.0, window_size=(4095, 0),
-                                    k_descale=desc, v_descale=desc, out=out)
+        vllm.flash_attn_varlen_func(c["q"], c["k_cache"], c["v_cache"], 1, c["cu_q"], max(c["ctx"]),
+                                    seqused_k=c["lengths"], block_table=c["table"], causal=True,
+                                    softcap=c["softcap"], window_size=c["window"], k_descale=c["descale"],
+                                    v_descale=c["descale"], out=out)
 
-    ms, call_ms, _ = time_calls(step, steps, warmup)
-    kv_bytes = sum(min(c, 4096) for c in ctx) * hkv * 2 * d * 1
-    del kc, vc
-    return dict(kv_bytes=kv_bytes, ms=ms, call_ms=call_ms, gbs=kv_bytes / (ms * 1e-3) / 1e9,
+    ms, call_ms, kernel_ms = time_calls(step, steps, warmup, kernel="fa_decode_fwd")
+    kv_bytes = c["kv_bytes"]
+    del c
+    return dict(kv_bytes=kv_bytes, ms=ms, call_ms=call_ms, kernel_ms=kernel_ms, gbs=kv_bytes / (ms * 1e-3) / 1e9,
                 call_gbs=kv_bytes / (call_ms * 1e-3) / 1e9)
 
 
-def config5(device, steps, warmup):
+def config5_inputs(device):
+    """Config 5: one DIFFKV call (Dqk 192 / Dv 128, Hq = Hkv = 16, bf16, 16-token pages) of
+    8 chunks of 512 new tokens on prefixes U[0, 4096] plus 120 decode requests with
+    contexts U[256, 16384]; per-head sinks N(0,1); caller-owned out."""
     import torch
-    from flash_attn_mps_amd import vllm
     g = torch.Generator().manual_seed(123 + 5)
     hq = hkv = 16
     dqk, dv, page = 192, 128, 16
@@ -267,23 +296,32 @@ def config5(device, steps, warmup):
     q_lens = [512] * 8 + [1] * 120
     k_lens = [p + 512 for p in prefixes] + dec_ctx
     kc, vc, table, _ = paged_cache(k_lens, page, hkv, dqk, torch.bfloat16, device, 123 + 5, dv=dv)
-    total_q = sum(q_lens)
-    q = torch.randn(total_q, hq, dqk, generator=g).to(torch.bfloat16).to(device)
+    q = torch.randn(sum(q_lens), hq, dqk, generator=g).to(torch.bfloat16).to(device)
     sinks = torch.randn(hq, generator=g).to(device)
-    cuq = cu_lengths(q_lens, device)
-    used = torch.tensor(k_lens, dtype=torch.int32, device=device)
-    out = torch.empty(total_q, hq, dv, dtype=torch.bfloat16, device=device)
+    return dict(q_lens=q_lens, k_lens=k_lens, dec_ctx=dec_ctx, q=q, k_cache=kc, v_cache=vc, table=table,
+                sinks=sinks, cu_q=cu_lengths(q_lens, device),
+                used=torch.tensor(k_lens, dtype=torch.int32, device=device), heads=hq, kv_heads=hkv,
+                dim_qk=dqk, dim_v=dv, page=page)
+
+
+def config5(device, steps, warmup):
+    import torch
+    from flash_attn_mps_amd import vllm
+    c = config5_inputs(device)
+    q_lens, k_lens, hkv, dqk, dv = c["q_lens"], c["k_lens"], c["kv_heads"], c["dim_qk"], c["dim_v"]
+    out = torch.empty(sum(q_lens), c["heads"], dv, dtype=torch.bfloat16, device=device)
 
     def step():
-        vllm.flash_attn_varlen_func(q, kc, vc, max(q_lens), cuq, max(k_lens), seqused_k=used,
-                                    block_table=table, causal=True, s_aux=sinks, out=out)
+        vllm.flash_attn_varlen_func(c["q"], c["k_cache"], c["v_cache"], max(q_lens), c["cu_q"], max(k_lens),
+                                    seqused_k=c["used"], block_table=c["table"], causal=True, s_aux=c["sinks"],
+                                    out=out)
 
     ms, call_ms, _ = time_calls(step, steps, warmup)
-    dec_bytes = sum(dec_ctx) * hkv * (dqk + dv) * 2
+    dec_bytes = sum(c["dec_ctx"]) * hkv * (dqk + dv) * 2
     chunk_bytes = sum(k_lens[:8]) * hkv * (dqk + dv) * 2
-    flops = causal_pairs(q_lens[:8], k_lens[:8]) * hq * 2 * (dqk + dv)
+    flops = causal_pairs(q_lens[:8], k_lens[:8]) * c["heads"] * 2 * (dqk + dv)
     roof_ms = max(flops / (PEAK_BF16_TFLOPS * 1e12), (dec_bytes + chunk_bytes) / (PEAK_HBM_GBS * 1e9)) * 1e3
-    del kc, vc
+    del c
     return dict(kv_bytes=dec_bytes + chunk_bytes, flops=flops, ms=ms, call_ms=call_ms,
                 gbs=(dec_bytes + chunk_bytes) / (ms * 1e-3) / 1e9, roofline_ms=roof_ms,
                 frac=roof_ms / ms)
@@ -311,7 +349,20 @@ def cpu_baseline(lengths, tensors):
     sec = sorted(times)[1]
     flops = causal_pairs(sample, sample) * 16 * 2 * 256
     return {"value": round(flops / sec / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "cpu": cpu_model(),
             "sample": f"config 2 sequences 0-{take - 1} (lengths {sample}), fp32 oracle, median of 3"}
+
+
+def cpu_model():
+    """The host CPU's model name (first 'model name' line of /proc/cpuinfo)."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
 
 
 def main():
@@ -343,11 +394,16 @@ def main():
         "config": {"workload": "config 2: varlen causal prefill, 16 seqs L~U[256,4096], Hq/Hkv 16/8, d128 "
                                "(Qwen3-0.6B attention)", "global_batch": 16, "seq_len": max(c2["lengths"]),
                    "total_tokens": sum(c2["lengths"]), "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "achieved": round(c2["kernel_tflops"], 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(c2["kernel_tflops"] / PEAK_BF16_TFLOPS, 4),
+        # achieved/frac: algorithmic FLOPs over the timed region's time per step
+        # (one launch per step); the HIP-event time of the launches alone and
+        # the median call are reported beside them.
+        "roofline": {"bound": "mfma", "achieved": round(c2["tflops"], 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(c2["tflops"] / PEAK_BF16_TFLOPS, 4),
                      "traffic": measured_traffic(),
                      "flops_per_launch": c2["flops"], "kernel": "prefill_kernel",
-                     "kernel_ms": round(c2["kernel_ms"], 4), "call_ms": round(c2["call_ms"], 4)},
+                     "kernel_event_ms": round(c2["kernel_ms"], 4),
+                     "kernel_event_frac": round(c2["kernel_tflops"] / PEAK_BF16_TFLOPS, 4),
+                     "call_median_ms": round(c2["call_ms"], 4)},
     }
     secondary = {}
     if not args.no_secondary:
@@ -360,8 +416,9 @@ def main():
                 entry.update(roofline_ms=round(r["roofline_ms"], 4), frac=round(r["frac"], 4),
                              chunk_flops=r["flops"])
             else:
-                entry.update(call_kv_GBps=round(r["call_gbs"], 1),
-                             frac_of_hbm=round(r["call_gbs"] / PEAK_HBM_GBS, 4), kv_bytes=r["kv_bytes"])
+                entry.update(frac_of_hbm=round(r["gbs"] / PEAK_HBM_GBS, 4), kv_bytes=r["kv_bytes"],
+                             call_median_kv_GBps=round(r["call_gbs"], 1),
+                             kernel_event_ms=round(r["kernel_ms"], 4))
             secondary["config" + name] = entry
             torch.cuda.empty_cache()
     line["secondary"] = secondary

@@ -1,8 +1,10 @@
 """FlashAttention inference for PyTorch-ROCm on AMD Instinct MI355X (gfx950).
 
-Drop-in for the public API of flash_attn_mps (flash_attn_mps/__init__.py:3-29):
-the same function names, signatures and tensor contracts, computed by
-hand-written gfx950 HIP kernels in libfa_gfx950.so.
+A drop-in for the public API of flash_attn_mps (flash_attn_mps/__init__.py:3-29):
+the FlashAttention-2 functions, ``store_kvcache`` and ``merge_attn_states``,
+with the same names, signatures and tensor contracts, computed by hand-written
+gfx950 HIP kernels in ``libfa_gfx950.so``.  The vLLM contract lives in
+``flash_attn_mps_amd.vllm``.
 """
 
 from .interface import (
@@ -16,14 +18,13 @@ from .interface import (
 )
 from .vllm import merge_attn_states
 
-__version__ = "0.1.0"
+__version__ = "0.2.0"
 
 
 def store_kvcache(key, value, k_cache, v_cache, slot_mapping, *, k_scale=None, v_scale=None):
-    """Scatter new K/V to physical cache slots; negative slots are skipped."""
-    from ._cache import store_kvcache as store
-    return store(key, value, k_cache, v_cache, slot_mapping,
-                 k_scale=k_scale, v_scale=v_scale)
+    """Write key/value [T, Hkv, D] rows to cache slots (slot // P, slot % P); slots < 0 are skipped."""
+    from ._cache import store_kvcache as _store
+    _store(key, value, k_cache, v_cache, slot_mapping, k_scale=k_scale, v_scale=v_scale)
 
 
 __all__ = [

@@ -1,171 +1,189 @@
-"""Cache scatter, FA2 append and rotary embedding on gfx950.
+"""KV-cache writes and rotary embedding on gfx950: host side of
+fa_store_kvcache / fa_append_kvcache / fa_rotary (counterpart of
+flash_attn_mps/_cache.py:55-155).
 
-Host side of fa_store_kvcache / fa_append_kvcache / fa_rotary; mirrors
-flash_attn_mps/_cache.py:67-155 (argument checks, scalar-or-per-head FP8
-scales, lengths broadcast, RoPE position rules) with the kernels of
-csrc/cache_kernels.hip.
+* store_kvcache scatters token rows to physical slots (page = slot // P,
+  row = slot % P); negative or out-of-range slots are skipped by the kernel.
+* append_kvcache writes new rows at ``lengths[b] + j`` of a dense cache row
+  or through a page table; the lengths themselves are not touched.
+* An FP8 (E4M3FN) cache stores E4M3(x / scale) with scale a scalar or one
+  value per KV head; 16-bit and fp32 caches of the input's dtype get the
+  input's bits.
 """
 from functools import lru_cache
 
 import torch
 
 from . import _lib
+from ._problem import on_gpu
+
+_INPUT_TYPES = (torch.float16, torch.bfloat16, torch.float32)
 
 
-def _gpu(*tensors):
-    if any(t.device.type != "cuda" for t in tensors if t is not None):
-        raise ValueError("operations require GPU (HIP) tensors")
+def _require_gpu(**tensors):
+    for name, t in tensors.items():
+        if t is not None and not on_gpu(t):
+            raise ValueError(f"{name} is on {t.device}; cache operations run on a ROCm GPU")
 
 
 @lru_cache(maxsize=None)
-def _unit_scale(device):
-    return torch.ones(1, device=device, dtype=torch.float32)
+def _one(device):
+    """A resident fp32 1.0 per device: the FP8 scale when the caller gives none."""
+    return torch.ones(1, dtype=torch.float32, device=device)
 
 
-def _scale(scale, heads, device):
-    """flash_attn_mps/_cache.py:55-59: scalar or one value per KV head, fp32."""
-    if scale is None:
-        scale = _unit_scale(device)
-    else:
-        scale = torch.as_tensor(scale, device=device, dtype=torch.float32)
-    if scale.numel() not in (1, heads):
-        raise ValueError("scale must be scalar or have one value per KV head")
-    return scale.reshape(-1).contiguous(), 0 if scale.numel() == 1 else 1
+def _per_head_scale(scale, heads, device):
+    """(fp32 tensor, stride): stride 0 shares one scale, 1 reads one per head."""
+    t = _one(device) if scale is None else torch.as_tensor(scale, dtype=torch.float32, device=device)
+    if t.numel() == 1:
+        return t.reshape(1), 0
+    if t.numel() == heads:
+        return t.reshape(heads).contiguous(), 1
+    raise ValueError(f"an FP8 scale is one value or one per KV head ({heads}); got {t.numel()} values")
 
 
-def _store_code(x, cache):
-    if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
-        raise TypeError("input dtype must be float16, bfloat16 or float32")
-    if cache.dtype != torch.float8_e4m3fn and cache.dtype != x.dtype:
-        raise TypeError("cache dtype must match input or be float8_e4m3fn")
-    return _lib.DTYPE_CODE[x.dtype], _lib.DTYPE_CODE[cache.dtype]
+def _per_request(value, count, device, name):
+    """An int32 [count] device tensor from an int, a 1-element or a [count] tensor."""
+    t = torch.as_tensor(0 if value is None else value, dtype=torch.int32, device=device)
+    if t.numel() == 1:
+        t = t.reshape(1).expand(count)
+    if t.numel() != count:
+        raise ValueError(f"{name}: expected 1 or {count} values, got {t.numel()}")
+    return t.contiguous()
 
 
-def _desc(x, cache, scale, tensor_strides, keep):
+def _write_desc(x, cache, scale, x_strides, keep):
+    """fa_store_desc for writing `x` rows into `cache` (checks the dtype pair)."""
+    if x.dtype not in _INPUT_TYPES:
+        raise TypeError(f"cache inputs are float16, bfloat16 or float32; got {x.dtype}")
+    fp8 = cache.dtype == torch.float8_e4m3fn
+    if not fp8 and cache.dtype != x.dtype:
+        raise TypeError(f"a {cache.dtype} cache cannot take {x.dtype} rows (use the same dtype or float8_e4m3fn)")
     d = _lib.StoreDesc()
-    xc, cc = _store_code(x, cache)
     d.x, d.cache = x.data_ptr(), cache.data_ptr()
-    d.x_dtype, d.cache_dtype = xc, cc
+    d.x_dtype, d.cache_dtype = _lib.DTYPE_CODE[x.dtype], _lib.DTYPE_CODE[cache.dtype]
     d.heads, d.dim = x.shape[-2], x.shape[-1]
-    d.x_stride[:] = tensor_strides
-    d.cache_stride[:] = list(cache.stride())
-    if cache.dtype == torch.float8_e4m3fn:
-        s, stride = _scale(scale, x.shape[-2], x.device)
+    d.x_stride[:] = x_strides
+    d.cache_stride[:] = cache.stride()
+    if fp8:
+        s, stride = _per_head_scale(scale, x.shape[-2], x.device)
         keep.append(s)
         d.scale, d.scale_stride = s.data_ptr(), stride
     return d
 
 
+def _check_cache_shape(x, cache, row_dims):
+    """cache [pages, page_size, heads, dim] matching the (heads, dim) of x."""
+    if cache.ndim != 4 or tuple(cache.shape[2:]) != tuple(x.shape[row_dims:]):
+        raise ValueError(f"cache {tuple(cache.shape)} must be [pages, page_size, {x.shape[-2]}, {x.shape[-1]}]")
+
+
 def store_kvcache(k, v, k_cache, v_cache, slot_mapping, *, k_scale=None, v_scale=None):
-    """Scatter [tokens, heads, dim] K/V into physical cache slots; -1 skips."""
-    _gpu(k, v, k_cache, v_cache, slot_mapping)
+    """Write k/v [T, Hkv, D] to the cache slots slot_mapping [T] (int32/int64)."""
+    _require_gpu(k=k, v=v, k_cache=k_cache, v_cache=v_cache, slot_mapping=slot_mapping)
     if k.ndim != 3 or v.ndim != 3 or k.shape[:2] != v.shape[:2]:
-        raise ValueError("K/V must have matching [tokens, heads, dim] shapes")
+        raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} must be [tokens, heads, dim] "
+                         "with the same tokens and heads")
     if (slot_mapping.ndim != 1 or slot_mapping.numel() != k.shape[0]
             or slot_mapping.dtype not in (torch.int32, torch.int64)):
-        raise ValueError("slot_mapping must be int32/int64 with one slot per token")
-    for x, cache in ((k, k_cache), (v, v_cache)):
-        if cache.ndim != 4 or cache.shape[2:] != x.shape[1:]:
-            raise ValueError("cache must have shape [blocks, block_size, heads, dim]")
+        raise ValueError(f"slot_mapping must be int32/int64 with one entry per token ({k.shape[0]})")
+    _check_cache_shape(k, k_cache, 1)
+    _check_cache_shape(v, v_cache, 1)
     if k_cache.shape[:2] != v_cache.shape[:2]:
-        raise ValueError("K and V caches must have the same pages and page size")
+        raise ValueError("the K and V caches must have the same pages and page size")
+    writes = [(x, c, s) for x, c, s in ((k, k_cache, k_scale), (v, v_cache, v_scale)) if x.numel()]
+    if not writes:
+        return
     keep = []
     args = _lib.StoreArgs()
-    pairs = [(x, c, s) for x, c, s in ((k, k_cache, k_scale), (v, v_cache, v_scale)) if x.numel()]
-    if not pairs or k.shape[0] == 0:
-        return
-    for i, (x, c, s) in enumerate(pairs):
-        args.kv[i] = _desc(x, c, s, list(x.stride()), keep)
+    for i, (x, c, s) in enumerate(writes):
+        args.kv[i] = _write_desc(x, c, s, x.stride(), keep)
     args.slots = slot_mapping.data_ptr()
     args.slot_dtype = _lib.I64 if slot_mapping.dtype == torch.int64 else _lib.I32
     args.slot_stride = slot_mapping.stride(0)
-    args.tokens = k.shape[0]
-    args.page_size = k_cache.shape[1]
-    args.num_pages = k_cache.shape[0]
+    args.tokens, args.page_size, args.num_pages = k.shape[0], k_cache.shape[1], k_cache.shape[0]
     _lib.call("fa_store_kvcache", args, k.device)
-
-
-def _integers(value, count, device):
-    if value is None:
-        value = 0
-    value = torch.as_tensor(value, dtype=torch.int32, device=device)
-    if value.numel() == 1:
-        value = value.reshape(1).expand(count)
-    if value.numel() != count:
-        raise ValueError(f"expected {count} integer values")
-    return value.contiguous()
 
 
 def append_kvcache(k, v, k_cache, v_cache, cache_seqlens, *, cache_batch_idx=None,
                    cache_leftpad=None, block_table=None, k_scale=None, v_scale=None):
-    """Append [batch, new_tokens, heads, dim] K/V at cache_seqlens[b] + j without
-    changing the lengths (flash_attn_mps/_cache.py:99-127)."""
-    _gpu(k, v, k_cache, v_cache, block_table)
+    """Write k/v [B, Snew, Hkv, D] at position cache_seqlens[b] + j of request b.
+
+    Dense caches [rows, capacity, Hkv, D] take row ``cache_batch_idx[b]``
+    (default b); with ``block_table`` [rows, pages] the position goes through
+    the table.  cache_leftpad does not move the write: FA2 lengths already
+    count the padding (flash_attn_mps/_cache.py:99-127).
+    """
+    _require_gpu(k=k, v=v, k_cache=k_cache, v_cache=v_cache, block_table=block_table)
     if k.ndim != 4 or v.ndim != 4 or k.shape[:3] != v.shape[:3]:
-        raise ValueError("K/V must have matching [batch, new_tokens, heads, dim] shapes")
+        raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} must be [batch, new_tokens, heads, dim] "
+                         "with the same batch, tokens and heads")
     batch = k.shape[0]
-    lengths = _integers(cache_seqlens, batch, k.device)
-    remap = block_table is None and cache_batch_idx is not None
-    indices = _integers(cache_batch_idx, batch, k.device) if remap else None
-    # FA2 lengths are physical exclusive ends that already include left padding,
-    # so new tokens go to length + j, never length + leftpad + j.
+    lengths = _per_request(cache_seqlens, batch, k.device, "cache_seqlens")
+    rows = None
+    if block_table is None and cache_batch_idx is not None:
+        rows = _per_request(cache_batch_idx, batch, k.device, "cache_batch_idx")
     if cache_leftpad is not None:
-        _integers(cache_leftpad, batch, k.device)
+        _per_request(cache_leftpad, batch, k.device, "cache_leftpad")
     if block_table is not None and block_table.ndim != 2:
-        raise ValueError("block_table must have shape [cache_batch, blocks_per_sequence]")
+        raise ValueError(f"block_table must be [rows, pages]; got {tuple(block_table.shape)}")
     table = None if block_table is None else block_table.to(torch.int32).contiguous()
-    for x, cache in ((k, k_cache), (v, v_cache)):
-        if cache.ndim != 4 or cache.shape[2:] != x.shape[2:]:
-            raise ValueError("cache must have shape [rows, capacity, heads, dim]")
-    keep = [lengths, indices, table]
-    pairs = [(x, c, s) for x, c, s in ((k, k_cache, k_scale), (v, v_cache, v_scale)) if x.numel()]
-    if not pairs:
+    _check_cache_shape(k, k_cache, 2)
+    _check_cache_shape(v, v_cache, 2)
+    writes = [(x, c, s) for x, c, s in ((k, k_cache, k_scale), (v, v_cache, v_scale)) if x.numel()]
+    if not writes:
         return
+    keep = [lengths, rows, table]
     args = _lib.AppendArgs()
-    for i, (x, c, s) in enumerate(pairs):
-        args.kv[i] = _desc(x, c, s, list(x.stride())[1:], keep)
+    for i, (x, c, s) in enumerate(writes):
+        args.kv[i] = _write_desc(x, c, s, x.stride()[1:], keep)
         args.x_batch_stride[i] = x.stride(0)
     args.lengths = lengths.data_ptr()
-    args.batch_index = _lib.ptr(indices)
+    args.batch_index = _lib.ptr(rows)
     args.block_table = _lib.ptr(table)
     args.batch, args.new_tokens = batch, k.shape[1]
     args.page_size, args.num_blocks = k_cache.shape[1], k_cache.shape[0]
-    args.table_rows = 0 if table is None else table.shape[0]
-    args.table_cols = 0 if table is None else table.shape[1]
+    args.table_rows, args.table_cols = (0, 0) if table is None else tuple(table.shape)
     _lib.call("fa_append_kvcache", args, k.device)
 
 
-def rotary(q, k, cos, sin, cache_seqlens, *, rotary_interleaved=True, causal=False,
-           window_size=(-1, -1)):
-    """Rotate new K at old_length + j and Q at its causal/local absolute position
-    (flash_attn_mps/_cache.py:130-155); returns new contiguous tensors."""
-    _gpu(q, k, cos, sin)
-    if q.ndim != 4 or (k is not None and (k.ndim != 4 or q.shape[0] != k.shape[0])):
-        raise ValueError("Q/K must have shape [batch, tokens, heads, dim]")
-    if cos.ndim != 2 or sin.shape != cos.shape or cos.shape[1] * 2 > q.shape[-1]:
-        raise ValueError("rotary cosine/sine must have shape [positions, rotary_dim/2]")
-    cosine, sine = cos.float().contiguous(), sin.float().contiguous()
-    lengths = _integers(cache_seqlens, q.shape[0], q.device)
-    outputs = []
-    for x, advance in ((q, causal or tuple(window_size) != (-1, -1)), (k, True)):
+def rotary(q, k, cos, sin, cache_seqlens, *, rotary_interleaved=True, causal=False, window_size=(-1, -1)):
+    """Rotary embedding of q [B, Sq, Hq, D] and new k [B, Snew, Hkv, D] (fresh tensors).
+
+    cos/sin are [positions, rotary_dim / 2]; the first rotary_dim dims rotate
+    as interleaved pairs (2i, 2i+1) or as halves (i, i + rotary_dim / 2).  New
+    key j sits at cache_seqlens[b] + j; queries advance with j only for causal
+    or local attention, else all sit at cache_seqlens[b]
+    (flash_attn_mps/_cache.py:130-155).  A position past the table rotates to NaN.
+    """
+    _require_gpu(q=q, k=k, cos=cos, sin=sin)
+    if q.ndim != 4 or (k is not None and (k.ndim != 4 or k.shape[0] != q.shape[0])):
+        raise ValueError("q and k must be [batch, tokens, heads, dim] with one batch")
+    if cos.ndim != 2 or sin.shape != cos.shape or 2 * cos.shape[1] > q.shape[-1]:
+        raise ValueError(f"cos/sin must be [positions, rotary_dim / 2] with rotary_dim <= {q.shape[-1]}; "
+                         f"got {tuple(cos.shape)} / {tuple(sin.shape)}")
+    cos32, sin32 = cos.float().contiguous(), sin.float().contiguous()
+    lengths = _per_request(cache_seqlens, q.shape[0], q.device, "cache_seqlens")
+    query_moves = bool(causal) or tuple(window_size) != (-1, -1)
+    rotated = []
+    for x, advance in ((q, query_moves), (k, True)):
         if x is None:
-            outputs.append(None)
+            rotated.append(None)
             continue
-        if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
-            raise TypeError("rotary supports float16, bfloat16 and float32")
-        if cos.shape[1] * 2 > x.shape[-1]:
-            raise ValueError("rotary dimension exceeds head dimension")
-        output = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+        if x.dtype not in _INPUT_TYPES:
+            raise TypeError(f"rotary embedding takes float16, bfloat16 or float32; got {x.dtype}")
+        if 2 * cos.shape[1] > x.shape[-1]:
+            raise ValueError(f"rotary_dim {2 * cos.shape[1]} exceeds the head dim {x.shape[-1]}")
+        y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
         if x.numel():
-            args = _lib.RotaryArgs()
-            args.x, args.out = x.data_ptr(), output.data_ptr()
-            args.cos_table, args.sin_table = cosine.data_ptr(), sine.data_ptr()
-            args.lengths = lengths.data_ptr()
-            args.dtype = _lib.DTYPE_CODE[x.dtype]
-            args.interleaved, args.advance = int(rotary_interleaved), int(bool(advance))
-            args.batch, args.seq, args.heads, args.dim = x.shape
-            args.half_rot, args.table_rows = cos.shape[1], cos.shape[0]
-            args.x_stride[:] = list(x.stride())
-            _lib.call("fa_rotary", args, x.device)
-        outputs.append(output)
-    return tuple(outputs)
+            a = _lib.RotaryArgs()
+            a.x, a.out = x.data_ptr(), y.data_ptr()
+            a.cos_table, a.sin_table, a.lengths = cos32.data_ptr(), sin32.data_ptr(), lengths.data_ptr()
+            a.dtype = _lib.DTYPE_CODE[x.dtype]
+            a.interleaved, a.advance = int(bool(rotary_interleaved)), int(advance)
+            a.batch, a.seq, a.heads, a.dim = x.shape
+            a.half_rot, a.table_rows = cos.shape[1], cos.shape[0]
+            a.x_stride[:] = x.stride()
+            _lib.call("fa_rotary", a, x.device)
+        rotated.append(y)
+    return tuple(rotated)

@@ -1,160 +1,68 @@
-"""Inference-only FlashAttention interfaces for PyTorch tensors on MI355X.
+"""FlashAttention-2 inference API for PyTorch-ROCm tensors on MI355X.
 
-Drop-in counterpart of flash_attn_mps/interface.py: the same public names,
-signatures, defaults, FlashAttention-2 layouts, LSE shapes and error classes
-(ValueError for shapes/devices/metadata, TypeError for dtype classes and mask
-objects, NotImplementedError for training features).  Every check runs on the
-host before any kernel is enqueued.  Tensors live on the GPU ('cuda' device
-type under PyTorch-ROCm) instead of 'mps'.
+Drop-in for flash_attn_mps/interface.py: the same public functions,
+positional order, defaults, keyword-only markers, tensor layouts and LSE
+shapes (``[Hq, T]`` for varlen, ``[B, Hq, Sq]`` for dense and KV-cache calls),
+on 'cuda' (HIP) tensors where the reference takes 'mps' ones.
+
+Each function only adapts its layout: dense batches become packed rows on
+uniform offsets, a dense KV cache becomes a one-column table of cache rows,
+packed QKV/KV tensors become views.  The adapted call is a
+:class:`~flash_attn_mps_amd._problem.Problem`, validated in full on the host
+and then solved by the gfx950 kernels (``_attention.solve``).
 """
-from dataclasses import dataclass
-from functools import lru_cache
+from collections import OrderedDict
 
 import torch
 
+from ._attention import solve
+from ._problem import MaskSpec, Problem, reject_training  # noqa: F401  (MaskSpec: vLLM masks)
 
-@lru_cache(maxsize=64)
-def _uniform_offsets(batch, length, device):
-    """Read-only metadata shared by layers with the same dense batch shape
-    (flash_attn_mps/interface.py:13-17)."""
-    offsets = torch.arange(batch + 1, device=device, dtype=torch.int32)
-    return offsets if length == 1 else offsets * length
+PAGE_MULTIPLE = 16   # paged caches: page sizes the FlashAttention contract accepts
 
 
-@dataclass(frozen=True)
-class MaskSpec:
-    """A supported vLLM mask semantic, not a Python callback to execute
-    (flash_attn_mps/interface.py:20-26)."""
+class _UniformOffsets:
+    """int32 offsets 0, L, 2L, ..., B*L on a device, made once per (device, B, L).
 
-    kind: int
-    sliding_window_left: int = -1
-    clamp_prefix_to_window: bool = False
+    Dense layers of one model reuse a handful of shapes, so a small LRU keeps
+    their offsets resident and a call adds no host-to-device copy (which also
+    keeps dense calls capturable in HIP graphs).  Entries are never written
+    after creation.
+    """
 
+    def __init__(self, capacity=64):
+        self._entries = OrderedDict()
+        self._capacity = capacity
 
-def _reshape(x, *shape):
-    # Reshape FP8 through its bytes so a needed copy keeps the exact payloads.
-    if x.dtype == torch.float8_e4m3fn:
-        return x.view(torch.uint8).reshape(*shape).view(x.dtype)
-    return x.reshape(*shape)
-
-
-def _inference_only(dropout_p, return_attn_probs, *tensors):
-    if dropout_p != 0:
-        raise NotImplementedError("flash-attn-mps-amd implements inference; dropout_p must be 0")
-    if return_attn_probs:
-        raise NotImplementedError(
-            "return_attn_probs is a training/debug interface; use return_softmax_lse=True")
-    if any(t is not None and t.requires_grad for t in tensors):
-        raise NotImplementedError("flash-attn-mps-amd implements inference without backward")
-
-
-def _on_gpu(t, device):
-    return t.device.type == "cuda" and t.device == device
+    def __call__(self, batch, length, device):
+        key = (str(device), batch, length)
+        hit = self._entries.get(key)
+        if hit is None:
+            hit = torch.arange(batch + 1, dtype=torch.int32, device=device) * length
+            self._entries[key] = hit
+            if len(self._entries) > self._capacity:
+                self._entries.popitem(last=False)
+        else:
+            self._entries.move_to_end(key)
+        return hit
 
 
-def _validate(q, k, v, cu_q, cu_k, used_k, block_table, out=None):
-    """flash_attn_mps/interface.py:48-86 with the GPU device in place of MPS."""
-    for name, tensor in (("q", q), ("k", k), ("v", v)):
-        if tensor.device.type != "cuda":
-            raise ValueError(f"{name} must be a GPU (HIP) tensor")
-    if q.ndim != 3 or k.ndim not in (3, 4) or v.ndim != k.ndim:
-        raise ValueError("expected q [T,H,D] and matching packed or paged K/V")
-    if k.shape[:-1] != v.shape[:-1] or q.shape[-1] != k.shape[-1]:
-        raise ValueError("Q/K head dimensions and K/V token/head dimensions must match")
-    if k.shape[-2] == 0 or q.shape[-2] % k.shape[-2]:
-        raise ValueError("query heads must be divisible by KV heads")
-    if not (1 <= q.shape[-1] <= 512 and 1 <= v.shape[-1] <= 512):
-        raise ValueError("head dimensions must be between 1 and 512")
-    if cu_q.ndim != 1 or cu_q.numel() < 1 or cu_q.dtype != torch.int32:
-        raise ValueError("cu_seqlens_q must be int32 [batch+1]")
-    batch = cu_q.numel() - 1
-    if (cu_k is None) == (used_k is None):
-        raise ValueError("provide exactly one of cu_seqlens_k and seqused_k")
-    for name, tensor, shape in (
-        ("cu_seqlens_q", cu_q, (batch + 1,)),
-        ("cu_seqlens_k", cu_k, (batch + 1,)),
-        ("seqused_k", used_k, (batch,)),
-    ):
-        if tensor is not None and (
-            tensor.device != q.device or tensor.dtype != torch.int32
-            or tuple(tensor.shape) != shape
-        ):
-            raise ValueError(f"{name} must be a GPU int32 tensor of shape {shape}")
-    if block_table is not None:
-        if (k.ndim != 4 or block_table.ndim != 2
-                or block_table.shape[0] != batch or block_table.dtype != torch.int32
-                or block_table.device != q.device):
-            raise ValueError("paged KV requires a GPU int32 block_table [B,P]")
-    elif k.ndim != 3:
-        raise ValueError("4D KV requires block_table")
-    if out is not None and (
-        tuple(out.shape) != (q.shape[0], q.shape[1], v.shape[-1])
-        or out.device != q.device
-    ):
-        raise ValueError("out must have shape [total_q, query_heads, value_head_dim] on the GPU")
+_offsets = _UniformOffsets()
 
 
-def _run(q, k, v, *, cu_seqlens_q, cu_seqlens_k=None, seqused_k=None,
-         max_seqlen_q, max_seqlen_k, block_table=None, softmax_scale=None,
-         causal=False, window_size=(-1, -1), alibi_slopes=None, softcap=0.0,
-         s_aux=None, q_descale=None, k_descale=None, v_descale=None, out=None,
-         num_splits=0, mask_mod=None, aux_tensors=None, leftpad_k=None,
-         deterministic=False):
-    """Validate every argument, then dispatch (flash_attn_mps/interface.py:89-147)."""
-    _inference_only(0, False, q, k, v, alibi_slopes, s_aux,
-                    q_descale, k_descale, v_descale, out)
-    _validate(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, block_table, out)
-    if len(window_size) != 2 or min(window_size) < -1:
-        raise ValueError("window_size must contain two bounds >= -1")
-    if softcap < 0 or num_splits < 0 or max_seqlen_q < 0 or max_seqlen_k < 0:
-        raise ValueError("softcap, lengths, and num_splits must be nonnegative")
-    if mask_mod is not None and not isinstance(mask_mod, MaskSpec):
-        raise TypeError("mask_mod must be an mm_prefix_mask() or rswa_mask() descriptor")
-    batch, heads, kvheads = cu_seqlens_q.numel() - 1, q.shape[1], k.shape[-2]
-    if torch.is_tensor(causal) and (
-        tuple(causal.shape) != (batch,) or causal.dtype != torch.bool or causal.device != q.device
-    ):
-        raise ValueError("dynamic causal must be a GPU bool [B] tensor")
-    for name, tensor in (("q_descale", q_descale), ("k_descale", k_descale),
-                         ("v_descale", v_descale)):
-        if tensor is not None and (
-            tuple(tensor.shape) != (batch, kvheads) or tensor.dtype != torch.float32
-            or tensor.device != q.device
-        ):
-            raise ValueError(f"{name} must be a GPU float32 [B,Hkv] tensor")
-    if alibi_slopes is not None and (
-        tuple(alibi_slopes.shape) not in ((heads,), (batch, heads))
-        or alibi_slopes.device != q.device or alibi_slopes.dtype != torch.float32
-    ):
-        raise ValueError("alibi_slopes must be GPU float32 [Hq] or [B,Hq]")
-    if s_aux is not None and (tuple(s_aux.shape) != (heads,) or s_aux.device != q.device):
-        raise ValueError("s_aux must be a GPU [Hq] tensor")
-    if mask_mod is not None:
-        if mask_mod.kind not in (1, 2) or aux_tensors is None or len(aux_tensors) != 2:
-            raise ValueError("a supported mask requires its two auxiliary tensors")
-        shapes = ((q.shape[0], 2), (batch + 1,)) if mask_mod.kind == 1 else ((batch,), (1,))
-        for tensor, shape in zip(aux_tensors, shapes):
-            if tuple(tensor.shape) != shape or tensor.dtype != torch.int32 or tensor.device != q.device:
-                raise ValueError(f"mask auxiliary tensor must be GPU int32 {shape}")
-    elif aux_tensors is not None:
-        raise ValueError("aux_tensors require a mask descriptor")
-    if q.dtype not in (torch.float16, torch.bfloat16, torch.float32, torch.float8_e4m3fn):
-        raise TypeError("attention supports FP16, BF16, FP32 and FP8 E4M3FN")
-    if out is not None and out.dtype not in (torch.float16, torch.bfloat16, torch.float32):
-        raise TypeError("out must have FP16, BF16 or FP32 dtype")
-    from ._attention import attention
+def _check_page_size(k):
+    if k.ndim != 4 or k.shape[1] % PAGE_MULTIPLE:
+        raise ValueError(f"a paged cache needs [pages, page_size, heads, dim] with page_size a multiple "
+                         f"of {PAGE_MULTIPLE}; got shape {tuple(k.shape)}")
 
-    kwargs = dict(
-        cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_seqlens_k,
-        seqused_k=seqused_k, max_seqlen_q=max_seqlen_q,
-        max_seqlen_k=max_seqlen_k, block_table=block_table,
-        softmax_scale=softmax_scale, causal=causal, window_size=window_size,
-        alibi_slopes=alibi_slopes, softcap=softcap, s_aux=s_aux,
-        q_descale=q_descale, k_descale=k_descale, v_descale=v_descale,
-        out=out, num_splits=num_splits, mask_mod=mask_mod, aux_tensors=aux_tensors,
-        leftpad_k=leftpad_k, deterministic=deterministic,
-    )
-    return attention(q, k, v, **kwargs)
+
+def _dense_lse(lse, batch, seqlen):
+    """[Hq, B*S] -> [B, Hq, S] (a view)."""
+    return lse.reshape(lse.shape[0], batch, seqlen).transpose(0, 1)
+
+
+def _finish(out, lse, return_lse):
+    return (out, lse) if return_lse else out
 
 
 def flash_attn_varlen_func(
@@ -163,19 +71,23 @@ def flash_attn_varlen_func(
     softcap=0.0, alibi_slopes=None, deterministic=False, return_attn_probs=False,
     block_table=None, *, return_softmax_lse=False, out=None,
 ):
-    """Packed or paged variable-length attention with lower-right causality."""
-    _inference_only(dropout_p, return_attn_probs, q, k, v)
+    """Variable-length attention over packed requests.
+
+    q [T, Hq, Dqk]; k/v packed [Tk, Hkv, D] or, with ``block_table`` [B, pages],
+    paged [pages, page_size, Hkv, D] (request lengths still come from
+    ``cu_seqlens_k``).  Causality is lower-right aligned per request.
+    ``deterministic`` fixes the per-row reduction order (one split).
+    Returns ``out`` [T, Hq, Dv], plus LSE [Hq, T] with ``return_softmax_lse``.
+    """
+    reject_training(dropout_p, return_attn_probs, (q, k, v))
     if block_table is not None:
-        if k.ndim != 4 or k.shape[1] % 16:
-            raise ValueError("paged KV requires a page size divisible by 16")
-    result, lse = _run(
-        q, k, v, cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_seqlens_k,
-        max_seqlen_q=max_seqlen_q, max_seqlen_k=max_seqlen_k,
-        block_table=block_table, softmax_scale=softmax_scale, causal=causal,
-        window_size=window_size, softcap=softcap, alibi_slopes=alibi_slopes,
-        num_splits=1 if deterministic else 0, out=out, deterministic=deterministic,
-    )
-    return (result, lse) if return_softmax_lse else result
+        _check_page_size(k)
+    problem = Problem(q, k, v, cu_seqlens_q, max_seqlen_q, max_seqlen_k, cu_k=cu_seqlens_k,
+                      table=block_table, scale=softmax_scale, causal=causal, window=tuple(window_size),
+                      softcap=softcap, alibi=alibi_slopes, out=out,
+                      splits=1 if deterministic else 0, deterministic=deterministic)
+    result, lse = solve(problem.validate())
+    return _finish(result, lse, return_softmax_lse)
 
 
 def flash_attn_func(
@@ -183,59 +95,72 @@ def flash_attn_func(
     window_size=(-1, -1), softcap=0.0, alibi_slopes=None,
     deterministic=False, return_attn_probs=False, *, return_softmax_lse=False,
 ):
-    """Dense attention: Q [B,Sq,Hq,D], K/V [B,Sk,Hkv,D]."""
-    if (q.ndim != 4 or k.ndim != 4 or v.ndim != 4 or q.shape[0] != k.shape[0]
-            or k.shape[:3] != v.shape[:3]):
-        raise ValueError("dense attention requires matching 4D batches")
-    batch, sq = q.shape[:2]
-    sk = k.shape[1]
-    cu_q = _uniform_offsets(batch, sq, q.device)
-    cu_k = _uniform_offsets(batch, sk, q.device)
+    """Dense batched attention: q [B, Sq, Hq, Dqk], k/v [B, Sk, Hkv, D].
+
+    Returns ``out`` [B, Sq, Hq, Dv], plus LSE [B, Hq, Sq] with ``return_softmax_lse``.
+    """
+    if not (q.ndim == k.ndim == v.ndim == 4):
+        raise ValueError("dense attention takes 4-D q [B, Sq, Hq, D] and k/v [B, Sk, Hkv, D]")
+    if q.shape[0] != k.shape[0] or k.shape[:3] != v.shape[:3]:
+        raise ValueError(f"batch/length/head extents disagree: q {tuple(q.shape)}, "
+                         f"k {tuple(k.shape)}, v {tuple(v.shape)}")
+    batch, sq, sk = q.shape[0], q.shape[1], k.shape[1]
     out, lse = flash_attn_varlen_func(
-        _reshape(q, -1, *q.shape[2:]), _reshape(k, -1, *k.shape[2:]),
-        _reshape(v, -1, *v.shape[2:]), cu_q, cu_k, sq, sk,
+        q.flatten(0, 1), k.flatten(0, 1), v.flatten(0, 1),
+        _offsets(batch, sq, q.device), _offsets(batch, sk, q.device), sq, sk,
         dropout_p, softmax_scale, causal, window_size, softcap, alibi_slopes,
         deterministic, return_attn_probs, return_softmax_lse=True,
     )
-    out = out.reshape(batch, sq, q.shape[2], v.shape[-1])
-    lse = lse.reshape(q.shape[2], batch, sq).transpose(0, 1)
-    return (out, lse) if return_softmax_lse else out
+    out = out.unflatten(0, (batch, sq))
+    return _finish(out, _dense_lse(lse, batch, sq), return_softmax_lse)
 
 
 def flash_attn_qkvpacked_func(qkv, *args, **kwargs):
-    """Dense QKV [B,S,3,H,D]."""
+    """Dense attention on one packed tensor qkv [B, S, 3, H, D]."""
     if qkv.ndim != 5 or qkv.shape[2] != 3:
-        raise ValueError("qkv must have shape [B,S,3,H,D]")
-    return flash_attn_func(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], *args, **kwargs)
+        raise ValueError(f"qkv must be [B, S, 3, H, D]; got {tuple(qkv.shape)}")
+    q, k, v = qkv.unbind(2)
+    return flash_attn_func(q, k, v, *args, **kwargs)
 
 
 def flash_attn_kvpacked_func(q, kv, *args, **kwargs):
-    """Dense Q [B,Sq,Hq,D], KV [B,Sk,2,Hkv,D]."""
+    """Dense attention with q [B, Sq, Hq, D] and kv [B, Sk, 2, Hkv, D]."""
     if kv.ndim != 5 or kv.shape[2] != 2:
-        raise ValueError("kv must have shape [B,S,2,H,D]")
-    return flash_attn_func(q, kv[:, :, 0], kv[:, :, 1], *args, **kwargs)
+        raise ValueError(f"kv must be [B, S, 2, H, D]; got {tuple(kv.shape)}")
+    k, v = kv.unbind(2)
+    return flash_attn_func(q, k, v, *args, **kwargs)
 
 
 def flash_attn_varlen_qkvpacked_func(qkv, cu_seqlens, max_seqlen, *args, **kwargs):
-    """Packed QKV [T,3,H,D]."""
+    """Varlen self-attention on qkv [T, 3, H, D] (queries and keys share offsets)."""
     if qkv.ndim != 4 or qkv.shape[1] != 3:
-        raise ValueError("qkv must have shape [T,3,H,D]")
-    return flash_attn_varlen_func(
-        qkv[:, 0], qkv[:, 1], qkv[:, 2], cu_seqlens, cu_seqlens,
-        max_seqlen, max_seqlen, *args, **kwargs,
-    )
+        raise ValueError(f"qkv must be [T, 3, H, D]; got {tuple(qkv.shape)}")
+    q, k, v = qkv.unbind(1)
+    return flash_attn_varlen_func(q, k, v, cu_seqlens, cu_seqlens, max_seqlen, max_seqlen, *args, **kwargs)
 
 
-def flash_attn_varlen_kvpacked_func(
-    q, kv, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, *args, **kwargs,
-):
-    """Packed KV [T,2,Hkv,D]."""
+def flash_attn_varlen_kvpacked_func(q, kv, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                                    *args, **kwargs):
+    """Varlen attention with q [T, Hq, D] and kv [Tk, 2, Hkv, D]."""
     if kv.ndim != 4 or kv.shape[1] != 2:
-        raise ValueError("kv must have shape [T,2,H,D]")
-    return flash_attn_varlen_func(
-        q, kv[:, 0], kv[:, 1], cu_seqlens_q, cu_seqlens_k,
-        max_seqlen_q, max_seqlen_k, *args, **kwargs,
-    )
+        raise ValueError(f"kv must be [T, 2, H, D]; got {tuple(kv.shape)}")
+    k, v = kv.unbind(1)
+    return flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                                  *args, **kwargs)
+
+
+def _cache_lengths(cache_seqlens, batch, k_new, table, capacity, device):
+    """cache_seqlens as an int32 [B] device tensor (the caller's, never modified)."""
+    if cache_seqlens is None:
+        if k_new is not None or table is not None:
+            raise ValueError("cache_seqlens is required to append to a cache or to read a paged one")
+        cache_seqlens = capacity
+    if isinstance(cache_seqlens, int):
+        return torch.full((batch,), cache_seqlens, dtype=torch.int32, device=device)
+    if (not torch.is_tensor(cache_seqlens) or tuple(cache_seqlens.shape) != (batch,)
+            or cache_seqlens.dtype != torch.int32 or cache_seqlens.device != device):
+        raise ValueError(f"cache_seqlens must be an int or an int32 [{batch}] tensor on {device}")
+    return cache_seqlens
 
 
 def flash_attn_with_kvcache(
@@ -245,73 +170,55 @@ def flash_attn_with_kvcache(
     rotary_interleaved=True, alibi_slopes=None, num_splits=0,
     return_softmax_lse=False,
 ):
-    """Attention over a cache, optionally appending KV at the supplied old lengths.
+    """Attention of q [B, Sq, Hq, D] over a KV cache, optionally appending first.
 
-    Cache lengths are not mutated.  They specify the physical exclusive end,
-    before append when k/v are provided.  cache_leftpad excludes an initial
-    portion of a dense cache from attention without changing append positions.
+    The cache is dense [rows, capacity, Hkv, D] (request b reads row
+    ``cache_batch_idx[b]``, default b) or paged [pages, page_size, Hkv, D]
+    through ``block_table``.  ``cache_seqlens`` are the lengths before the
+    append and are never modified; new k/v [B, Snew, Hkv, D] land at
+    ``cache_seqlens[b] + j`` (after an optional rotary embedding of q and k).
+    ``cache_leftpad`` hides the first positions of a dense cache row from
+    attention without moving where appends go.
+    Returns ``out`` [B, Sq, Hq, Dv], plus LSE [B, Hq, Sq] with ``return_softmax_lse``.
     """
-    _inference_only(0, False, q, k, v, k_cache, v_cache)
-    if q.ndim != 4 or k_cache.ndim != 4 or v_cache.ndim != 4:
-        raise ValueError("q and KV caches must be 4D")
+    reject_training(0.0, False, (q, k, v, k_cache, v_cache))
+    if not (q.ndim == k_cache.ndim == v_cache.ndim == 4):
+        raise ValueError("q and both caches must be 4-D")
     if (k is None) != (v is None):
-        raise ValueError("k and v must be provided together")
-    if block_table is not None and cache_leftpad is not None:
-        raise ValueError("FlashAttention does not combine paged cache with cache_leftpad")
-    if block_table is not None and k_cache.shape[1] % 16:
-        raise ValueError("paged KV requires a page size divisible by 16")
-    batch, sq = q.shape[:2]
-    if cache_seqlens is None:
-        if k is not None or block_table is not None:
-            raise ValueError("cache_seqlens is required for append or paged cache")
-        cache_seqlens = k_cache.shape[1]
-    if isinstance(cache_seqlens, int):
-        lengths = torch.full((batch,), cache_seqlens, device=q.device, dtype=torch.int32)
-    else:
-        lengths = cache_seqlens
-    if (tuple(lengths.shape) != (batch,) or lengths.dtype != torch.int32
-            or lengths.device != q.device):
-        raise ValueError("cache_seqlens must be an int or GPU int32 [B]")
+        raise ValueError("new k and v come together")
+    if block_table is not None:
+        if cache_leftpad is not None:
+            raise ValueError("cache_leftpad applies to dense caches only, not to a block_table")
+        _check_page_size(k_cache)
+    batch, sq = q.shape[0], q.shape[1]
+    lengths = _cache_lengths(cache_seqlens, batch, k, block_table, k_cache.shape[1], q.device)
     if (rotary_cos is None) != (rotary_sin is None):
-        raise ValueError("rotary_cos and rotary_sin must be provided together")
+        raise ValueError("rotary_cos and rotary_sin come together")
     if rotary_cos is not None:
         if k is None:
-            raise ValueError("rotary embedding requires new k and v")
+            raise ValueError("a rotary embedding is applied to new k/v only; none were given")
         from ._cache import rotary
-        q, k = rotary(
-            q, k, rotary_cos, rotary_sin, lengths,
-            rotary_interleaved=rotary_interleaved, causal=causal, window_size=window_size,
-        )
+        q, k = rotary(q, k, rotary_cos, rotary_sin, lengths, rotary_interleaved=rotary_interleaved,
+                      causal=causal, window_size=window_size)
     if k is not None:
         if k.ndim != 4 or v.ndim != 4 or k.shape[0] != batch or v.shape[:3] != k.shape[:3]:
-            raise ValueError("new k/v must have matching [B,Snew,Hkv,D] dimensions")
+            raise ValueError(f"new k {tuple(k.shape)} / v {tuple(v.shape)} must be [{batch}, Snew, Hkv, D]")
         from ._cache import append_kvcache
-        append_kvcache(
-            k, v, k_cache, v_cache, lengths, cache_batch_idx=cache_batch_idx,
-            cache_leftpad=cache_leftpad, block_table=block_table,
-        )
+        append_kvcache(k, v, k_cache, v_cache, lengths, cache_batch_idx=cache_batch_idx,
+                       cache_leftpad=cache_leftpad, block_table=block_table)
         lengths = lengths + k.shape[1]
-    if block_table is None:
-        indices = cache_batch_idx
-        if indices is None:
-            indices = torch.arange(batch, device=q.device, dtype=torch.int32)
-        table = indices.to(torch.int32).reshape(batch, 1)
-        max_k = k_cache.shape[1]
+    if block_table is not None:
+        # Table rows follow the query batch; cache_batch_idx only remaps dense rows.
+        table, max_k = block_table, block_table.shape[1] * k_cache.shape[1]
     else:
-        # A page table already selects physical storage; its rows correspond
-        # to the query batch even when cache_batch_idx was also supplied.
-        table = block_table
-        max_k = table.shape[1] * k_cache.shape[1]
+        rows = cache_batch_idx if cache_batch_idx is not None else torch.arange(batch, device=q.device)
+        table, max_k = rows.to(torch.int32).reshape(batch, 1), k_cache.shape[1]
     if cache_leftpad is not None:
         lengths = lengths - cache_leftpad
-    cu_q = _uniform_offsets(batch, sq, q.device)
-    out, lse = _run(
-        _reshape(q, -1, *q.shape[2:]), k_cache, v_cache,
-        cu_seqlens_q=cu_q, seqused_k=lengths, max_seqlen_q=sq,
-        max_seqlen_k=max_k, block_table=table, softmax_scale=softmax_scale,
-        causal=causal, window_size=window_size, alibi_slopes=alibi_slopes,
-        softcap=softcap, num_splits=num_splits, leftpad_k=cache_leftpad,
-    )
-    out = out.reshape(batch, sq, q.shape[2], v_cache.shape[-1])
-    lse = lse.reshape(q.shape[2], batch, sq).transpose(0, 1)
-    return (out, lse) if return_softmax_lse else out
+    problem = Problem(q.flatten(0, 1), k_cache, v_cache, _offsets(batch, sq, q.device), sq, max_k,
+                      used_k=lengths, table=table, leftpad=cache_leftpad, scale=softmax_scale,
+                      causal=causal, window=tuple(window_size), softcap=softcap, alibi=alibi_slopes,
+                      splits=num_splits)
+    out, lse = solve(problem.validate())
+    out = out.unflatten(0, (batch, sq))
+    return _finish(out, _dense_lse(lse, batch, sq), return_softmax_lse)

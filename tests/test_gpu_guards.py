@@ -11,8 +11,8 @@ import pytest
 import torch
 
 from flash_attn_mps_amd import _lib
-from flash_attn_mps_amd._attention import build_args
 from flash_attn_mps_amd._cache import rotary
+from harness import kernel_args
 
 pytestmark = pytest.mark.gpu
 
@@ -26,11 +26,8 @@ def _decode_args(device, keys, keep):
     cu_q = torch.tensor([0, 1], device=device, dtype=torch.int32)
     cu_k = torch.tensor([0, keys], device=device, dtype=torch.int32)
     keep += [q, k, v, out, lse, cu_q, cu_k]
-    return build_args(q, k, v, out, lse, cu_seqlens_q=cu_q, cu_seqlens_k=cu_k, seqused_k=None,
-                      max_seqlen_q=1, max_seqlen_k=keys, block_table=None, softmax_scale=None,
-                      causal=False, window_size=(-1, -1), alibi_slopes=None, softcap=0.0, s_aux=None,
-                      q_descale=None, k_descale=None, v_descale=None, mask_mod=None, aux_tensors=None,
-                      leftpad_k=None, keep=keep)
+    return kernel_args(q, k, v, out, lse, keep=keep, cu_seqlens_q=cu_q, cu_seqlens_k=cu_k, max_seqlen_q=1,
+                       max_seqlen_k=keys)
 
 
 def test_decode_rejects_a_split_plan_that_drops_keys(device):

@@ -14,8 +14,7 @@ import pytest
 import torch
 
 from flash_attn_mps_amd import _lib
-from flash_attn_mps_amd._attention import attention, build_args
-from helpers import assert_north_star, attention_reference, cu_from_lengths
+from harness import assert_parity, attention, kernel_args, offsets, oracle_attention
 
 pytestmark = pytest.mark.gpu
 
@@ -30,7 +29,7 @@ def _route(q, k, v, **kw):
                 aux_tensors=None, leftpad_k=None)
     full.update(kw)
     keep = []
-    return _lib.supported("fa_prefill_supported", build_args(q, k, v, out, lse, keep=keep, **full))
+    return _lib.supported("fa_prefill_supported", kernel_args(q, k, v, out, lse, keep=keep, **full))
 
 
 def _case(device, dtype, d, hq, hkv, q_lens, k_lens, seed):
@@ -38,7 +37,7 @@ def _case(device, dtype, d, hq, hkv, q_lens, k_lens, seed):
     q = (torch.randn(sum(q_lens), hq, d, generator=g) * 0.5).to(dtype).to(device)
     k = (torch.randn(sum(k_lens), hkv, d, generator=g) * 0.5).to(dtype).to(device)
     v = torch.randn(sum(k_lens), hkv, d, generator=g).to(dtype).to(device)
-    return q, k, v, cu_from_lengths(q_lens, device), cu_from_lengths(k_lens, device)
+    return q, k, v, offsets(q_lens, device), offsets(k_lens, device)
 
 
 def _bloom_slopes(heads):
@@ -57,8 +56,8 @@ def test_alibi_prefill(device, dtype, d, causal):
               causal=causal, alibi_slopes=slopes)
     assert _route(q, k, v, **kw)
     out, lse = attention(q, k, v, **kw)
-    ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=causal, alibi=slopes)
-    assert_north_star(out, lse, ref, ref_lse, dtype)
+    ref, ref_lse = oracle_attention(q, k, v, cuq, cuk, causal=causal, alibi=slopes)
+    assert_parity(out, lse, ref, ref_lse, dtype)
 
 
 @pytest.mark.parametrize("hq,hkv", [(16, 16), (16, 8), (12, 4), (8, 1)])
@@ -72,8 +71,8 @@ def test_alibi_per_request_slopes_gqa(device, hq, hkv):
               alibi_slopes=slopes)
     assert _route(q, k, v, **kw)
     out, lse = attention(q, k, v, **kw)
-    ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=True, alibi=slopes)
-    assert_north_star(out, lse, ref, ref_lse, torch.bfloat16)
+    ref, ref_lse = oracle_attention(q, k, v, cuq, cuk, causal=True, alibi=slopes)
+    assert_parity(out, lse, ref, ref_lse, torch.bfloat16)
 
 
 def test_alibi_long_keys_steep_slopes(device):
@@ -91,8 +90,8 @@ def test_alibi_long_keys_steep_slopes(device):
     for causal in (True, False):
         out, lse = attention(q, k, v, cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=2048,
                              max_seqlen_k=2048, causal=causal, alibi_slopes=slopes)
-        ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=causal, alibi=slopes)
-        assert_north_star(out, lse, ref, ref_lse, torch.bfloat16)
+        ref, ref_lse = oracle_attention(q, k, v, cuq, cuk, causal=causal, alibi=slopes)
+        assert_parity(out, lse, ref, ref_lse, torch.bfloat16)
 
 
 @pytest.mark.parametrize("page", [16, 128])
@@ -106,7 +105,7 @@ def test_alibi_paged_with_sinks(device, page):
     kc = (torch.randn(pool, page, hkv, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
     vc = torch.randn(pool, page, hkv, d, generator=g).to(torch.bfloat16).to(device)
     q = (torch.randn(sum(q_lens), hq, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
-    cuq = cu_from_lengths(q_lens, device)
+    cuq = offsets(q_lens, device)
     used = torch.tensor(k_lens, dtype=torch.int32, device=device)
     table = table.to(device)
     slopes = _bloom_slopes(hq).to(device)
@@ -115,9 +114,9 @@ def test_alibi_paged_with_sinks(device, page):
               block_table=table, causal=True, alibi_slopes=slopes, s_aux=sinks)
     assert _route(q, kc, vc, **kw)
     out, lse = attention(q, kc, vc, **kw)
-    ref, ref_lse = attention_reference(q, kc, vc, cuq, used_k=used, block_table=table, causal=True,
+    ref, ref_lse = oracle_attention(q, kc, vc, cuq, used_k=used, block_table=table, causal=True,
                                        alibi=slopes, sinks=sinks)
-    assert_north_star(out, lse, ref, ref_lse, torch.bfloat16)
+    assert_parity(out, lse, ref, ref_lse, torch.bfloat16)
 
 
 @pytest.mark.parametrize("extra", ["softcap", "window", "fp8"])
@@ -136,5 +135,5 @@ def test_alibi_combinations_use_generic_kernel(device, extra):
         k, v = k.to(torch.float8_e4m3fn), v.to(torch.float8_e4m3fn)
     assert not _route(q, k, v, **kw)
     out, lse = attention(q, k, v, **kw)
-    ref, ref_lse = attention_reference(q, k, v, cuq, cuk, **ref_kw)
-    assert_north_star(out, lse, ref, ref_lse, torch.float16)
+    ref, ref_lse = oracle_attention(q, k, v, cuq, cuk, **ref_kw)
+    assert_parity(out, lse, ref, ref_lse, torch.float16)

@@ -13,9 +13,8 @@ import pytest
 import torch
 
 from flash_attn_mps_amd import _lib
-from flash_attn_mps_amd._attention import attention, build_args
 from flash_attn_mps_amd.vllm import flash_attn_varlen_func
-from helpers import assert_north_star, attention_reference, cu_from_lengths
+from harness import assert_parity, attention, kernel_args, offsets, oracle_attention
 
 pytestmark = pytest.mark.gpu
 
@@ -27,7 +26,7 @@ def _inputs(device, dtype, hq, hkv, d, q_lens, k_lens, seed):
     v = torch.randn(sum(k_lens), hkv, d, generator=g).to(dtype).to(device)
     flags = torch.rand(len(q_lens), generator=g) < 0.5
     flags[0], flags[-1] = True, False
-    return q, k, v, cu_from_lengths(q_lens, device), cu_from_lengths(k_lens, device), flags.to(device)
+    return q, k, v, offsets(q_lens, device), offsets(k_lens, device), flags.to(device)
 
 
 def _routes_to_mfma(q, k, v, **kw):
@@ -39,7 +38,7 @@ def _routes_to_mfma(q, k, v, **kw):
                 aux_tensors=None, leftpad_k=None)
     full.update(kw)
     keep = []
-    return _lib.supported("fa_prefill_supported", build_args(q, k, v, out, lse, keep=keep, **full))
+    return _lib.supported("fa_prefill_supported", kernel_args(q, k, v, out, lse, keep=keep, **full))
 
 
 @pytest.mark.parametrize("hq,hkv", [(16, 8), (8, 2)])
@@ -51,8 +50,8 @@ def test_causal_flags_packed(device, hq, hkv, window):
               causal=flags, window_size=window)
     assert _routes_to_mfma(q, k, v, **kw)
     out, lse = attention(q, k, v, **kw)
-    ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=flags, window=window)
-    assert_north_star(out, lse, ref, ref_lse, torch.bfloat16)
+    ref, ref_lse = oracle_attention(q, k, v, cuq, cuk, causal=flags, window=window)
+    assert_parity(out, lse, ref, ref_lse, torch.bfloat16)
 
 
 def test_causal_flags_many_requests(device):
@@ -63,8 +62,8 @@ def test_causal_flags_many_requests(device):
     q, k, v, cuq, cuk, flags = _inputs(device, torch.float16, 16, 8, 64, q_lens, k_lens, seed=8)
     out, lse = attention(q, k, v, cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=max(q_lens),
                          max_seqlen_k=max(k_lens), causal=flags)
-    ref, ref_lse = attention_reference(q, k, v, cuq, cuk, causal=flags)
-    assert_north_star(out, lse, ref, ref_lse, torch.float16)
+    ref, ref_lse = oracle_attention(q, k, v, cuq, cuk, causal=flags)
+    assert_parity(out, lse, ref, ref_lse, torch.float16)
 
 
 @pytest.mark.parametrize("page", [16, 64])
@@ -84,12 +83,12 @@ def test_dynamic_causal_vllm_paged(device, page):
             vc[table[b, pos // page], pos % page] = torch.randn(hkv, d, generator=g)
     kc, vc = kc.to(torch.bfloat16).to(device), vc.to(torch.bfloat16).to(device)
     q = (torch.randn(sum(q_lens), hq, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
-    cuq = cu_from_lengths(q_lens, device)
+    cuq = offsets(q_lens, device)
     used = torch.tensor(k_lens, dtype=torch.int32, device=device)
     table = table.to(device)
     flags = torch.tensor([True, False, False, True], device=device)
     out, lse = flash_attn_varlen_func(q, kc, vc, max(q_lens), cuq, cols * page, seqused_k=used,
                                       block_table=table, causal=True, dynamic_causal=flags,
                                       return_softmax_lse=True, fa_version=4)
-    ref, ref_lse = attention_reference(q, kc, vc, cuq, used_k=used, block_table=table, causal=flags)
-    assert_north_star(out, lse, ref, ref_lse, torch.bfloat16)
+    ref, ref_lse = oracle_attention(q, kc, vc, cuq, used_k=used, block_table=table, causal=flags)
+    assert_parity(out, lse, ref, ref_lse, torch.bfloat16)

@@ -13,8 +13,8 @@ import pytest
 import torch
 
 from flash_attn_mps_amd import _lib
-from flash_attn_mps_amd._attention import build_args
-from flash_attn_mps_amd._decode import decode_workgroups_per_token, split_plan
+from flash_attn_mps_amd._decode import split_plan, workgroups_per_token
+from harness import kernel_args
 
 pytestmark = pytest.mark.gpu
 
@@ -50,12 +50,10 @@ def _paged_case(device, *, batch, heads, kvheads, dim, max_ctx, pool_pages, kv_d
 
 
 def _args(t, out, lse, keep):
-    return build_args(t["q"], t["k"], t["v"], out, lse, cu_seqlens_q=t["cu_q"], cu_seqlens_k=None,
-                      seqused_k=t["used"], max_seqlen_q=1, max_seqlen_k=t["max_ctx"],
-                      block_table=t["table"], softmax_scale=None, causal=False, window_size=t["window"],
-                      alibi_slopes=None, softcap=t["softcap"], s_aux=t.get("s_aux"),
-                      q_descale=None, k_descale=t.get("k_descale"), v_descale=t.get("v_descale"),
-                      mask_mod=None, aux_tensors=None, leftpad_k=None, keep=keep)
+    return kernel_args(t["q"], t["k"], t["v"], out, lse, keep=keep, cu_seqlens_q=t["cu_q"], seqused_k=t["used"],
+                       max_seqlen_q=1, max_seqlen_k=t["max_ctx"], block_table=t["table"], window_size=t["window"],
+                       softcap=t["softcap"], s_aux=t.get("s_aux"), k_descale=t.get("k_descale"),
+                       v_descale=t.get("v_descale"))
 
 
 def _outputs(t):
@@ -67,7 +65,7 @@ def _outputs(t):
 
 def _python_plan(t):
     batch, heads, dim = t["q"].shape
-    groups = decode_workgroups_per_token(heads, t["k"].shape[2], dim, dim)
+    groups = workgroups_per_token(heads, t["k"].shape[2], dim, dim)
     wl = t["window"][0]
     visible = min(t["max_ctx"], wl + 1) if wl >= 0 else t["max_ctx"]
     return split_plan(batch, groups, visible, 0)
