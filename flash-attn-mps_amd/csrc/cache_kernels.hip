@@ -6,6 +6,8 @@
 // The gfx950 kernels here move 16-byte vectors per lane when the head
 // dimension is contiguous and aligned, and fall back to one element per lane
 // for arbitrary strides.
+#include <type_traits>
+
 #include "fa_device.h"
 
 namespace {
@@ -98,6 +100,93 @@ __global__ __launch_bounds__(256) void store_kernel(const StoreParams p) {
   }
 }
 
+// Vector path by whole token rows.  A wave stores one token at a time: lane l
+// owns the (head, 16-byte chunk) tasks l, l + 64, ... (TPL per lane, fixed for
+// the kernel, so no element does any division), the slot is read once per
+// token and split into page and row with a shift (power-of-two pages) or one
+// 32-bit division.  FP8: x / scale[h] (correctly rounded, by div_by_scale
+// with the scale's reciprocal) then the integer E4M3 encoder, VEC codes
+// stored as one 8- or 4-byte word.
+template <typename XT, bool FP8, typename IT, int TPL>
+__global__ __launch_bounds__(256) void store_rows_kernel(const StoreParams p, const int log2_page) {
+  constexpr int VEC = 16 / XT::bytes;
+  using S = typename XT::storage;
+  const StoreDescK& d = p.d[blockIdx.y];
+  const int lane = threadIdx.x & 63;
+  const int tasks = (int)(d.heads * d.chunks);
+  int64_t src[TPL], dst[TPL];
+  float scale[TPL], recip[TPL];
+  bool on[TPL], fast_div[TPL];
+#pragma unroll
+  for (int i = 0; i < TPL; ++i) {
+    const int task = lane + 64 * i;
+    on[i] = task < tasks;
+    const int h = on[i] ? task / (int)d.chunks : 0, c = on[i] ? task % (int)d.chunks : 0;
+    src[i] = h * d.xs[1] + (int64_t)c * VEC * d.xs[2];
+    dst[i] = h * d.cs[2] + (int64_t)c * VEC * d.cs[3];
+    scale[i] = FP8 ? d.scale[h * d.scale_stride] : 1.0f;
+    recip[i] = 1.0f / scale[i];                 // IEEE: rounded to nearest
+    fast_div[i] = scale_in_range(scale[i]);
+  }
+  // All of this wave's scales in range (the usual case): the loop below is
+  // instantiated with the reciprocal division only.
+  bool all_fast = true;
+#pragma unroll
+  for (int i = 0; i < TPL; ++i) all_fast = all_fast && fast_div[i];
+  all_fast = __all(all_fast);
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  auto run = [&](auto fast) {
+    for (int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); t < p.tokens; t += nwaves) {
+      const int64_t slot = read_slot<IT>(p.slots, t, p.slot_stride);
+      if (slot < 0 || slot >= p.num_slots) continue;
+      int64_t block, offset;
+      if (log2_page >= 0) {
+        block = slot >> log2_page;
+        offset = slot & ((1ll << log2_page) - 1);
+      } else if (p.num_slots <= 0xffffffffll) {
+        const uint32_t s32 = (uint32_t)slot, ps = (uint32_t)p.page_size;
+        block = s32 / ps;
+        offset = s32 - (uint32_t)block * ps;
+      } else {
+        block = slot / p.page_size;
+        offset = slot - block * p.page_size;
+      }
+      const S* xrow = (const S*)d.x + t * d.xs[0];
+      const int64_t crow = block * d.cs[0] + offset * d.cs[1];
+#pragma unroll
+      for (int i = 0; i < TPL; ++i) {
+        if (!on[i]) continue;
+        const uint4 raw = *(const uint4*)(xrow + src[i]);
+        if constexpr (!FP8) {
+          *(uint4*)((S*)d.cache + crow + dst[i]) = raw;
+        } else {
+          const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+          uint32_t packed[VEC / 4];
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) {
+            float f;
+            if constexpr (XT::bytes == 4) f = __uint_as_float(w[j]);
+            else {
+              const uint32_t half = (w[j / 2] >> (16 * (j & 1))) & 0xffffu;
+              f = XT::id == FA_BF16 ? bf16_bits_to_f32(half) : f16_bits_to_f32(half);
+            }
+            float q;
+            if constexpr (decltype(fast)::value) q = div_by_scale(f, scale[i], recip[i]);
+            else q = f / scale[i];
+            const uint32_t code = e4m3_code(q) & 0xffu;
+            packed[j / 4] = (j & 3) == 0 ? code : packed[j / 4] | (code << (8 * (j & 3)));
+          }
+          uint8_t* out = (uint8_t*)d.cache + crow + dst[i];
+          if constexpr (VEC == 8) *(uint2*)out = make_uint2(packed[0], packed[1]);
+          else *(uint32_t*)out = packed[0];
+        }
+      }
+    }
+  };
+  if (!FP8 || all_fast) run(std::true_type());
+  else run(std::false_type());
+}
+
 int elem_bytes(int dtype) { return dtype == FA_F32 ? 4 : dtype == FA_E4M3 ? 1 : 2; }
 
 bool aligned(const void* p, int64_t a) { return ((uintptr_t)p % (uintptr_t)a) == 0; }
@@ -105,6 +194,25 @@ bool aligned(const void* p, int64_t a) { return ((uintptr_t)p % (uintptr_t)a) ==
 template <typename XT, bool FP8, typename IT>
 int launch_store(const StoreParams& p, bool vec, hipStream_t stream) {
   constexpr int VEC = 16 / XT::bytes;
+  if (vec) {
+    // Token rows of at most 512 tasks (8 per lane) take the row kernel.
+    int64_t tasks = 0;
+    for (int i = 0; i < p.ndesc; ++i) tasks = p.d[i].heads * p.d[i].chunks > tasks ? p.d[i].heads * p.d[i].chunks : tasks;
+    if (tasks <= 512) {
+      int log2_page = -1;
+      if ((p.page_size & (p.page_size - 1)) == 0)
+        for (log2_page = 0; (1ll << log2_page) < p.page_size; ++log2_page) {}
+      int64_t blocks = fa_ceil_div(p.tokens, 4);
+      if (blocks > 2048) blocks = 2048;   // 8 workgroups per CU; each wave then loops over tokens
+      const dim3 grid((unsigned)blocks, (unsigned)p.ndesc);
+      const int tpl = (int)fa_ceil_div(tasks, 64);
+      if (tpl == 1) hipLaunchKernelGGL((store_rows_kernel<XT, FP8, IT, 1>), grid, dim3(256), 0, stream, p, log2_page);
+      else if (tpl == 2) hipLaunchKernelGGL((store_rows_kernel<XT, FP8, IT, 2>), grid, dim3(256), 0, stream, p, log2_page);
+      else if (tpl <= 4) hipLaunchKernelGGL((store_rows_kernel<XT, FP8, IT, 4>), grid, dim3(256), 0, stream, p, log2_page);
+      else hipLaunchKernelGGL((store_rows_kernel<XT, FP8, IT, 8>), grid, dim3(256), 0, stream, p, log2_page);
+      return fa_check_launch("fa_store_kvcache");
+    }
+  }
   int64_t work = 0;
   for (int i = 0; i < p.ndesc; ++i) {
     const int64_t w = p.tokens * p.d[i].heads * p.d[i].chunks;

@@ -49,16 +49,47 @@ FA_DEV float e4m3_to_f32(uint32_t b) {
 
 // fp32 -> E4M3FN byte: NaN -> sign|0x7F, |a| >= 448 saturates to sign|0x7E,
 // otherwise round-to-nearest-even (subnormals in units of 2^-9).
-FA_DEV uint8_t f32_to_e4m3(float v) {
-  uint32_t sign = (__float_as_uint(v) >> 24) & 0x80u;
-  float a = fabsf(v);
-  if (a != a) return (uint8_t)(sign | 0x7fu);
-  if (a >= 448.0f) return (uint8_t)(sign | 0x7eu);
-  if (a < 0.015625f) return (uint8_t)(sign | (uint32_t)__builtin_rintf(a * 512.0f));
-  int e = (int)((__float_as_uint(a) >> 23) & 0xffu) - 127;        // -6 .. 8
-  int mant = (int)__builtin_rintf(__builtin_ldexpf(a, 3 - e));      // 8 .. 16
-  int code = ((e + 7) << 3) + mant - 8;
-  return (uint8_t)(sign | (uint32_t)(code < 126 ? code : 126));
+// Integer form: for |a| >= 2^-6 the fp32 magnitude is rounded to 3 mantissa
+// bits at bit 20 (ties to even) and its exponent rebiased from 127 to 7, so
+// code = (rounded >> 20) - (120 << 3); below 2^-6, fma(|a|, 512, 2^23) rounds
+// |a| * 512 to an integer in the low mantissa bits.  Codes past 126 (|a|
+// rounding to 480 or more, infinities) clamp to 126.  Host-callable so the
+// CPU tests check this very function against the C codec on every fp32 bit
+// pattern.
+__host__ __device__ __forceinline__ uint32_t e4m3_code(float v) {
+  const uint32_t bits = __builtin_bit_cast(uint32_t, v);
+  const uint32_t sign = (bits >> 24) & 0x80u;
+  const uint32_t mag = bits & 0x7fffffffu;
+  const uint32_t normal = (mag + 0x7ffffu + ((mag >> 20) & 1u) - (120u << 23)) >> 20;
+  const uint32_t subnormal =
+      __builtin_bit_cast(uint32_t, __builtin_fmaf(__builtin_bit_cast(float, mag), 512.0f, 8388608.0f)) - 0x4b000000u;
+  uint32_t code = mag < 0x3c800000u ? subnormal : normal;   // 2^-6
+  code = code < 126u ? code : 126u;
+  code = mag > 0x7f800000u ? 0x7fu : code;                  // NaN
+  return sign | code;
+}
+
+FA_DEV uint8_t f32_to_e4m3(float v) { return (uint8_t)e4m3_code(v); }
+
+// x / s as the E4M3 encoder needs it, given r = 1/s rounded to nearest (one
+// IEEE division per scale): q0 = x r, then one residual step (Markstein)
+// q1 = q0 + (x - s q0) r, the residual exact under FMA.  Where |x / s| lies
+// in [2^-14, 2^10] q1 is the correctly rounded quotient; elsewhere it is
+// within an ulp, which E4M3 cannot see (saturation above 448, zero below
+// 2^-11).  q1 is NaN, infinite or zero only where q0 already carries the
+// code: x = +-0 (q0 keeps the sign), x = +-inf or overflow (saturates), NaN.
+// Valid for scales of magnitude in [2^-100, 2^100] (callers divide directly
+// otherwise).  Host-callable: the CPU tests compare it with IEEE division on
+// every bf16 and fp16 input over thousands of scales.
+__host__ __device__ __forceinline__ float div_by_scale(float x, float s, float r) {
+  const float q0 = x * r;
+  const float q1 = __builtin_fmaf(__builtin_fmaf(-q0, s, x), r, q0);
+  return __builtin_isfinite(q1) && q1 != 0.0f ? q1 : q0;
+}
+
+__host__ __device__ __forceinline__ bool scale_in_range(float s) {
+  const float a = __builtin_fabsf(s);
+  return a >= 0x1p-100f && a <= 0x1p100f;
 }
 
 template <typename T> FA_DEV float load_elem(const void* base, int64_t off);
