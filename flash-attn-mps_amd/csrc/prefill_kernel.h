@@ -76,6 +76,17 @@ template <> FA_DEV f32x16 mfma32<F16T>(u32x4 a, u32x4 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
+typedef __attribute__((ext_vector_type(8))) int i32x8;
+
+// S += A B over 64 E4M3 dims with v_mfma_f32_32x32x64_f8f6f4 (no block
+// scales).  Lane (r, h) holds 32 bytes of row r; the instruction contracts
+// over (lane half, byte), so A and B need only split each 64-dim step the
+// same way: here lane half h holds dims 32 h .. 32 h + 31 in byte order.
+// E4M3 x E4M3 products are exact in fp32.
+FA_DEV f32x16 mfma32_fp8(i32x8 a, i32x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
 // Two fp32 values -> one word of two 16-bit values (RNE).
 template <typename T> FA_DEV uint32_t pack2(float lo, float hi);
 template <> FA_DEV uint32_t pack2<BF16T>(float lo, float hi) {
@@ -279,30 +290,41 @@ FA_DEV bool compact_item(const fa_attn_args& a, int slot, int xcd, int lane, int
 // ALIBI: linear biases -slope[b][h] |q_pos - k_pos| seeded into the score
 // accumulators (instantiated without softcap, which would come first)
 // (flash_attn_mps/kernels/attention.metal:47-51, 87).
+// QT: query storage type, T or E4M3.  E4M3 queries (with E4M3 K/V) compute
+// S = K Q^T on v_mfma_f32_32x32x64_f8f6f4 with K kept as raw bytes in LDS;
+// V is staged and widened exactly to T for O += V P (P stays 16-bit).
 template <typename T, int DQ, int DV, int W, int NB, int MINB, bool CAUSAL, bool CAP, bool WIN, int DQT = DQ,
-          int DVT = DV, typename KT = T, bool ALIBI = false>
+          int DVT = DV, typename KT = T, bool ALIBI = false, typename QT = T>
 __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_args a, const PrefillShape shp) {
   constexpr bool FP8 = KT::id == FA_E4M3;
+  constexpr bool FQ = QT::id == FA_E4M3;       // E4M3 queries: FP8 MFMA for S
   static_assert(!(CAP && ALIBI), "the ALiBi bias is added before the softcap would apply");
   constexpr int KEB = KT::bytes;               // bytes per K/V element
   static_assert(!FP8 || (DQT == DQ && DVT == DV && DQ == DV && (DQ == 64 || DQ == 128 || DQ == 256)),
                 "FP8 K/V tiles: 64/128/256-dim heads");
+  static_assert(!FQ || (FP8 && !ALIBI), "E4M3 queries: E4M3 K/V, no ALiBi");
   constexpr int BM = 32 * NB * W;              // query rows per workgroup
   constexpr int KST = DQ / 16;                 // k-steps of the QK^T MFMA
   constexpr int KSTT = (DQT + 15) / 16;        // k-steps holding real dims
   static_assert(DQT % 8 == 0 && DVT % 8 == 0 && DQT <= DQ && DVT <= DV, "true head dims");
   constexpr int DB = DV / 32;                  // 32-dim blocks of O^T
   constexpr int KG = DQ / 64, VG = DV / 64;    // 64-dim column groups (K), pairs of 32-dim blocks (V)
-  constexpr int KTILE = KG * PF_GROUP_BYTES, VTILE = VG * PF_GROUP_BYTES;
+  // A K tile is KGD 128-byte-row column groups: 64 bf16 dims each, or 128
+  // E4M3 dims (E4M3 queries keep K raw; a 64-dim head fills half of its
+  // group's rows, the other half holds whatever follows the row in memory,
+  // or zeros past the request, and is never read).
+  constexpr int KGD = FQ ? (DQ + 127) / 128 : KG;
+  constexpr int KTILE = KGD * PF_GROUP_BYTES, VTILE = VG * PF_GROUP_BYTES;
   static_assert(DQ % 64 == 0 && DV % 64 == 0, "head dims are multiples of 64");
   static_assert(W == 2 || W == 4 || W == 8, "wave count");
 
   extern __shared__ __attribute__((aligned(16))) char smem[];
   char* const kbuf0 = smem;
   char* const vbuf0 = smem + 2 * KTILE;
-  // FP8: one staging tile of raw K and V rows (64 x DQ and 64 x DV bytes).
+  // FP8: one staging tile of raw K and V rows (64 x DQ and 64 x DV bytes);
+  // E4M3 queries: two staging tiles of raw V rows only.
   char* const stk = smem + 2 * KTILE + 2 * VTILE;
-  char* const stv = stk + 64 * DQ;
+  char* const stv = FQ ? stk : stk + 64 * DQ;
 
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int wave_u = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index as a scalar
@@ -366,18 +388,34 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // Q^T operands for the whole kernel: block nb, lane holds
   // Q[wq0 + 32 nb + l32][16 kk + 8 hh .. +8].
   const int wq0 = q0 + (wave_u % wph) * 32 * NB;
-  u32x4 qop[NB][KST];
+  constexpr int KST8 = DQ / 64;                // k-steps of the E4M3 S MFMA
+  u32x4 qop[FQ ? 1 : NB][FQ ? 1 : KST];
+  i32x8 qop8[FQ ? NB : 1][FQ ? KST8 : 1];      // E4M3: Q[row][64 j + 32 hh .. +32]
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     const int row = wq0 + 32 * nb + l32;
     const bool ok = row < r.q_len;
-    const uint16_t* qp = (const uint16_t*)a.q + ((int64_t)r.q_begin + row) * a.q_stride[0] +
-                         (int64_t)h * a.q_stride[1] + 8 * hh;
+    if constexpr (FQ) {
+      const uint8_t* qp = (const uint8_t*)a.q + ((int64_t)r.q_begin + row) * a.q_stride[0] +
+                          (int64_t)h * a.q_stride[1] + 32 * hh;
 #pragma unroll
-    for (int kk = 0; kk < KST; ++kk) {
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (ok && 16 * kk + 8 * hh + 8 <= DQT) v = *(const u32x4*)(qp + 16 * kk);
-      qop[nb][kk] = v;
+      for (int j = 0; j < KST8; ++j) {
+        u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
+        if (ok) {
+          lo = *(const u32x4*)(qp + 64 * j);
+          hi = *(const u32x4*)(qp + 64 * j + 16);
+        }
+        qop8[nb][j] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      }
+    } else {
+      const uint16_t* qp = (const uint16_t*)a.q + ((int64_t)r.q_begin + row) * a.q_stride[0] +
+                           (int64_t)h * a.q_stride[1] + 8 * hh;
+#pragma unroll
+      for (int kk = 0; kk < KST; ++kk) {
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (ok && 16 * kk + 8 * hh + 8 <= DQT) v = *(const u32x4*)(qp + 16 * kk);
+        qop[nb][kk] = v;
+      }
     }
   }
 
@@ -385,7 +423,8 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // some hardware paths; zeroed V buffers keep p * v finite for them.
   // (FP8: the staging tile, whose rows are converted whole.)
   if constexpr (FP8) {
-    for (int i = tid; i < 64 * (DQ + DV) / 16; i += 64 * W) {
+    constexpr int STAGE_BYTES = FQ ? 2 * 64 * DV : 64 * (DQ + DV);
+    for (int i = tid; i < STAGE_BYTES / 16; i += 64 * W) {
       const u32x4 z = {0u, 0u, 0u, 0u};
       *(u32x4*)(stk + 16 * i) = z;
     }
@@ -411,7 +450,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   const bool paged = a.page_size != 0;
   const int lp = shp.log2_page;
   const int drow = 8 * (wave_u & 1) + (lane >> 3);   // row within its 16-key group
-  const int kdoff = 2 * (int)(sigma(drow) * a.k_stride[1]) + (((lane & 7) ^ ((drow >> 1) & 7)) * 16);
+  const int kdoff = KEB * (int)(sigma(drow) * a.k_stride[1]) + (((lane & 7) ^ ((drow >> 1) & 7)) * 16);
   const int vdoff = 2 * (int)((lane >> 2) * a.v_stride[1]) + (lane & 3) * 16;
   const char* const khead = (const char*)a.k + KEB * (int64_t)kh * a.k_stride[2];
   const char* const vhead = (const char*)a.v + KEB * (int64_t)kh * a.v_stride[2];
@@ -466,7 +505,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
       const auto rsrc = decltype(mode)::value == PF_ANY_TILE
                             ? group_rsrc(khead, krow_b, kpage_b, key0, KEB * DQT)
                             : full_rsrc(paged_tag(mode), khead, krow_b, kpage_b, key0, knrec);
-      dma_columns<KG>(rsrc, kbuf0 + buf * KTILE + rb * 1024, kdoff);
+      dma_columns<KGD>(rsrc, kbuf0 + buf * KTILE + rb * 1024, kdoff);
     }
   };
   auto dma_v = [&](auto mode, int tile, int buf) {
@@ -499,6 +538,31 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
       const int n = wave_u + W * i;
       const auto rsrc = group_rsrc(vhead, vrow_b, vpage_b, tile * PF_BN + ((n * VR8) & ~15), DV);
       dma16<0>(rsrc, stv + n * 1024, v8off);
+    }
+  };
+  // E4M3 queries: V tile -> staging slot `slot` (two 64 x DV byte tiles).
+  auto dma_v8 = [&](int tile, int slot) {
+#pragma unroll
+    for (int i = 0; i < 64 / VR8 / W; ++i) {
+      const int n = wave_u + W * i;
+      const auto rsrc = group_rsrc(vhead, vrow_b, vpage_b, tile * PF_BN + ((n * VR8) & ~15), DV);
+      dma16<0>(rsrc, stv + slot * 64 * DV + n * 1024, v8off);
+    }
+  };
+  // ... and staging slot -> V buffer buf, widened exactly to T.
+  auto widen_v = [&](int slot, int buf) {
+    int t = tid;
+    asm volatile("" : "+v"(t));
+    constexpr int CPR = DV / 16, ROWS = 64 * W / CPR;
+    const int r = t / CPR, u = t % CPR;
+    char* const dst = vbuf0 + buf * VTILE + (u >> 1) * PF_VBLOCK_BYTES + r * 64 + 32 * (u & 1);
+    const char* const src = stv + slot * 64 * DV + 16 * t;
+#pragma unroll
+    for (int it = 0; it < 4 * DV / (64 * W); ++it) {
+      u32x4 lo, hi;
+      widen_fp8_16<T>(*(const u32x4*)(src + 1024 * W * it), lo, hi);
+      *(u32x4*)(dst + ROWS * 64 * it) = lo;
+      *(u32x4*)(dst + ROWS * 64 * it + 16) = hi;
     }
   };
   // FP8: staging -> tile buffer buf in the 16-bit layouts above (K: key r
@@ -546,6 +610,11 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   int krd[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) krd[s] = l32 * 128 + (((2 * s + hh) ^ ((l32 >> 1) & 7)) * 16);
+  // E4M3 K (A of S^T, 64 dims per step): step j reads chunks 4 (j % 2) + 2 hh
+  // and + 1 of column group j / 2; index 2 (j % 2) + e.
+  int krd8[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) krd8[s] = l32 * 128 + (((4 * (s >> 1) + 2 * hh + (s & 1)) ^ ((l32 >> 1) & 7)) * 16);
   // V^T (A of O^T) through ds_read_b64_tr_b16: in each 16-lane group g, lane
   // i = a + 4 t' reads row 8 (g / 2) + t' (+ 32 (st % 2) + 16 c + 4 t) of
   // block db at dims 16 (g % 2) + 4 a .. +4; the hardware hands lane 4 a + e
@@ -618,14 +687,25 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
         for (int i = 0; i < 16; ++i) s[nb][i] = 0.0f;
       }
     }
+    if constexpr (FQ) {
 #pragma unroll
-    for (int kk = 0; kk < KSTT; ++kk) {
-      u32x4 av = lds_read16(kl, krd[kk % 4] + (kk / 4) * PF_GROUP_BYTES);
-      if constexpr (DQT % 16 == 8) {
-        if (kk == KSTT - 1 && hh) av = u32x4{0u, 0u, 0u, 0u};   // dims past DQT: whatever the DMA read
+      for (int j = 0; j < KST8; ++j) {
+        const char* g = kl + (j >> 1) * PF_GROUP_BYTES;
+        const u32x4 lo = lds_read16(g, krd8[2 * (j & 1)]), hi = lds_read16(g, krd8[2 * (j & 1) + 1]);
+        const i32x8 av = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) s[nb] = mfma32_fp8(av, qop8[nb][j], s[nb]);
       }
+    } else {
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) s[nb] = mfma32<T>(av, qop[nb][kk], s[nb]);
+      for (int kk = 0; kk < KSTT; ++kk) {
+        u32x4 av = lds_read16(kl, krd[kk % 4] + (kk / 4) * PF_GROUP_BYTES);
+        if constexpr (DQT % 16 == 8) {
+          if (kk == KSTT - 1 && hh) av = u32x4{0u, 0u, 0u, 0u};   // dims past DQT: whatever the DMA read
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) s[nb] = mfma32<T>(av, qop[nb][kk], s[nb]);
+      }
     }
   };
   // Phase A: softcap, mask, row max and the lazy rescale of (m, l); fills
@@ -732,7 +812,15 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
       const int j = st >> 1;
       __builtin_amdgcn_s_waitcnt(0x0F70);
       __syncthreads();
-      if constexpr (FP8) {
+      if constexpr (FQ) {
+        // V(j+1) is in staging slot (j+1) % 2 and buffer (j+1) % 2 is free
+        // (V(j-1) is done); slot j % 2 was widened a tile ago, so it takes
+        // V(j+2).  K as in the 16-bit path.
+        if (j + 1 < n_tiles) widen_v((j + 1) & 1, (j + 1) & 1);
+        if (j + 2 < n_tiles) dma_v8(j + 2, j & 1);
+        if (j + 1 < n_tiles) dma_k(mode, j + 1, (j + 1) & 1, 1);
+        if (j + 2 < n_tiles) dma_k(mode, j + 2, j & 1, 0);
+      } else if constexpr (FP8) {
         if (j + 1 < n_tiles) {
           widen_tile((j + 1) & 1);
           __syncthreads();
@@ -796,7 +884,18 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     // Prologue: tile tile0 and K(tile0 + 1) rows 0..31 in LDS; S(st0) and
     // its phase A.
     const std::integral_constant<int, PF_ANY_TILE> any_tile;
-    if constexpr (FP8) {
+    if constexpr (FQ) {
+      dma_k(any_tile, tile0, tile0 & 1, 0);
+      dma_k(any_tile, tile0, tile0 & 1, 1);
+      dma_v8(tile0, tile0 & 1);
+      if (tile0 + 1 < n_tiles) {
+        dma_k(any_tile, tile0 + 1, (tile0 + 1) & 1, 0);
+        dma_v8(tile0 + 1, (tile0 + 1) & 1);
+      }
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      __syncthreads();
+      widen_v(tile0 & 1, tile0 & 1);   // visible after the barrier that starts the first tile
+    } else if constexpr (FP8) {
       dma_fp8(tile0);
       __builtin_amdgcn_s_waitcnt(0x0F70);
       __syncthreads();
@@ -994,11 +1093,42 @@ PrefillChoice pick_dims_large(int64_t dq, int64_t dv, bool causal, int score, bo
   return PrefillChoice{nullptr, 0, 0, 0};
 }
 
-// Defined in prefill_inst_{bf16,f16}_{small,large}.hip.
+// E4M3 queries over E4M3 K/V (S on the FP8 MFMA), output type T; head dims
+// 64, 128 and 256.  K tiles hold raw bytes (ceil(DQ / 128) column groups), V
+// is staged twice (64 x DV bytes each) and widened into 16-bit tiles.
+template <typename T, int D, bool CAUSAL>
+PrefillChoice pick_tile_fp8q(int score, bool win) {
+  using S = PrefillTile<D, D>;
+  if (score == 2) return PrefillChoice{nullptr, 0, 0, 0};   // ALiBi: not with descaled FP8 inputs
+  const bool cap = score == 1;
+  PrefillChoice c;
+  if (win)
+    c.kern = cap ? prefill_kernel<T, D, D, S::W, S::NB, S::MINB_WIN, CAUSAL, true, true, D, D, E4M3T, false, E4M3T>
+                 : prefill_kernel<T, D, D, S::W, S::NB, S::MINB_WIN, CAUSAL, false, true, D, D, E4M3T, false, E4M3T>;
+  else
+    c.kern = cap ? prefill_kernel<T, D, D, S::W, S::NB, S::MINB, CAUSAL, true, false, D, D, E4M3T, false, E4M3T>
+                 : prefill_kernel<T, D, D, S::W, S::NB, S::MINB, CAUSAL, false, false, D, D, E4M3T, false, E4M3T>;
+  c.bm = 32 * S::NB * S::W;
+  c.threads = 64 * S::W;
+  c.lds = 2 * (size_t)((D + 127) / 128) * PF_GROUP_BYTES + 2 * (size_t)(D / 64) * PF_GROUP_BYTES + 2 * 64 * (size_t)D;
+  return c;
+}
+
+template <typename T>
+PrefillChoice pick_dims_fp8q(int64_t dq, int64_t dv, bool causal, int score, bool win) {
+  if (dq != dv) return PrefillChoice{nullptr, 0, 0, 0};
+  if (dq == 64) return causal ? pick_tile_fp8q<T, 64, true>(score, win) : pick_tile_fp8q<T, 64, false>(score, win);
+  if (dq == 128) return causal ? pick_tile_fp8q<T, 128, true>(score, win) : pick_tile_fp8q<T, 128, false>(score, win);
+  if (dq == 256) return causal ? pick_tile_fp8q<T, 256, true>(score, win) : pick_tile_fp8q<T, 256, false>(score, win);
+  return PrefillChoice{nullptr, 0, 0, 0};
+}
+
+// Defined in prefill_inst_{bf16,f16}_{small,large}.hip and prefill_inst_fp8q.hip.
 PrefillChoice pick_bf16_small(int64_t dq, int64_t dv, bool causal, int score, bool win);
 PrefillChoice pick_f16_small(int64_t dq, int64_t dv, bool causal, int score, bool win);
 PrefillChoice pick_bf16_large(int64_t dq, int64_t dv, bool causal, int score, bool win, bool fp8);
 PrefillChoice pick_f16_large(int64_t dq, int64_t dv, bool causal, int score, bool win, bool fp8);
+PrefillChoice pick_fp8q(int out_dtype, int64_t dq, int64_t dv, bool causal, int score, bool win);
 
 }  // namespace fa_prefill
 

@@ -20,6 +20,7 @@ PrefillChoice select_prefill(const fa_attn_args& a) {
   // A right window bounds nothing under causality.
   const bool win = window_set(a);
   const int64_t dq = a.head_dim_qk, dv = a.head_dim_v;
+  if (a.q_dtype == FA_E4M3) return pick_fp8q(a.out_dtype, dq, dv, causal, score, win);
   const bool bf16 = a.q_dtype == FA_BF16;
   if (!fp8 && dq <= 128)
     return bf16 ? pick_bf16_small(dq, dv, causal, score, win) : pick_f16_small(dq, dv, causal, score, win);
@@ -30,11 +31,17 @@ PrefillChoice select_prefill(const fa_attn_args& a) {
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 bool prefill_ok(const fa_attn_args& a) {
-  if (a.q_dtype != FA_BF16 && a.q_dtype != FA_F16) return false;
-  if (a.out_dtype != a.q_dtype || a.k_dtype != a.v_dtype) return false;
-  const bool fp8 = a.k_dtype == FA_E4M3;
-  if (!fp8 && a.k_dtype != a.q_dtype) return false;
+  const bool fp8 = a.k_dtype == FA_E4M3, fp8q = a.q_dtype == FA_E4M3;
   const int64_t dq = a.head_dim_qk, dv = a.head_dim_v;
+  if (a.k_dtype != a.v_dtype) return false;
+  if (fp8q) {
+    // E4M3 queries: E4M3 K/V, 16-bit output.
+    if (!fp8 || (a.out_dtype != FA_F16 && a.out_dtype != FA_BF16)) return false;
+  } else {
+    if (a.q_dtype != FA_BF16 && a.q_dtype != FA_F16) return false;
+    if (a.out_dtype != a.q_dtype) return false;
+    if (!fp8 && a.k_dtype != a.q_dtype) return false;
+  }
   if (fp8) {
     if (!(dq == dv && (dq == 64 || dq == 128 || dq == 256))) return false;
   } else if (!((dq == dv && (dq == 32 || dq == 64 || dq == 72 || dq == 80 || dq == 96 || dq == 128 || dq == 256)) ||
@@ -53,8 +60,9 @@ bool prefill_ok(const fa_attn_args& a) {
   if (a.num_splits != 1) return false;
   if (a.q_stride[2] != 1 || a.k_stride[3] != 1 || a.v_stride[3] != 1 || a.out_stride[2] != 1) return false;
   if (!aligned16(a.q) || !aligned16(a.k) || !aligned16(a.v) || ((uintptr_t)a.out & 7u)) return false;
+  const int qb = fp8q ? 1 : 2;   // query bytes per element
   for (int i = 0; i < 2; ++i)
-    if ((a.q_stride[i] * 2) % 16 || (a.out_stride[i] * 2) % 8) return false;
+    if ((a.q_stride[i] * qb) % 16 || (a.out_stride[i] * 2) % 8) return false;
   for (int i = a.page_size ? 0 : 1; i < 3; ++i)
     if ((a.k_stride[i] * kb) % 16 || (a.v_stride[i] * kb) % 16) return false;
   // Group-bounded buffer loads need non-overlapping rows and 16-row groups

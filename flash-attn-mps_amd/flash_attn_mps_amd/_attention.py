@@ -104,11 +104,18 @@ def build_args(p, out, lse, max_q=None):
 
 
 def _fits_prefill(p, out):
-    """Features the MFMA route takes at all (the kernel is asked about the rest)."""
-    return (not p.deterministic and p.splits in (0, 1)
-            and p.q.dtype in (torch.float16, torch.bfloat16) and out.dtype == p.q.dtype
-            and p.k.dtype == p.v.dtype and p.k.dtype in (p.q.dtype, torch.float8_e4m3fn)
-            and p.mask is None and p.leftpad is None)
+    """Features the MFMA route takes at all (the kernel is asked about the rest):
+    16-bit queries over same-type or E4M3 K/V with output in the query's type,
+    or E4M3 queries over E4M3 K/V with fp16/bf16 output (S on the FP8 MFMA)."""
+    if p.deterministic or p.splits not in (0, 1) or p.mask is not None or p.leftpad is not None:
+        return False
+    fp8 = torch.float8_e4m3fn
+    if p.k.dtype != p.v.dtype:
+        return False
+    if p.q.dtype == fp8:
+        return p.k.dtype == fp8 and out.dtype in (torch.float16, torch.bfloat16)
+    return (p.q.dtype in (torch.float16, torch.bfloat16) and out.dtype == p.q.dtype
+            and p.k.dtype in (p.q.dtype, fp8))
 
 
 def _partials(p, a, shape_out, shape_lse):
