@@ -42,7 +42,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=200)
     p.add_argument("--no-secondary", action="store_true", help="only the headline prefill config")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", default="", help="comma list of secondary configs to run (3,4,5,store4,prefill_fp8); config 2 always runs")
+    p.add_argument("--only", default="", help="comma list of secondary configs to run (3,4,5,5_fixed_order,store4,prefill_fp8); config 2 always runs")
     p.add_argument("--copy-probe", action="store_true",
                    help="first run a known-size copy kernel (reads and writes 1 GiB) that calibrates "
                         "rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -340,7 +340,9 @@ def config5_inputs(device):
                 dim_qk=dqk, dim_v=dv, page=page)
 
 
-def config5(device, steps, warmup):
+def config5(device, steps, warmup, splits=0):
+    """Config 5; splits=1 is vLLM's fixed-order (batch-invariant) call, which
+    keeps every request, single-query ones included, in the MFMA prefill."""
     import torch
     from flash_attn_mps_amd import vllm
     c = config5_inputs(device)
@@ -350,7 +352,7 @@ def config5(device, steps, warmup):
     def step():
         vllm.flash_attn_varlen_func(c["q"], c["k_cache"], c["v_cache"], max(q_lens), c["cu_q"], max(k_lens),
                                     seqused_k=c["used"], block_table=c["table"], causal=True, s_aux=c["sinks"],
-                                    out=out)
+                                    out=out, num_splits=splits)
 
     ms, call_ms, _ = time_calls(step, steps, warmup)
     dec_bytes = sum(c["dec_ctx"]) * hkv * (dqk + dv) * 2
@@ -441,7 +443,8 @@ def main():
     # run up to 15% slower while its clock ramps).
     secondary = {}
     if not args.no_secondary:
-        for name, fn in (("3", config3), ("4", config4), ("5", config5), ("store4", store_fp8),
+        for name, fn in (("3", config3), ("4", config4), ("5", config5),
+                         ("5_fixed_order", lambda *x: config5(*x, splits=1)), ("store4", store_fp8),
                          ("prefill_fp8", prefill_fp8)):
             if only and name not in only and not (name == "store4" and "4" in only):
                 continue
@@ -454,13 +457,15 @@ def main():
             elif name == "store4":
                 entry.update(GBps=round(r["gbs"], 1), frac_of_hbm=round(r["gbs"] / PEAK_HBM_GBS, 4),
                              bytes=r["bytes"], what=r["what"])
-            elif name == "5":
+            elif name.startswith("5"):
                 entry.update(kv_GBps=round(r["gbs"], 1), roofline_ms=round(r["roofline_ms"], 4),
                              frac=round(r["frac"], 4), chunk_flops=r["flops"])
             else:
                 entry.update(kv_GBps=round(r["gbs"], 1), frac_of_hbm=round(r["gbs"] / PEAK_HBM_GBS, 4),
                              kv_bytes=r["kv_bytes"], call_median_kv_GBps=round(r["call_gbs"], 1),
                              kernel_event_ms=round(r["kernel_ms"], 4))
+            if name == "5_fixed_order":
+                entry["what"] = "config 5 with num_splits=1: every request in the MFMA prefill, batch-invariant"
             secondary["config" + name if name[0].isdigit() else name] = entry
             torch.cuda.empty_cache()
     c2 = config2(device, args.steps, args.warmup)

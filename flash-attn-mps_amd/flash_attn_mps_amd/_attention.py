@@ -7,15 +7,24 @@ a HIP graph:
 
 1. one query per request, not deterministic, no vLLM mask -> split-KV decode
    (`_decode.decode`; the reference's decode route, _attention.py:134-147);
-2. 16-bit queries whose feature set the MFMA prefill kernel compiles
+2. inputs whose feature set the MFMA prefill kernel compiles
    (fa_prefill_supported) -> fa_prefill_fwd (the reference's `fast` route,
-   _attention.py:149-158, which this kernel widens to windows, sinks, FP8 K/V,
-   ALiBi and per-request causality); in a batch of several requests the
-   single-query ones go to the decode kernel first and fa_prefill_fwd skips
-   them (FA_FLAG_SKIP_SINGLE_QUERY);
+   _attention.py:149-158, which this kernel widens to windows, sinks, FP8
+   K/V, E4M3 queries, ALiBi and per-request causality); in a batch of
+   several requests the single-query ones go to the decode kernel first and
+   fa_prefill_fwd skips them (FA_FLAG_SKIP_SINGLE_QUERY);
 3. everything else -> fa_attn_fwd, the generic kernel, with the reference's
    split rule: deterministic -> 1, else num_splits, else min(32, ceil(max_k /
    256)) when the row is decode-like or d > 256 (_attention.py:159-161).
+
+Deterministic calls (vLLM's num_splits=1, the reference's fixed
+batch-invariant path, docs/contracts.md:76-79) take route 2 for every
+request, single-query ones included, or route 3 with one split.  Either
+kernel computes a row from its own request alone, in a fixed order: query
+blocks and key tiles are aligned to the request's first query and key, the
+kernel variant depends only on dtypes, head dims and feature flags, and a
+key tile that a row cannot see adds exact zeros to its sums.  So a request's
+rows are bit-identical whatever else is in the batch.
 """
 import torch
 
@@ -106,8 +115,9 @@ def build_args(p, out, lse, max_q=None):
 def _fits_prefill(p, out):
     """Features the MFMA route takes at all (the kernel is asked about the rest):
     16-bit queries over same-type or E4M3 K/V with output in the query's type,
-    or E4M3 queries over E4M3 K/V with fp16/bf16 output (S on the FP8 MFMA)."""
-    if p.deterministic or p.splits not in (0, 1) or p.mask is not None or p.leftpad is not None:
+    or E4M3 queries over E4M3 K/V with fp16/bf16 output (S on the FP8 MFMA).
+    The kernel never splits a row, so deterministic calls qualify."""
+    if p.splits not in (0, 1) or p.mask is not None or p.leftpad is not None:
         return False
     fp8 = torch.float8_e4m3fn
     if p.k.dtype != p.v.dtype:
@@ -164,9 +174,11 @@ def solve(p):
         # take the decode kernel: a 128-row MFMA query tile per head would be
         # almost empty for them.  Packed self-attention (queries and keys on
         # the same offsets) gives a single-query request a single key, so the
-        # MFMA kernel keeps it and no decode pass runs.
+        # MFMA kernel keeps it and no decode pass runs.  Deterministic calls
+        # keep every request in this kernel (the decode kernel's split count
+        # follows the batch).
         self_attention = p.cu_k is p.cu_q and p.used_k is None and not p.paged
-        if p.batch > 1 and not self_attention and _single_query_rows(p, a):
+        if p.batch > 1 and not self_attention and not p.deterministic and _single_query_rows(p, a):
             a.flags |= _lib.FLAG_SKIP_SINGLE_QUERY
         _lib.call("fa_prefill_fwd", a, p.device)
         return out, lse
