@@ -107,6 +107,20 @@ __global__ __launch_bounds__(256) void store_kernel(const StoreParams p) {
 // 32-bit division.  FP8: x / scale[h] (correctly rounded, by div_by_scale
 // with the scale's reciprocal) then the integer E4M3 encoder, VEC codes
 // stored as one 8- or 4-byte word.
+// Streaming (non-temporal) accesses: the token rows are read once and the
+// cache rows written once, so neither is kept in the caches (1.5% faster
+// than ordinary loads and stores on a 590K-token FP8 store).
+typedef uint32_t nt_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t nt_u32x2 __attribute__((ext_vector_type(2)));
+
+FA_DEV uint4 load16_nt(const void* p) {
+  const nt_u32x4 v = __builtin_nontemporal_load((const nt_u32x4*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+FA_DEV void store16_nt(void* p, uint4 v) { __builtin_nontemporal_store(nt_u32x4{v.x, v.y, v.z, v.w}, (nt_u32x4*)p); }
+FA_DEV void store8_nt(void* p, uint2 v) { __builtin_nontemporal_store(nt_u32x2{v.x, v.y}, (nt_u32x2*)p); }
+FA_DEV void store4_nt(void* p, uint32_t v) { __builtin_nontemporal_store(v, (uint32_t*)p); }
+
 template <typename XT, bool FP8, typename IT, int TPL>
 __global__ __launch_bounds__(256) void store_rows_kernel(const StoreParams p, const int log2_page) {
   constexpr int VEC = 16 / XT::bytes;
@@ -156,9 +170,9 @@ __global__ __launch_bounds__(256) void store_rows_kernel(const StoreParams p, co
 #pragma unroll
       for (int i = 0; i < TPL; ++i) {
         if (!on[i]) continue;
-        const uint4 raw = *(const uint4*)(xrow + src[i]);
+        const uint4 raw = load16_nt(xrow + src[i]);
         if constexpr (!FP8) {
-          *(uint4*)((S*)d.cache + crow + dst[i]) = raw;
+          store16_nt((S*)d.cache + crow + dst[i], raw);
         } else {
           const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
           uint32_t packed[VEC / 4];
@@ -177,8 +191,8 @@ __global__ __launch_bounds__(256) void store_rows_kernel(const StoreParams p, co
             packed[j / 4] = (j & 3) == 0 ? code : packed[j / 4] | (code << (8 * (j & 3)));
           }
           uint8_t* out = (uint8_t*)d.cache + crow + dst[i];
-          if constexpr (VEC == 8) *(uint2*)out = make_uint2(packed[0], packed[1]);
-          else *(uint32_t*)out = packed[0];
+          if constexpr (VEC == 8) store8_nt(out, make_uint2(packed[0], packed[1]));
+          else store4_nt(out, packed[0]);
         }
       }
     }
@@ -203,7 +217,10 @@ int launch_store(const StoreParams& p, bool vec, hipStream_t stream) {
       if ((p.page_size & (p.page_size - 1)) == 0)
         for (log2_page = 0; (1ll << log2_page) < p.page_size; ++log2_page) {}
       int64_t blocks = fa_ceil_div(p.tokens, 4);
-      if (blocks > 2048) blocks = 2048;   // 8 workgroups per CU; each wave then loops over tokens
+      // 64 workgroups per CU at most; each wave then loops over tokens.  (On
+      // a 590K-token FP8 store 16K workgroups per descriptor ran 7% faster
+      // than 2K, and 64K or one per four tokens were slower again.)
+      if (blocks > 16384) blocks = 16384;
       const dim3 grid((unsigned)blocks, (unsigned)p.ndesc);
       const int tpl = (int)fa_ceil_div(tasks, 64);
       if (tpl == 1) hipLaunchKernelGGL((store_rows_kernel<XT, FP8, IT, 1>), grid, dim3(256), 0, stream, p, log2_page);

@@ -4,9 +4,13 @@
 // merge_partials merge.metal:30-58: weights w_s = exp(lse_s - max) (an LSE of
 // +inf takes all the weight, equally shared among +inf states), states with
 // zero weight are never read (so NaN payloads of empty states vanish), an
-// all -inf row gives output 0 and LSE -inf.  One lane owns a whole
-// (token, head) row, which makes in-place merging (out aliasing an input)
-// safe: every element is read before it is written by the same lane.
+// all -inf row gives output 0 and LSE -inf.  One wave owns a (token, head)
+// row: its lanes take the head dimension 64 elements at a time (consecutive
+// elements in consecutive lanes, so each load and store instruction is one
+// contiguous segment of the row), and every lane computes the row's weights.
+// In-place merging (out or out_lse aliasing an input) is safe: each element
+// is read and written by the same lane, and the LSE inputs are read by the
+// whole wave before lane 0 writes the merged LSE.
 #include "fa_device.h"
 
 namespace {
@@ -30,7 +34,8 @@ struct MergePairParams {
 
 template <typename T>
 __global__ __launch_bounds__(256) void merge_pair_kernel(const MergePairParams p) {
-  const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   if (row >= p.tokens * p.heads) return;
   const int64_t t = row / p.heads, h = row - t * p.heads;
   const float la = p.al[h * p.als[0] + t * p.als[1]];
@@ -39,14 +44,14 @@ __global__ __launch_bounds__(256) void merge_pair_kernel(const MergePairParams p
   const bool empty = peak == -INFINITY;
   const float wa = merge_weight(la, peak), wb = merge_weight(lb, peak);
   const float total = wa + wb;
-  for (int64_t d = 0; d < p.dim; ++d) {
+  for (int64_t d = lane; d < p.dim; d += 64) {
     float v = 0.0f;
     if (wa > 0.0f) v += wa * load_elem<T>(p.a, t * p.as[0] + h * p.as[1] + d * p.as[2]);
     if (wb > 0.0f) v += wb * load_elem<T>(p.b, t * p.bs[0] + h * p.bs[1] + d * p.bs[2]);
     if (!empty) v /= total;
     store_elem<T>(p.out, t * p.os[0] + h * p.os[1] + d * p.os[2], v);
   }
-  if (p.ol) p.ol[h * p.ols[0] + t * p.ols[1]] = empty ? -INFINITY : peak + logf(total);
+  if (p.ol && lane == 0) p.ol[h * p.ols[0] + t * p.ols[1]] = empty ? -INFINITY : peak + logf(total);
 }
 
 struct MergePartialsParams {
@@ -60,7 +65,8 @@ struct MergePartialsParams {
 };
 
 __global__ __launch_bounds__(256) void merge_partials_kernel(const MergePartialsParams p) {
-  const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   if (row >= p.tokens * p.heads) return;
   const int64_t t = row / p.heads, h = row - t * p.heads;
   float peak = -INFINITY;
@@ -68,7 +74,7 @@ __global__ __launch_bounds__(256) void merge_partials_kernel(const MergePartials
   const bool empty = peak == -INFINITY;
   float denom = 0.0f;
   for (int64_t s = 0; s < p.splits; ++s) denom += merge_weight(p.plse[s * p.pls[0] + h * p.pls[1] + t * p.pls[2]], peak);
-  for (int64_t d = 0; d < p.dim; ++d) {
+  for (int64_t d = lane; d < p.dim; d += 64) {
     float v = 0.0f;
     if (!empty) {
       for (int64_t s = 0; s < p.splits; ++s) {
@@ -79,7 +85,7 @@ __global__ __launch_bounds__(256) void merge_partials_kernel(const MergePartials
     }
     store_any(p.out, t * p.os[0] + h * p.os[1] + d * p.os[2], p.out_dtype, v);
   }
-  p.lse[h * p.ls[0] + t * p.ls[1]] = empty ? -INFINITY : peak + logf(denom);
+  if (lane == 0) p.lse[h * p.ls[0] + t * p.ls[1]] = empty ? -INFINITY : peak + logf(denom);
 }
 
 }  // namespace
@@ -95,7 +101,8 @@ extern "C" int fa_merge_pair(const fa_merge_pair_args* a, void* stream) {
   for (int i = 0; i < 2; ++i) { p.als[i] = a->a_lse_stride[i]; p.bls[i] = a->b_lse_stride[i]; p.ols[i] = a->out_lse_stride[i]; }
   const int64_t rows = p.tokens * p.heads;
   if (rows == 0) return FA_OK;
-  const dim3 grid((unsigned)fa_ceil_div(rows, 256));
+  FA_REQUIRE(fa_ceil_div(rows, 4) <= 0x7fffffffll, "fa_merge_pair: too many rows");
+  const dim3 grid((unsigned)fa_ceil_div(rows, 4));   // a wave per row
   hipStream_t s = (hipStream_t)stream;
   switch (a->dtype) {
     case FA_F16: hipLaunchKernelGGL(merge_pair_kernel<F16T>, grid, dim3(256), 0, s, p); break;
@@ -121,7 +128,8 @@ extern "C" int fa_merge_partials(const fa_merge_partials_args* a, void* stream) 
   p.part_dtype = a->partial_dtype; p.out_dtype = a->out_dtype;
   const int64_t rows = p.tokens * p.heads;
   if (rows == 0) return FA_OK;
-  hipLaunchKernelGGL(merge_partials_kernel, dim3((unsigned)fa_ceil_div(rows, 256)), dim3(256), 0,
+  FA_REQUIRE(fa_ceil_div(rows, 4) <= 0x7fffffffll, "fa_merge_partials: too many rows");
+  hipLaunchKernelGGL(merge_partials_kernel, dim3((unsigned)fa_ceil_div(rows, 4)), dim3(256), 0,   // a wave per row
                      (hipStream_t)stream, p);
   return fa_check_launch("fa_merge_partials");
 }

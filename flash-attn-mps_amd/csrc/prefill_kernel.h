@@ -748,6 +748,9 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     }
   };
   // Phase B: probabilities (<= 2^8), row sums, packed B operand of O^T.
+  // The row sums add the fp32 probabilities: summing the 16-bit values that
+  // P.V consumes (v_dot2 with (1, 1), half the instructions) puts the LSE
+  // ~1.5e-3 off for bf16, past its 1e-4 bar.
   auto phase_b = [&](f32x16 (&s)[NB], u32x4 (&pop)[NB][2]) {
     const float sc = CAP ? 1.0f : c_scale;
 #pragma unroll

@@ -136,20 +136,46 @@ def _partials(p, a, shape_out, shape_lse):
     a.partial_out, a.partial_lse = po.data_ptr(), pl.data_ptr()
 
 
-def _single_query_rows(p, a):
-    """Decode the single-query requests of a mixed batch (the decode kernel
-    skips every other request); True if it ran."""
-    if not _lib.supported("fa_decode_supported", a):
+_SIDE_STREAMS = {}
+
+
+def _side_stream(device):
+    """A second stream per device (default priority) for the decode rows of a
+    mixed batch."""
+    index = torch.device(device).index
+    stream = _SIDE_STREAMS.get(index)
+    if stream is None:
+        stream = _SIDE_STREAMS[index] = torch.cuda.Stream(device)
+    return stream
+
+
+def _mixed_batch(p, a):
+    """A batch of several requests with single-query ones among them: the
+    decode kernel takes the single-query requests (it skips the others) and
+    fa_prefill_fwd the rest (FA_FLAG_SKIP_SINGLE_QUERY).  The two kernels
+    write disjoint rows, so they run concurrently: the prefill is enqueued
+    first on the caller's stream and the decode on a side stream that starts
+    after the caller's earlier work; the caller's stream then waits for it.
+    The memory-bound decode fills the CUs the compute-bound prefill leaves.
+    Returns False (nothing launched) when the decode kernel cannot take the
+    single-query rows."""
+    dec = _lib.AttnArgs.from_buffer_copy(a)
+    if not _lib.supported("fa_decode_supported", dec):
         return False
     from ._decode import split_plan, workgroups_per_token
     splits, span = split_plan(p.batch, workgroups_per_token(p.heads, p.kv_heads, p.dim_qk, p.dim_v),
                               p.max_k, 0)
-    a.num_splits, a.split_span = splits, span
+    dec.num_splits, dec.split_span = splits, span
     if splits > 1:
-        _partials(p, a, (p.batch, p.heads, splits, p.dim_v), (p.batch, p.heads, splits))
-    _lib.call("fa_decode_fwd", a, p.device)
-    a.num_splits, a.split_span = 1, 0
-    a.partial_out = a.partial_lse = None
+        _partials(p, dec, (p.batch, p.heads, splits, p.dim_v), (p.batch, p.heads, splits))
+    main = torch.cuda.current_stream(p.device)
+    side = _side_stream(p.device)
+    side.wait_stream(main)
+    a.flags |= _lib.FLAG_SKIP_SINGLE_QUERY
+    _lib.call("fa_prefill_fwd", a, p.device)
+    with torch.cuda.stream(side):
+        _lib.call("fa_decode_fwd", dec, p.device)
+    main.wait_stream(side)
     return True
 
 
@@ -178,9 +204,8 @@ def solve(p):
         # keep every request in this kernel (the decode kernel's split count
         # follows the batch).
         self_attention = p.cu_k is p.cu_q and p.used_k is None and not p.paged
-        if p.batch > 1 and not self_attention and not p.deterministic and _single_query_rows(p, a):
-            a.flags |= _lib.FLAG_SKIP_SINGLE_QUERY
-        _lib.call("fa_prefill_fwd", a, p.device)
+        if not (p.batch > 1 and not self_attention and not p.deterministic and _mixed_batch(p, a)):
+            _lib.call("fa_prefill_fwd", a, p.device)
         return out, lse
     per_row = p.deterministic or p.max_q == 1 or max(p.dim_qk, p.dim_v) > 256
     if p.deterministic:
