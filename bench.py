@@ -57,22 +57,29 @@ def cu_lengths(lengths, device):
 
 
 def causal_pairs(q_lens, k_lens):
+    """Visible (query, key) pairs under lower-right causality: row i of a
+    request sees max(0, lk - lq + 1 + i) keys, consecutive integers from
+    lk - lq + 1 up to lk, so a request's sum is that of the positive ones."""
     total = 0
     for lq, lk in zip(q_lens, k_lens):
-        # rows i = 0..lq-1 see min(lk, lk - lq + i + 1) keys (lower-right)
-        first = lk - lq + 1
-        total += sum(max(0, min(lk, first + i)) for i in range(lq))
+        if lq <= 0 or lk <= 0:
+            continue
+        lo = max(lk - lq + 1, 1)
+        total += (lo + lk) * (lk - lo + 1) // 2
     return total
 
 
-def time_calls(fn, steps, warmup, kernel=None):
+def time_calls(fn, steps, warmup, kernel=None, defer=False):
     """Warmup, then `steps` back-to-back calls bracketed by synchronize with
     no other work in between (ms per step = the region over `steps`).  A
     second pass of `steps` calls then records a HIP event pair around every
     call, and around every launch of the C-ABI entry point `kernel` when one
     is named, on the launching stream (event records cost a few microseconds
     each, so they stay out of the first region).  Returns (ms per step, median
-    ms per call, mean ms per `kernel` launch or None)."""
+    ms per call, mean ms per `kernel` launch or None); with `defer`, a
+    function that returns them, leaving the final synchronize (which the
+    event readings need) to that function, so the caller can enqueue its next
+    work before the GPU drains."""
     import torch
     for _ in range(warmup):
         fn()
@@ -92,10 +99,14 @@ def time_calls(fn, steps, warmup, kernel=None):
             starts[i].record()
             fn()
             ends[i].record()
+
+    def finish():
         torch.cuda.synchronize()
-    per_call = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
-    kernel_ms = sum(s.elapsed_time(e) for s, e in pairs) / len(pairs) if pairs else None
-    return total / steps, per_call[len(per_call) // 2], kernel_ms
+        per_call = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
+        kernel_ms = sum(s.elapsed_time(e) for s, e in pairs) / len(pairs) if pairs else None
+        return total / steps, per_call[len(per_call) // 2], kernel_ms
+
+    return finish if defer else finish()
 
 
 class launch_events:
@@ -167,16 +178,17 @@ def config2_inputs(device):
     q = (torch.randn(total, hq, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
     k = (torch.randn(total, hkv, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
     v = (torch.randn(total, hkv, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
-    return dict(lengths=lengths, q=q, k=k, v=v, cu=cu_lengths(lengths, device), heads=hq, kv_heads=hkv, dim=d)
+    return dict(lengths=lengths, q=q, k=k, v=v, cu=cu_lengths(lengths, device), heads=hq, kv_heads=hkv, dim=d,
+                out=torch.empty_like(q))
 
 
-def config2(device, steps, warmup):
+def config2(device, steps, warmup, c=None):
     import torch
     import flash_attn_mps_amd as fa
-    c = config2_inputs(device)
+    c = c or config2_inputs(device)
     q, k, v, cu, lengths = c["q"], c["k"], c["v"], c["cu"], c["lengths"]
     maxlen = max(lengths)
-    out = torch.empty_like(q)
+    out = c["out"]
 
     def step():
         fa.flash_attn_varlen_func(q, k, v, cu, cu, maxlen, maxlen, causal=True, out=out)
@@ -188,7 +200,7 @@ def config2(device, steps, warmup):
                 kernel_tflops=flops / (kernel_ms * 1e-3) / 1e12, tensors=(q, k, v, cu))
 
 
-def prefill_fp8(device, steps, warmup):
+def prefill_fp8(device, steps, warmup, c=None, defer=False):
     """Config 2 with E4M3 queries, keys and values (per-(request, KV head)
     descales) and bf16 output: S = Q K^T on the FP8 MFMA, P.V on the bf16
     MFMA.  Same algorithmic FLOPs as config 2; half of them (Q K^T) run at
@@ -196,7 +208,7 @@ def prefill_fp8(device, steps, warmup):
     2 / (1/5.0 + 1/2.5) = 3.33 PF."""
     import torch
     from flash_attn_mps_amd import vllm
-    c = config2_inputs(device)
+    c = c or config2_inputs(device)
     lengths, cu, hkv = c["lengths"], c["cu"], c["kv_heads"]
     g = torch.Generator().manual_seed(123 + 20)
     desc = {n: torch.empty(len(lengths), hkv).uniform_(0.005, 0.01, generator=g).to(device) for n in "qkv"}
@@ -206,7 +218,6 @@ def prefill_fp8(device, steps, warmup):
     q = q.to(torch.float8_e4m3fn)
     k = (c["k"].float() / per_tok[1][..., None]).clamp(-448, 448).to(torch.float8_e4m3fn)
     v = (c["v"].float() / per_tok[2][..., None]).clamp(-448, 448).to(torch.float8_e4m3fn)
-    del c
     maxlen = max(lengths)
     out = torch.empty(q.shape, dtype=torch.bfloat16, device=device)
 
@@ -214,10 +225,15 @@ def prefill_fp8(device, steps, warmup):
         vllm.flash_attn_varlen_func(q, k, v, maxlen, cu, maxlen, cu_seqlens_k=cu, causal=True, out=out,
                                     q_descale=desc["q"], k_descale=desc["k"], v_descale=desc["v"])
 
-    ms, call_ms, kernel_ms = time_calls(step, steps, warmup, kernel="fa_prefill_fwd")
     flops = causal_pairs(lengths, lengths) * 16 * 2 * (128 + 128)
-    return dict(ms=ms, call_ms=call_ms, kernel_ms=kernel_ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12,
-                what="config 2 lengths, E4M3 Q/K/V with descales, bf16 out; Q.K^T on the FP8 MFMA")
+    timing = time_calls(step, steps, warmup, kernel="fa_prefill_fwd", defer=True)
+
+    def finish():
+        ms, call_ms, kernel_ms = timing()
+        return dict(ms=ms, call_ms=call_ms, kernel_ms=kernel_ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12,
+                    what="config 2 lengths, E4M3 Q/K/V with descales, bf16 out; Q.K^T on the FP8 MFMA")
+
+    return finish if defer else finish()
 
 
 def paged_cache(ctx, page, hkv, d, dtype, device, gen_seed, scale=None, dv=None):
@@ -425,6 +441,28 @@ def cpu_model():
     return platform.processor() or "unknown"
 
 
+def secondary_entry(name, r):
+    """The JSON object of one secondary line."""
+    entry = {"ms_per_step": round(r["ms"], 4)}
+    if name == "prefill_fp8":
+        entry.update(TFLOPs=round(r["tflops"], 2), frac_of_fp8_peak=round(r["tflops"] / PEAK_FP8_TFLOPS, 4),
+                     frac_of_mixed_peak=round(r["tflops"] / PEAK_FP8_BF16_MIXED_TFLOPS, 4),
+                     kernel_event_ms=round(r["kernel_ms"], 4), flops=r["flops"], what=r["what"])
+    elif name == "store4":
+        entry.update(GBps=round(r["gbs"], 1), frac_of_hbm=round(r["gbs"] / PEAK_HBM_GBS, 4),
+                     bytes=r["bytes"], what=r["what"])
+    elif name.startswith("5"):
+        entry.update(kv_GBps=round(r["gbs"], 1), roofline_ms=round(r["roofline_ms"], 4),
+                     frac=round(r["frac"], 4), chunk_flops=r["flops"])
+        if name == "5_fixed_order":
+            entry["what"] = "config 5 with num_splits=1: every request in the MFMA prefill, batch-invariant"
+    else:
+        entry.update(kv_GBps=round(r["gbs"], 1), frac_of_hbm=round(r["gbs"] / PEAK_HBM_GBS, 4),
+                     kv_bytes=r["kv_bytes"], call_median_kv_GBps=round(r["call_gbs"], 1),
+                     kernel_event_ms=round(r["kernel_ms"], 4))
+    return entry
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -440,35 +478,34 @@ def main():
     # The secondary configurations run first: their cache writes and timed
     # calls keep the GPU busy for seconds, so the headline configuration is
     # timed at the clock a loaded GPU holds (a cold GPU's first ~100 launches
-    # run up to 15% slower while its clock ramps).
+    # run up to 15% slower while its clock ramps).  Config 2's inputs are
+    # built before them (on the CPU, from its seeded generator, which takes
+    # about a second), so no input building leaves the GPU idle between the
+    # last secondary line and config 2's warmup.
+    # The last secondary line (config 2 in E4M3, the same MFMA-bound work) is
+    # read only after config 2's warmup is enqueued: a host synchronize
+    # between the two would leave the GPU idle for a few milliseconds, after
+    # which the first ~40 prefill launches run up to 15% slower while the
+    # clock settles again (kernel traces: 505-545 us per launch without the
+    # gap, 502-614 us after a 3-6 ms gap).
+    c2_inputs = config2_inputs(device)
     secondary = {}
+    pending = None
     if not args.no_secondary:
-        for name, fn in (("3", config3), ("4", config4), ("5", config5),
-                         ("5_fixed_order", lambda *x: config5(*x, splits=1)), ("store4", store_fp8),
-                         ("prefill_fp8", prefill_fp8)):
+        for name, fn in (("3", config3), ("4", config4), ("store4", store_fp8), ("5", config5),
+                         ("5_fixed_order", lambda *x: config5(*x, splits=1)),
+                         ("prefill_fp8", lambda *x: prefill_fp8(*x, c=c2_inputs, defer=True))):
             if only and name not in only and not (name == "store4" and "4" in only):
                 continue
             r = fn(device, args.steps, args.warmup)
-            entry = {"ms_per_step": round(r["ms"], 4)}
             if name == "prefill_fp8":
-                entry.update(TFLOPs=round(r["tflops"], 2), frac_of_fp8_peak=round(r["tflops"] / PEAK_FP8_TFLOPS, 4),
-                             frac_of_mixed_peak=round(r["tflops"] / PEAK_FP8_BF16_MIXED_TFLOPS, 4),
-                             kernel_event_ms=round(r["kernel_ms"], 4), flops=r["flops"], what=r["what"])
-            elif name == "store4":
-                entry.update(GBps=round(r["gbs"], 1), frac_of_hbm=round(r["gbs"] / PEAK_HBM_GBS, 4),
-                             bytes=r["bytes"], what=r["what"])
-            elif name.startswith("5"):
-                entry.update(kv_GBps=round(r["gbs"], 1), roofline_ms=round(r["roofline_ms"], 4),
-                             frac=round(r["frac"], 4), chunk_flops=r["flops"])
-            else:
-                entry.update(kv_GBps=round(r["gbs"], 1), frac_of_hbm=round(r["gbs"] / PEAK_HBM_GBS, 4),
-                             kv_bytes=r["kv_bytes"], call_median_kv_GBps=round(r["call_gbs"], 1),
-                             kernel_event_ms=round(r["kernel_ms"], 4))
-            if name == "5_fixed_order":
-                entry["what"] = "config 5 with num_splits=1: every request in the MFMA prefill, batch-invariant"
-            secondary["config" + name if name[0].isdigit() else name] = entry
+                pending = r
+                continue
+            secondary["config" + name if name[0].isdigit() else name] = secondary_entry(name, r)
             torch.cuda.empty_cache()
-    c2 = config2(device, args.steps, args.warmup)
+    c2 = config2(device, args.steps, args.warmup, c=c2_inputs)
+    if pending is not None:
+        secondary["prefill_fp8"] = secondary_entry("prefill_fp8", pending())
     line = {
         "metric": "bf16 prefill TFLOP/s & paged-decode KV GB/s, % of MI355X roofline, 1 GPU",
         "value": round(c2["tflops"], 2),
