@@ -139,14 +139,33 @@ FA_DEV float sum_hh(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// 16 bytes a lane from a buffer straight into LDS at lds + 16 * lane.  The
-// host compilation pass rejects this builtin (and would drop the kernel
-// stub without a diagnostic), so only the device pass sees the call.
-// IMM is added to both the global and the LDS address.
+// 16 bytes a lane from a buffer straight into LDS at lds + 16 * lane
+// (buffer_load_dwordx4 ... lds: LDS address = m0 + IMM + 16 * lane, global
+// address = base + voffset + IMM).  Written as inline assembly so that the
+// compiler does not track it: it treats an LDS-DMA load as a possible writer
+// of whatever a later ds_read_b64_tr_b16 reads and puts an
+// `s_waitcnt vmcnt(0)` before the first transposed V read after it, which
+// stalled every wave in each tile until the DMAs it had just issued for the
+// NEXT tiles had landed.  The kernel orders DMA writes and LDS reads itself
+// (s_waitcnt vmcnt(0) + barrier at each tile start, and DMAs only ever
+// target buffers no wave reads until then).  m0 (a register the compiler
+// reserves, so it cannot be declared clobbered) is saved and restored
+// around the load, with the one wait state the hardware needs between
+// writing m0 and the load.
 template <int IMM>
 FA_DEV void dma16(__amdgpu_buffer_rsrc_t rsrc, char* lds, int voffset) {
 #if __HIP_DEVICE_COMPILE__
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(lds - IMM), 16, voffset, 0, IMM, 0);
+  const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)(lds - IMM));
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %2, %3, 0 offen offset:%4 lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(base), "v"(voffset), "s"(rsrc), "i"(IMM)
+      : "memory");
 #endif
 }
 
