@@ -73,6 +73,14 @@ FA_DEV void load_words(const char* p, uint32_t (&w)[BYTES / 4]) {
   }
 }
 
+// s_waitcnt vmcnt(N): every vector-memory load but the N most recent has
+// returned (loads return in order).
+template <int N>
+FA_DEV void wait_older_than() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 template <typename T, int N>
 FA_DEV void words_to_f32(const uint32_t* w, float* f) {
   if constexpr (T::id == FA_BF16) {
@@ -160,7 +168,14 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
   // (request, split) run together and read whole token rows of the same pages.
   const int split = blockIdx.y;
   const int64_t b = blockIdx.z;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, rg = lane >> 4, l16 = lane & 15;
+  // The wave index as a scalar: everything the steps derive from it (their
+  // positions, whether a step lies wholly inside the split) is then
+  // wave-uniform, so the full / partial load paths are scalar branches
+  // rather than exec-masked ones the compiler would run back to back (and
+  // whose merged loads made it wait for most of the next step's loads
+  // before computing the current one).
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, rg = lane >> 4, l16 = lane & 15;
   const RequestInfo r = load_request(a, b);
   if (r.q_len != 1) return;
   // Workgroup x holds query heads t GT .. t GT + GT - 1 of KV head kh's group
@@ -252,18 +267,15 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
     }
   }
 
-  // Block-table window: tab[c] of lane 4u + row holds the page of that row at
-  // step t0 + 16c + u (0 for rows outside the split).
-  int tab[4] = {0, 0, 0, 0};
-  auto load_tab = [&](int t0) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int tt = t0 + 16 * c + (lane >> 2);
-      const int rp = sb0 + WSTRIDE * tt + NT * (lane & 3);
-      const bool ok = tt < nsteps && rp + NT > plo && rp < phi;
-      tab[c] = ok ? a.block_table[b * a.bt_stride[0] + (int64_t)(rp / P) * a.bt_stride[1]] : 0;
-    }
-  };
+  // Pages: a wave step covers STEP consecutive positions from sbt (a
+  // multiple of STEP) and P is a multiple of 8, so the step's positions
+  // inside the split lie in at most two pages, A and B, and each row's NT
+  // positions in one of them.  Their block-table entries are read through
+  // the scalar cache (wave-uniform addresses, tracked apart from the K/V
+  // loads, so waiting for them never waits for K/V).  Pages are taken of
+  // positions clamped into the split, so the table is read in bounds.
+  const int lp = (P > 0 && (P & (P - 1)) == 0) ? 31 - __builtin_clz(P) : -1;
+  auto page_of = [&](int pos) { return lp >= 0 ? pos >> lp : pos / P; };
 
   // Row state advanced once per issued step: paged -> row index inside the
   // page (and its byte offsets); packed -> byte offsets of the row itself.
@@ -274,25 +286,33 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
   uint64_t vin = P ? (uint64_t)inr * vrow_b : (uint64_t)rp0 * vrow_b;
   const uint64_t kstep_packed = (uint64_t)WSTRIDE * krow_b, vstep_packed = (uint64_t)WSTRIDE * vrow_b;
 
+  // One load site per buffer: a step wholly inside the split reads positions
+  // rp .. rp + NT - 1 of each row; otherwise each row clamps them into the
+  // split (rows with none read the split's first key).  The choice is a
+  // scalar branch that only sets offsets, so the loads of consecutive steps
+  // never alias registers the compiler must wait on.
   auto issue = [&](int t, uint32_t (&kw)[NT][KB / 4], uint32_t (&vw)[NT][VB / 4]) {
     const int sbt = sb0 + WSTRIDE * t;
-    const bool full = sbt >= plo && sbt + STEP <= phi;   // every position of the wave step is in the split
+    const bool full = sbt >= plo && sbt + STEP <= phi;
     const char* krow = kbase + kin;
     const char* vrow = vbase + vin;
+    const int rp = rp0 + WSTRIDE * t;
     if (P) {
-      const int u = t & 63, c = u >> 4;
-      const int e = c == 0 ? tab[0] : c == 1 ? tab[1] : c == 2 ? tab[2] : tab[3];
-      const uint32_t blk = (uint32_t)__builtin_amdgcn_ds_bpermute((((u & 15) << 2) + rg) << 2, e);
+      const int pa = page_of(min(max(sbt, plo), phi - 1)), pb = page_of(min(max(sbt + STEP - 1, plo), phi - 1));
+      const int64_t trow = b * a.bt_stride[0];
+      const uint32_t ba = (uint32_t)load_invariant_i32(a.block_table, trow + (int64_t)pa * a.bt_stride[1]);
+      const uint32_t bb = (uint32_t)load_invariant_i32(a.block_table, trow + (int64_t)pb * a.bt_stride[1]);
+      const uint32_t blk = rp >= pb * P ? bb : ba;
       krow += (uint64_t)blk * kpage_b;
       vrow += (uint64_t)blk * vpage_b;
     }
-    if (full) {
+    uint32_t ko[NT], vo[NT];
 #pragma unroll
-      for (int i = 0; i < NT; ++i) load_words<KB>(krow + i * krow_b, kw[i]);
-#pragma unroll
-      for (int i = 0; i < NT; ++i) load_words<VB>(vrow + i * vrow_b, vw[i]);
-    } else {
-      const int rp = rp0 + WSTRIDE * t;
+    for (int i = 0; i < NT; ++i) {
+      ko[i] = (uint32_t)i * krow_b;
+      vo[i] = (uint32_t)i * vrow_b;
+    }
+    if (!full) {
       const bool row_ok = rp + NT > plo && rp < phi;
       const int lo_i = row_ok ? max(plo - rp, 0) : 0;
       const int hi_i = row_ok ? min(phi - rp, NT) - 1 : 0;
@@ -301,10 +321,16 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
         vrow = vsafe;
       }
 #pragma unroll
-      for (int i = 0; i < NT; ++i) load_words<KB>(krow + min(max(i, lo_i), hi_i) * krow_b, kw[i]);
-#pragma unroll
-      for (int i = 0; i < NT; ++i) load_words<VB>(vrow + min(max(i, lo_i), hi_i) * vrow_b, vw[i]);
+      for (int i = 0; i < NT; ++i) {
+        const uint32_t j = (uint32_t)min(max(i, lo_i), hi_i);
+        ko[i] = j * krow_b;
+        vo[i] = j * vrow_b;
+      }
     }
+#pragma unroll
+    for (int i = 0; i < NT; ++i) load_words<KB>(krow + ko[i], kw[i]);
+#pragma unroll
+    for (int i = 0; i < NT; ++i) load_words<VB>(vrow + vo[i], vw[i]);
     if (P) {
       inr += wrap;
       kin += (uint64_t)wrap * krow_b;
@@ -389,22 +415,26 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
 
   if (nsteps > 0) {
     uint32_t kwa[NT][KB / 4], vwa[NT][VB / 4], kwb[NT][KB / 4], vwb[NT][VB / 4];
-    if (P) load_tab(0);
+    // Every step issues the next step's loads unconditionally (past the last
+    // step they read the split's first key, so at most one step of extra,
+    // cached loads per wave): with a conditional issue the compiler's wait
+    // analysis merges a path with and one without those loads and then waits
+    // for the next step's loads before computing the current one.
     issue(0, kwa, vwa);
+    // The first step's loads land before the loop: the loop head then merges
+    // a preheader with nothing in flight, and the compiler keeps the next
+    // step's loads in flight across it on every iteration (without this it
+    // put an s_waitcnt vmcnt(0) at the loop head).
+    wait_older_than<0>();
     for (int t = 0;; t += 2) {
-      if (t + 1 < nsteps) {
-        if (P && ((t + 1) & 63) == 0) load_tab(t + 1);
-        issue(t + 1, kwb, vwb);
-      }
+      issue(t + 1, kwb, vwb);
       compute(t, kwa, vwa);
       if (t + 1 >= nsteps) break;
-      if (t + 2 < nsteps) {
-        if (P && ((t + 2) & 63) == 0) load_tab(t + 2);
-        issue(t + 2, kwa, vwa);
-      }
+      issue(t + 2, kwa, vwa);
       compute(t + 1, kwb, vwb);
       if (t + 2 >= nsteps) break;
     }
+    wait_older_than<0>();
   }
 
   // Combine the four 16-lane rows of the wave (same l16 <-> same dims).
