@@ -128,6 +128,20 @@ FA_DEV void widen_fp8_16(u32x4 w, u32x4& lo, u32x4& hi) {
 // Swap bits 2 and 3 of a row index (an involution).
 FA_DEV int sigma(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 
+// LDS bank slots on gfx950, measured with probe kernels
+// (SQ_LDS_BANK_CONFLICT): a 16-byte read is served 16 consecutive lanes a
+// cycle, each lane's slot being address bits [7:4] XOR (bits [9:8] << 1); a
+// 16-byte write is served 8 consecutive lanes a cycle, slot = bits [6:4].
+// The FP8 staging rows are stored with their 16-byte chunks permuted (chunk
+// u of row r at u ^ stage_rows(r), inside the row) so that the widening
+// passes, which read 4 consecutive keys x 4 consecutive chunks per 16-lane
+// group, hit 16 distinct read slots.
+template <int D> FA_DEV int stage_rows(int r) {
+  if constexpr (D == 128) return 4 * ((r >> 1) & 1);
+  else if constexpr (D == 256) return 4 * (r & 3);
+  else return 0;
+}
+
 // x combined with the value of lane ^ 32 (v_permlane32_swap exchanges the
 // wave halves; max / sum of the two results is symmetric in them).
 FA_DEV float max_hh(float x) {
@@ -542,9 +556,14 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // FP8: whole tiles into the staging buffer, 1 KiB (1024 / D rows) per
   // instruction; a wave's instructions n = w + W i each stay inside one
   // 16-key group, at the same row offset within it.
+  // The staging rows are stored with their 16-byte chunks permuted (chunk u
+  // of row r at position u ^ stage_rows(r), a per-row XOR that stays inside
+  // the row): the widening passes below then read them without bank
+  // conflicts.
   constexpr int KR8 = 1024 / DQ, VR8 = 1024 / DV;   // rows per instruction
-  const int k8off = (((KR8 * wave_u) & 15) + lane / (DQ / 16)) * (int)krow_b + (lane % (DQ / 16)) * 16;
-  const int v8off = (((VR8 * wave_u) & 15) + lane / (DV / 16)) * (int)vrow_b + (lane % (DV / 16)) * 16;
+  const int k8row = ((KR8 * wave_u) & 15) + lane / (DQ / 16), v8row = ((VR8 * wave_u) & 15) + lane / (DV / 16);
+  const int k8off = k8row * (int)krow_b + ((lane % (DQ / 16)) ^ stage_rows<DQ>(k8row)) * 16;
+  const int v8off = v8row * (int)vrow_b + ((lane % (DV / 16)) ^ stage_rows<DV>(v8row)) * 16;
   auto dma_fp8 = [&](int tile) {
 #pragma unroll
     for (int i = 0; i < 64 / KR8 / W; ++i) {
@@ -568,59 +587,59 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
       dma16<0>(rsrc, stv + slot * 64 * DV + n * 1024, v8off);
     }
   };
-  // ... and staging slot -> V buffer buf, widened exactly to T.
+  // Staging -> tile buffers, widened exactly to T.  Each 16-lane group
+  // converts 16-byte staging chunks (16 E4M3 values -> 32 bytes of T) of 4
+  // consecutive keys x 4 consecutive chunks: one 64-dim K column group, or
+  // two 32-dim V blocks.  Every lane writes its two 16-byte halves in an
+  // order that depends on the lane, so each 8-lane write cycle covers 8
+  // distinct slots: K rows r and r + 1 share a swizzle, so odd keys write
+  // their upper half first; V rows are 64 bytes, so the second block of the
+  // pair writes its upper half first.  (A mapping by consecutive staging
+  // chunks conflicted 2-4 ways on K and 4-8 ways on V writes.)  The
+  // addresses derive from an opaque copy of t so that none of them is held
+  // in registers across the main loop.
+  static_assert(!FP8 || (DQ % (16 * W) == 0 && DV % (16 * W) == 0), "FP8 widening: whole groups per pass");
+  auto widen_k_rows = [&](int t, int buf) {
+    constexpr int NG = DQ / 64, GPI = 64 * W / 16;   // column groups; 16-lane groups per pass
+    const int l16 = t & 15, m = l16 & 3, g = (t >> 4) % NG;
+#pragma unroll
+    for (int it = 0; it < DQ / (16 * W); ++it) {
+      const int q = (it * GPI + (t >> 4)) / NG;
+      const int r = 4 * q + (l16 >> 2), u = 4 * g + m, rho = sigma(r), sw = (rho >> 1) & 7, up = r & 1;
+      u32x4 lo, hi;
+      widen_fp8_16<T>(*(const u32x4*)(stk + r * DQ + 16 * (u ^ stage_rows<DQ>(r))), lo, hi);
+      char* const row = kbuf0 + buf * KTILE + g * PF_GROUP_BYTES + rho * 128;
+      *(u32x4*)(row + ((2 * m + up) ^ sw) * 16) = up ? hi : lo;
+      *(u32x4*)(row + ((2 * m + 1 - up) ^ sw) * 16) = up ? lo : hi;
+    }
+  };
+  auto widen_v_rows = [&](int t, const char* stage, int buf) {
+    constexpr int NC = DV / 64, GPI = 64 * W / 16;   // 64-dim block pairs; 16-lane groups per pass
+    const int l16 = t & 15, c = (t >> 4) % NC, up = (l16 >> 1) & 1, h = l16 & 1;
+    const int blk = 2 * c + up, u = 4 * c + (l16 & 3);
+#pragma unroll
+    for (int it = 0; it < DV / (16 * W); ++it) {
+      const int r = 4 * ((it * GPI + (t >> 4)) / NC) + (l16 >> 2);
+      u32x4 lo, hi;
+      widen_fp8_16<T>(*(const u32x4*)(stage + r * DV + 16 * (u ^ stage_rows<DV>(r))), lo, hi);
+      char* const dst = vbuf0 + buf * VTILE + blk * PF_VBLOCK_BYTES + r * 64 + 32 * h;
+      *(u32x4*)(dst + 16 * up) = up ? hi : lo;
+      *(u32x4*)(dst + 16 * (1 - up)) = up ? lo : hi;
+    }
+  };
+  // E4M3 queries: staging slot -> V buffer buf.
   auto widen_v = [&](int slot, int buf) {
     int t = tid;
     asm volatile("" : "+v"(t));
-    constexpr int CPR = DV / 16, ROWS = 64 * W / CPR;
-    const int r = t / CPR, u = t % CPR;
-    char* const dst = vbuf0 + buf * VTILE + (u >> 1) * PF_VBLOCK_BYTES + r * 64 + 32 * (u & 1);
-    const char* const src = stv + slot * 64 * DV + 16 * t;
-#pragma unroll
-    for (int it = 0; it < 4 * DV / (64 * W); ++it) {
-      u32x4 lo, hi;
-      widen_fp8_16<T>(*(const u32x4*)(src + 1024 * W * it), lo, hi);
-      *(u32x4*)(dst + ROWS * 64 * it) = lo;
-      *(u32x4*)(dst + ROWS * 64 * it + 16) = hi;
-    }
+    widen_v_rows(t, stv + slot * 64 * DV, buf);
   };
-  // FP8: staging -> tile buffer buf in the 16-bit layouts above (K: key r
-  // at row sigma(r), swizzled 8-dim chunks; V: 32-dim blocks).  Thread t
-  // converts 16-byte chunks t + 64 W i; successive i advance by 1024 W / D
-  // rows (a multiple of 16, so sigma and the swizzle shift by constants).
-  // The addresses derive from an opaque copy of t so that none of them is
-  // held in registers across the main loop.
+  // FP8 K/V: staging -> tile buffer buf in the 16-bit layouts above (K: key r
+  // at row sigma(r), swizzled 8-dim chunks; V: 32-dim blocks).
   auto widen_tile = [&](int buf) {
     int t = tid;
     asm volatile("" : "+v"(t));
-    {
-      constexpr int CPR = DQ / 16, ROWS = 64 * W / CPR;
-      const int r = t / CPR, u = t % CPR, rho = sigma(r), sw = (rho >> 1) & 7, c0 = 2 * (u & 3);
-      char* const row = kbuf0 + buf * KTILE + (u >> 2) * PF_GROUP_BYTES + rho * 128;
-      char* const lo_p = row + (c0 ^ sw) * 16;
-      char* const hi_p = row + ((c0 + 1) ^ sw) * 16;
-      const char* const src = stk + 16 * t;
-#pragma unroll
-      for (int it = 0; it < 4 * DQ / (64 * W); ++it) {
-        u32x4 lo, hi;
-        widen_fp8_16<T>(*(const u32x4*)(src + 1024 * W * it), lo, hi);
-        *(u32x4*)(lo_p + ROWS * 128 * it) = lo;
-        *(u32x4*)(hi_p + ROWS * 128 * it) = hi;
-      }
-    }
-    {
-      constexpr int CPR = DV / 16, ROWS = 64 * W / CPR;
-      const int r = t / CPR, u = t % CPR;
-      char* const dst = vbuf0 + buf * VTILE + (u >> 1) * PF_VBLOCK_BYTES + r * 64 + 32 * (u & 1);
-      const char* const src = stv + 16 * t;
-#pragma unroll
-      for (int it = 0; it < 4 * DV / (64 * W); ++it) {
-        u32x4 lo, hi;
-        widen_fp8_16<T>(*(const u32x4*)(src + 1024 * W * it), lo, hi);
-        *(u32x4*)(dst + ROWS * 64 * it) = lo;
-        *(u32x4*)(dst + ROWS * 64 * it + 16) = hi;
-      }
-    }
+    widen_k_rows(t, buf);
+    widen_v_rows(t, stv, buf);
   };
 
   // ---- Operand read offsets (bytes within a tile buffer).
