@@ -73,6 +73,27 @@ FA_DEV void load_words(const char* p, uint32_t (&w)[BYTES / 4]) {
   }
 }
 
+// The K/V stream: the same loads with the non-temporal hint (each cache row is
+// read once per call).
+typedef __attribute__((ext_vector_type(4))) uint32_t dec_u32x4;
+typedef __attribute__((ext_vector_type(2))) uint32_t dec_u32x2;
+template <int BYTES>
+FA_DEV void load_words_nt(const char* p, uint32_t (&w)[BYTES / 4]) {
+  constexpr int C = LoadChunk<BYTES>::value;
+#pragma unroll
+  for (int c = 0; c < BYTES / C; ++c) {
+    if constexpr (C == 16) {
+      const dec_u32x4 v = __builtin_nontemporal_load((const dec_u32x4*)(p + 16 * c));
+      w[4 * c] = v[0]; w[4 * c + 1] = v[1]; w[4 * c + 2] = v[2]; w[4 * c + 3] = v[3];
+    } else if constexpr (C == 8) {
+      const dec_u32x2 v = __builtin_nontemporal_load((const dec_u32x2*)(p + 8 * c));
+      w[2 * c] = v[0]; w[2 * c + 1] = v[1];
+    } else {
+      w[c] = __builtin_nontemporal_load((const uint32_t*)(p + 4 * c));
+    }
+  }
+}
+
 // s_waitcnt vmcnt(N): every vector-memory load but the N most recent has
 // returned (loads return in order).
 template <int N>
@@ -328,9 +349,9 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
       }
     }
 #pragma unroll
-    for (int i = 0; i < NT; ++i) load_words<KB>(krow + ko[i], kw[i]);
+    for (int i = 0; i < NT; ++i) load_words_nt<KB>(krow + ko[i], kw[i]);
 #pragma unroll
-    for (int i = 0; i < NT; ++i) load_words<VB>(vrow + vo[i], vw[i]);
+    for (int i = 0; i < NT; ++i) load_words_nt<VB>(vrow + vo[i], vw[i]);
     if (P) {
       inr += wrap;
       kin += (uint64_t)wrap * krow_b;
