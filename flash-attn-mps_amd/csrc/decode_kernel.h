@@ -56,6 +56,34 @@ struct LoadChunk {
   static constexpr int value = BYTES % 16 == 0 ? 16 : BYTES % 8 == 0 ? 8 : 4;
 };
 
+// Lane layout of a K or V row: a lane's BYTES are split into pieces of 16,
+// 8 or 4 bytes (largest first), and piece j of lane l sits at byte
+// 16 * start(j) + size(j) * l of the row, so each piece is one load
+// instruction over a contiguous span of the 16-lane row (a bf16 192-dim
+// row: 16 bytes at 16 l, then 8 bytes at 256 + 8 l, instead of three
+// 8-byte loads at a 24-byte lane stride; a bf16 256-dim row: 16 bytes at
+// 16 l and at 256 + 16 l).  The query takes the K row's element layout;
+// the output dims follow the V row's.
+constexpr int piece_bytes(int total, int j) {
+  int rem = total;
+  for (int i = 0; rem > 0; ++i) {
+    const int s = rem >= 16 ? 16 : rem >= 8 ? 8 : 4;
+    if (i == j) return s;
+    rem -= s;
+  }
+  return 0;
+}
+constexpr int piece_count(int total) {
+  int n = 0;
+  while (piece_bytes(total, n) > 0) ++n;
+  return n;
+}
+constexpr int piece_start(int total, int j) {
+  int s = 0;
+  for (int i = 0; i < j; ++i) s += piece_bytes(total, i);
+  return s;
+}
+
 template <int BYTES>
 FA_DEV void load_words(const char* p, uint32_t (&w)[BYTES / 4]) {
   constexpr int C = LoadChunk<BYTES>::value;
@@ -73,23 +101,27 @@ FA_DEV void load_words(const char* p, uint32_t (&w)[BYTES / 4]) {
   }
 }
 
-// The K/V stream: the same loads with the non-temporal hint (each cache row is
-// read once per call).
+// Non-temporal vector types for the K/V stream (each cache row is read once
+// per call).
 typedef __attribute__((ext_vector_type(4))) uint32_t dec_u32x4;
 typedef __attribute__((ext_vector_type(2))) uint32_t dec_u32x2;
+
+// A lane's pieces of a K or V row (non-temporal): off[j] = the lane's byte
+// offset of piece j inside the row.
 template <int BYTES>
-FA_DEV void load_words_nt(const char* p, uint32_t (&w)[BYTES / 4]) {
-  constexpr int C = LoadChunk<BYTES>::value;
+FA_DEV void load_pieces_nt(const char* row, const uint32_t (&off)[piece_count(BYTES)], uint32_t (&w)[BYTES / 4]) {
 #pragma unroll
-  for (int c = 0; c < BYTES / C; ++c) {
-    if constexpr (C == 16) {
-      const dec_u32x4 v = __builtin_nontemporal_load((const dec_u32x4*)(p + 16 * c));
-      w[4 * c] = v[0]; w[4 * c + 1] = v[1]; w[4 * c + 2] = v[2]; w[4 * c + 3] = v[3];
-    } else if constexpr (C == 8) {
-      const dec_u32x2 v = __builtin_nontemporal_load((const dec_u32x2*)(p + 8 * c));
-      w[2 * c] = v[0]; w[2 * c + 1] = v[1];
+  for (int j = 0; j < piece_count(BYTES); ++j) {
+    const char* p = row + off[j];
+    const int w0 = piece_start(BYTES, j) / 4;
+    if (piece_bytes(BYTES, j) == 16) {
+      const dec_u32x4 v = __builtin_nontemporal_load((const dec_u32x4*)p);
+      w[w0] = v[0]; w[w0 + 1] = v[1]; w[w0 + 2] = v[2]; w[w0 + 3] = v[3];
+    } else if (piece_bytes(BYTES, j) == 8) {
+      const dec_u32x2 v = __builtin_nontemporal_load((const dec_u32x2*)p);
+      w[w0] = v[0]; w[w0 + 1] = v[1];
     } else {
-      w[c] = __builtin_nontemporal_load((const uint32_t*)(p + 4 * c));
+      w[w0] = __builtin_nontemporal_load((const uint32_t*)p);
     }
   }
 }
@@ -182,6 +214,8 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
   constexpr int STEP = 4 * NT;          // positions of one wave step
   constexpr int WSTRIDE = 4 * STEP;     // positions between a wave's consecutive steps
   static_assert(EK % 4 == 0 && EV % 4 == 0 && KB % 4 == 0 && VB % 4 == 0, "decode tile shape");
+  static_assert(LK == 16 || piece_count(KB) == 1, "padded K rows use a single piece per lane");
+  static_assert(LV == 16 || piece_count(VB) == 1, "padded V rows use a single piece per lane");
   __shared__ float sm_m[4][GT], sm_l[4][GT];
   __shared__ float sm_acc[4][GT][DV];
 
@@ -231,19 +265,39 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
   }
   const int qrow = r.k_base + r.left + r.k_len - 1;
 
-  // Query pairs of this lane's dims (l16 * EK ..), unscaled, in the compute type.
+  // Query pairs of this lane's dims (the K row's piece layout), unscaled, in
+  // the compute type.  Piece j holds EP_j = size(j) / KT::bytes elements,
+  // dims 16 E_j + EP_j lq .. + EP_j (E_j = elements before piece j).
+  const int lq = min(l16, LK - 1);
   uint32_t qp[GT][EK / 2];
 #pragma unroll
   for (int g = 0; g < GT; ++g) {
     const int64_t q0 = tq * a.q_stride[0] + (int64_t)(h0 + min(g, nreal - 1)) * a.q_stride[1];
-    if (a.q_stride[2] == 1) {
-      load_words<EK * 2>((const char*)a.q + (q0 + min(l16, LK - 1) * EK) * 2, qp[g]);
-    } else {
-      const int lq = min(l16, LK - 1);
 #pragma unroll
-      for (int j = 0; j < EK / 2; ++j)
-        qp[g][j] = pack_pair_bits<CT>(load_elem<CT>(a.q, q0 + (int64_t)(lq * EK + 2 * j) * a.q_stride[2]),
-                                      load_elem<CT>(a.q, q0 + (int64_t)(lq * EK + 2 * j + 1) * a.q_stride[2]));
+    for (int j = 0; j < piece_count(KB); ++j) {
+      const int ep = piece_bytes(KB, j) / KT::bytes, e0 = piece_start(KB, j) / KT::bytes;
+      const int d0 = 16 * e0 + ep * lq;
+      uint32_t* dst = qp[g] + e0 / 2;
+      if (a.q_stride[2] == 1) {
+        const char* src = (const char*)a.q + (q0 + d0) * 2;
+        if (ep == 8) {
+          uint32_t w[4];
+          load_words<16>(src, w);
+          for (int i = 0; i < 4; ++i) dst[i] = w[i];
+        } else if (ep == 4) {
+          uint32_t w[2];
+          load_words<8>(src, w);
+          for (int i = 0; i < 2; ++i) dst[i] = w[i];
+        } else {
+          uint32_t w[8];
+          load_words<32>(src, w);
+          for (int i = 0; i < 8; ++i) dst[i] = w[i];
+        }
+      } else {
+        for (int i = 0; i < ep / 2; ++i)
+          dst[i] = pack_pair_bits<CT>(load_elem<CT>(a.q, q0 + (int64_t)(d0 + 2 * i) * a.q_stride[2]),
+                                      load_elem<CT>(a.q, q0 + (int64_t)(d0 + 2 * i + 1) * a.q_stride[2]));
+      }
     }
     if (LK < 16 && l16 >= LK) {
 #pragma unroll
@@ -271,8 +325,15 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
   // base + blk * page_stride + r * row_stride + kh * head_stride + l16 * E * bytes.
   const uint32_t kpage_b = (uint32_t)(a.k_stride[0] * KT::bytes), vpage_b = (uint32_t)(a.v_stride[0] * VT::bytes);
   const uint32_t krow_b = (uint32_t)(a.k_stride[1] * KT::bytes), vrow_b = (uint32_t)(a.v_stride[1] * VT::bytes);
-  const char* kbase = (const char*)a.k + (int64_t)kh * a.k_stride[2] * KT::bytes + min(l16, LK - 1) * KB;
-  const char* vbase = (const char*)a.v + (int64_t)kh * a.v_stride[2] * VT::bytes + min(l16, LV - 1) * VB;
+  const char* kbase = (const char*)a.k + (int64_t)kh * a.k_stride[2] * KT::bytes;
+  uint32_t koff[piece_count(KB)];
+#pragma unroll
+  for (int j = 0; j < piece_count(KB); ++j) koff[j] = 16 * piece_start(KB, j) + piece_bytes(KB, j) * lq;
+  const char* vbase = (const char*)a.v + (int64_t)kh * a.v_stride[2] * VT::bytes;
+  const int lv = min(l16, LV - 1);
+  uint32_t voff[piece_count(VB)];
+#pragma unroll
+  for (int j = 0; j < piece_count(VB); ++j) voff[j] = 16 * piece_start(VB, j) + piece_bytes(VB, j) * lv;
 
   // Address of the split's first key: the read target of rows with no valid position.
   const char* ksafe = kbase;
@@ -349,9 +410,9 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
       }
     }
 #pragma unroll
-    for (int i = 0; i < NT; ++i) load_words_nt<KB>(krow + ko[i], kw[i]);
+    for (int i = 0; i < NT; ++i) load_pieces_nt<KB>(krow + ko[i], koff, kw[i]);
 #pragma unroll
-    for (int i = 0; i < NT; ++i) load_words_nt<VB>(vrow + vo[i], vw[i]);
+    for (int i = 0; i < NT; ++i) load_pieces_nt<VB>(vrow + vo[i], voff, vw[i]);
     if (P) {
       inr += wrap;
       kin += (uint64_t)wrap * krow_b;
@@ -458,7 +519,8 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
     wait_older_than<0>();
   }
 
-  // Combine the four 16-lane rows of the wave (same l16 <-> same dims).
+  // Combine the four 16-lane rows of the wave (same l16 <-> same dims; the V
+  // row's piece layout: element e of piece j is dim 16 E_j + EP_j l16 + e - E_j).
 #pragma unroll
   for (int g = 0; g < GT; ++g) {
 #pragma unroll
@@ -482,7 +544,11 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
         sm_l[wave][g] = l[g];
       }
 #pragma unroll
-      for (int e = 0; e < EV; ++e) sm_acc[wave][g][l16 * EV + e] = acc[g][e];
+      for (int j = 0; j < piece_count(VB); ++j) {
+        const int ep = piece_bytes(VB, j) / VT::bytes, e0 = piece_start(VB, j) / VT::bytes;
+#pragma unroll
+        for (int e = 0; e < ep; ++e) sm_acc[wave][g][16 * e0 + ep * l16 + e] = acc[g][e0 + e];
+      }
     }
   }
   __syncthreads();
