@@ -497,24 +497,20 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
 
   if (nsteps > 0) {
     uint32_t kwa[NT][KB / 4], vwa[NT][VB / 4], kwb[NT][KB / 4], vwb[NT][VB / 4];
-    // Every step issues the next step's loads unconditionally (past the last
-    // step they read the split's first key, so at most one step of extra,
-    // cached loads per wave): with a conditional issue the compiler's wait
-    // analysis merges a path with and one without those loads and then waits
-    // for the next step's loads before computing the current one.
+    // Steps t + 1 and t + 2 are issued unconditionally (past the last step
+    // they read the split's first key: one K and one V row per wave,
+    // cached) and only the compute of step t + 1 is conditional, so the loop
+    // has one exit, at the bottom.  With exits after each compute (and a
+    // conditional issue before), the compiler's wait analysis put an
+    // s_waitcnt vmcnt(0) at the loop head, draining the step in flight once
+    // every two steps; in this form the next step's loads stay in flight
+    // throughout.
     issue(0, kwa, vwa);
-    // The first step's loads land before the loop: the loop head then merges
-    // a preheader with nothing in flight, and the compiler keeps the next
-    // step's loads in flight across it on every iteration (without this it
-    // put an s_waitcnt vmcnt(0) at the loop head).
-    wait_older_than<0>();
-    for (int t = 0;; t += 2) {
+    for (int t = 0; t < nsteps; t += 2) {
       issue(t + 1, kwb, vwb);
       compute(t, kwa, vwa);
-      if (t + 1 >= nsteps) break;
       issue(t + 2, kwa, vwa);
-      compute(t + 1, kwb, vwb);
-      if (t + 2 >= nsteps) break;
+      if (t + 1 < nsteps) compute(t + 1, kwb, vwb);
     }
     wait_older_than<0>();
   }
