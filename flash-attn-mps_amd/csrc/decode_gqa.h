@@ -1,0 +1,357 @@
+// Split-KV decode on the matrix cores for large GQA groups: one workgroup
+// takes up to 32 query heads of one KV head (one query token each) and a
+// split of its keys, so every K/V byte read from HBM feeds MFMAs for all of
+// them.  The VALU decode kernel (decode_kernel.h) spends per head and key a
+// 16-lane dot product and P.V FMAs; with 8 or more query heads per KV head
+// that arithmetic, not HBM, sets its pace (Hq/Hkv = 128/8 at d128: 2.3
+// TB/s).  Here the scores of 32 keys x 32 head columns are one
+// v_mfma_f32_32x32x16 chain, exactly as in the prefill kernel with the
+// group's heads in place of query rows (counterpart of the reference's decode
+// route, flash_attn_mps/_decode.py:40-99 and
+// kernels/attention_decode.metal:18-149).
+//
+// * Each of the 4 waves owns the 32-key stages w, w + 4, ... of the split and
+//   streams their 16-key groups (global -> LDS DMA) through private slots,
+//   so the waves never wait on each other inside the loop; at the end they
+//   combine (m, l, O) through LDS.  A wave loads a stage, waits for it and
+//   computes it: the latency is hidden by the other waves, and two slots per
+//   wave (16 KiB at d128) let two workgroups share a CU.  Rings of 3-5 slots
+//   per wave (one workgroup per CU, the next stage in flight while one is
+//   computed) measured 4-25% slower at d128 and up to 36% at d64: fewer
+//   waves per CU cost more than the prefetch gains.
+// * LDS layouts as in the prefill kernel (prefill_kernel.h), per 16-key
+//   slot: K rows hold key sigma(r) with 16-byte chunks XOR-swizzled by
+//   (r / 2) % 8, 64-dim column groups of 16 rows x 128 bytes; V 32-dim blocks
+//   of 16 rows x 64 bytes.
+//   S^T = K Q^T (A = K from LDS, B = Q^T in registers), P rounded to the
+//   query type, O^T += V^T P^T with V^T read by ds_read_b64_tr_b16.
+// * Supports 16-bit Q/K/V of one type, head dims 64 and 128 (Dqk = Dv),
+//   packed or paged K/V (page size a multiple of 16), sinks, softcap, left
+//   windows and descales; the host keeps other combinations on the VALU
+//   kernel.
+#ifndef FA_DECODE_GQA_H
+#define FA_DECODE_GQA_H
+
+#include "decode_kernel.h"
+#include "prefill_kernel.h"
+
+namespace fa_decode_gqa {
+
+using namespace fa_prefill;
+
+constexpr int GQA_THREADS = 256;   // 4 waves
+constexpr int GQA_HEADS = 32;      // head columns per workgroup (one MFMA tile)
+constexpr int GQA_STAGE = 32;      // keys per wave stage
+
+// One 16-key slot: K (D / 64 column groups of 16 rows x 128 bytes) then V
+// (D / 32 blocks of 16 rows x 64 bytes); slots per wave.
+template <int D> constexpr int gqa_slot_bytes() { return 64 * D; }
+template <int D> constexpr int gqa_slots() { return 2; }
+template <int D> constexpr int gqa_lds_bytes() {
+  const int ring = 4 * gqa_slots<D>() * gqa_slot_bytes<D>();
+  const int combine = 4 * GQA_HEADS * (D + 2) * 4;
+  return ring > combine ? ring : combine;
+}
+
+// One 8-row block of each of N 64-dim column groups (16 rows x 128 bytes
+// apart), and one 16-key group of each of N 32-dim V blocks (16 rows x 64
+// bytes apart): the prefill kernel's DMA shapes on 16-row slots.
+template <int N, int I = 0>
+FA_DEV void dma_columns_gqa(__amdgpu_buffer_rsrc_t rsrc, char* lds, int voffset) {
+  if constexpr (I < N) {
+    dma16<128 * I>(rsrc, lds + I * 16 * 128, voffset);
+    dma_columns_gqa<N, I + 1>(rsrc, lds, voffset);
+  }
+}
+template <int N, int I = 0>
+FA_DEV void dma_blocks_gqa(__amdgpu_buffer_rsrc_t rsrc, char* lds, int voffset) {
+  if constexpr (I < N) {
+    dma16<64 * I>(rsrc, lds + I * 16 * 64, voffset);
+    dma_blocks_gqa<N, I + 1>(rsrc, lds, voffset);
+  }
+}
+
+// s_waitcnt vmcnt(N) (the LDS DMAs of all but the N most recent
+// instructions have landed), and s_waitcnt lgkmcnt(0) (this wave's LDS
+// reads and writes are done).
+template <int N>
+FA_DEV void wait_dma_older_than() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+FA_DEV void wait_lds() { __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4)); }
+// s_waitcnt vmcnt(n * PER) for a runtime n in [0, MAXN].
+template <int PER, int MAXN>
+FA_DEV void wait_dma_groups(int n) {
+  if constexpr (MAXN == 0) {
+    wait_dma_older_than<0>();
+  } else {
+    if (n >= MAXN) wait_dma_older_than<MAXN * PER>();
+    else wait_dma_groups<PER, MAXN - 1>(n);
+  }
+}
+
+template <typename T, int D, bool CAP>
+__global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_attn_args a, const int span) {
+  static_assert(D == 64 || D == 128, "head dims 64 and 128");
+  constexpr int KSTEPS = D / 16;          // k-steps of S^T = K Q^T
+  constexpr int KG = D / 64;              // 64-dim column groups of a K slot
+  constexpr int DB = D / 32;              // 32-dim blocks of O^T / of a V slot
+  constexpr int KGROUP = 16 * 128;        // one column group: 16 rows x 128 bytes
+  constexpr int VBLOCK = 16 * 64;         // one V block: 16 rows x 64 bytes
+  constexpr int KBYTES = KG * KGROUP, SLOT = gqa_slot_bytes<D>(), NSLOT = gqa_slots<D>();
+  static_assert(NSLOT >= 2, "a stage's two slots");
+
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  char* const ring = smem + wave * NSLOT * SLOT;   // this wave's slots
+
+  // Grid: x = KV head * head tiles + tile, y = split, z = request.
+  const int group = (int)(a.heads_q / a.heads_k);
+  const int tiles = (group + GQA_HEADS - 1) / GQA_HEADS;
+  const int kh = blockIdx.x / tiles, t0 = (blockIdx.x % tiles) * GQA_HEADS;
+  const int nheads = min(GQA_HEADS, group - t0);
+  const int h0 = kh * group + t0;
+  const int split = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const RequestInfo r = load_request(a, b);
+  if (r.q_len != 1) return;
+  const int vis_begin = fa_decode::decode_vis_begin(a, r.k_len);
+  const int begin = vis_begin + split * span;
+  const int end = min(r.k_len, begin + span);
+  if (split > 0 && begin >= end) return;
+  const int S = a.num_splits;
+  const int64_t tq = r.q_begin;
+
+  // Zeroed V buffers: rows the DMA does not write (past the request) then
+  // hold finite values, which a zero probability keeps out of O.  The
+  // stores land before this wave's first DMA is issued.
+  for (int i = lane; i < NSLOT * SLOT / 16; i += 64) {
+    const int off = 16 * i;
+    if ((off % SLOT) >= KBYTES) *(u32x4*)(ring + off) = u32x4{0u, 0u, 0u, 0u};
+  }
+  wait_lds();
+
+  // Q^T operands: k-step kk, lane (l32, hh) holds head h0 + l32, dims 16 kk +
+  // 8 hh .. +8 (zeros for columns past the group).
+  u32x4 qop[KSTEPS];
+  {
+    const bool ok = l32 < nheads;
+    const uint16_t* qp = (const uint16_t*)a.q + tq * a.q_stride[0] + (int64_t)(h0 + (ok ? l32 : 0)) * a.q_stride[1] + 8 * hh;
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) qop[kk] = ok ? *(const u32x4*)(qp + 16 * kk) : u32x4{0u, 0u, 0u, 0u};
+  }
+
+  const float kdsc = descale_of(a.q_descale, a.q_descale_stride, b, kh) * descale_of(a.k_descale, a.k_descale_stride, b, kh);
+  const float vdsc = descale_of(a.v_descale, a.v_descale_stride, b, kh);
+  const float c_scale = a.softmax_scale * kdsc * LOG2E;   // raw dot -> log2 units
+  const float cap_in = CAP ? 2.0f * LOG2E * a.softmax_scale * kdsc / a.softcap : 0.0f;
+  const float cap_out = a.softcap * LOG2E;
+  // A sink logit seeds the state of one wave of split 0 (max = sink, sum = 1).
+  const bool seed = a.sinks && split == 0 && wave == 0;
+  float m_run = seed && l32 < nheads ? a.sinks[(int64_t)(h0 + l32) * a.sink_stride] * LOG2E : -INFINITY;
+  float l_run = seed && hh == 0 ? 1.0f : 0.0f;
+  f32x16 o[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
+
+  // ---- DMA.  Storage position of key j: k_base + left + j (a packed row,
+  // or slot j of the request's pages).  Stages cover 32 storage positions
+  // aligned to 32; a stage is two 16-key groups, each inside one page (the
+  // host requires a page size that is a multiple of 16).  K: one instruction
+  // moves one 8-row block of one column group (lane p -> LDS row 8 rb + p / 8,
+  // slot p % 8 holding chunk (p % 8) ^ ((row / 2) % 8); row r holds key
+  // sigma(r) of its group); V: one instruction moves one 16-key group of one
+  // 32-dim block (lane p -> row p / 4, chunk p % 4).
+  const int P = (int)a.page_size;
+  const int pos_lo = r.k_base + r.left + begin, pos_hi = r.k_base + r.left + end;   // this split's keys
+  const int pos_end = r.k_base + r.left + r.k_len;                                   // the request's end
+  const uint32_t krow_b = (uint32_t)(2 * a.k_stride[1]), vrow_b = (uint32_t)(2 * a.v_stride[1]);
+  const uint32_t kpage_b = (uint32_t)(2 * a.k_stride[0]), vpage_b = (uint32_t)(2 * a.v_stride[0]);
+  const char* const khead = (const char*)a.k + 2 * (int64_t)kh * a.k_stride[2];
+  const char* const vhead = (const char*)a.v + 2 * (int64_t)kh * a.v_stride[2];
+  const int32_t* const trow = P ? a.block_table + b * a.bt_stride[0] : nullptr;
+  int kdoff[2];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const int drow = 8 * rb + (lane >> 3);   // row within the 16-key group
+    kdoff[rb] = (int)(sigma(drow) * krow_b) + (((lane & 7) ^ ((drow >> 1) & 7)) * 16);
+  }
+  const int vdoff = (int)((lane >> 2) * vrow_b) + (lane & 3) * 16;
+  // Buffer descriptor of the 16-key group at storage position pos (a
+  // multiple of 16), covering only its keys in [pos_lo, pos_end): the base is
+  // the row of the first such key (row `first` of the group) and the size
+  // ends at the request's last key.  Lanes address their row relative to
+  // that base (voffset - first * row_b), so rows before pos_lo get negative,
+  // i.e. out-of-range offsets and are never read (they may be left padding
+  // holding anything); rows past the request are out of range at the top.
+  auto group_rsrc = [&](const char* head, uint32_t row_b, uint32_t page_b, int pos, int row_bytes, int& shift) {
+    const int first = min(max(pos_lo - pos, 0), 16);
+    const int nvalid = min(max(pos_end - pos, 0), 16) - first;
+    const char* g = head;
+    if (nvalid > 0) {
+      if (P) {
+        const uint32_t blk = (uint32_t)load_invariant_i32(trow, (int64_t)(pos / P) * a.bt_stride[1]);
+        g = head + (uint64_t)blk * page_b + (uint64_t)(uint32_t)(pos % P + first) * row_b;
+      } else {
+        g = head + (uint64_t)(uint32_t)(pos + first) * row_b;
+      }
+    }
+    shift = __builtin_amdgcn_readfirstlane(first * (int)row_b);
+    const int bytes = __builtin_amdgcn_readfirstlane(nvalid > 0 ? (nvalid - 1) * (int)row_b + row_bytes : 0);
+    return __builtin_amdgcn_make_buffer_rsrc((void*)g, (short)0, bytes, 0x00020000);
+  };
+  // Stage i of this wave: storage positions st_pos(i) .. +32, its 16-key
+  // groups 2 i and 2 i + 1; group j lives in slot j % NSLOT.
+  const int pos0 = pos_lo & ~(GQA_STAGE - 1);
+  auto st_pos = [&](int i) { return pos0 + GQA_STAGE * (wave + 4 * i); };
+  const int nst = pos_hi > pos0 + GQA_STAGE * wave ? (pos_hi - pos0 - GQA_STAGE * wave + 4 * GQA_STAGE - 1) / (4 * GQA_STAGE) : 0;
+  // 2 KG + DB DMA instructions per group.
+  constexpr int DMA_PER_GROUP = 2 * KG + DB;
+  auto dma_group = [&](int j) {
+    char* const kb = ring + (j % NSLOT) * SLOT;
+    char* const vb = kb + KBYTES;
+    const int pos = st_pos(j >> 1) + 16 * (j & 1);
+    int kshift, vshift;
+    const auto kr = group_rsrc(khead, krow_b, kpage_b, pos, 2 * D, kshift);
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) dma_columns_gqa<KG>(kr, kb + 8 * rb * 128, kdoff[rb] - kshift);
+    const auto vr = group_rsrc(vhead, vrow_b, vpage_b, pos, 2 * D, vshift);
+    dma_blocks_gqa<DB>(vr, vb, vdoff - vshift);
+  };
+
+  // Operand read offsets (bytes within a slot): K (A of S^T) row l32 % 16 of
+  // the stage's slot l32 / 16, chunk 2 (kk % 4) + hh of column group kk / 4;
+  // V^T through ds_read_b64_tr_b16 as in the prefill kernel, keys 16 c ..
+  // +16 from the stage's slot c.
+  const int r16 = l32 & 15;
+  int krd[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) krd[s] = r16 * 128 + (((2 * s + hh) ^ ((r16 >> 1) & 7)) * 16);
+  const int vg16 = lane >> 4, vi = lane & 15, va = vi & 3, vt = vi >> 2;
+  const int vrd = KBYTES + (8 * (vg16 >> 1) + vt) * 64 + (4 * (vg16 & 1) + va) * 8;
+
+  auto compute = [&](int i) {
+    const char* const slot0 = ring + ((2 * i) % NSLOT) * SLOT;
+    const char* const slot1 = ring + ((2 * i + 1) % NSLOT) * SLOT;
+    const char* const kb = l32 < 16 ? slot0 : slot1;
+    f32x16 s;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s[e] = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) s = mfma32<T>(lds_read16(kb, krd[kk % 4] + (kk / 4) * KGROUP), qop[kk], s);
+    // s[e] = score of storage position st_pos(i) + 16 (e >> 3) + 8 hh + (e & 7).
+    const int p0 = st_pos(i) + 8 * hh;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      float v = s[e];
+      if constexpr (CAP) v = cap_out * (1.0f - 2.0f * __builtin_amdgcn_rcpf(fast_exp2(cap_in * v) + 1.0f));
+      else v *= c_scale;
+      const int pos = p0 + 16 * (e >> 3) + (e & 7);
+      v = (pos >= pos_lo && pos < pos_hi) ? v : -INFINITY;
+      s[e] = v;
+      mx = fmaxf(mx, v);
+    }
+    mx = max_hh(mx);
+    const float m_new = fmaxf(m_run, mx);
+    const float mref = m_new == -INFINITY ? 0.0f : m_new;
+    const float f = fast_exp2((m_run == -INFINITY ? mref : m_run) - mref);
+    m_run = m_new;
+    l_run *= f;
+    if (__builtin_expect(__any(f != 1.0f), 0)) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[db][e] *= f;
+    }
+    float psum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float p = fast_exp2(s[e] - mref);
+      s[e] = p;
+      psum += p;
+    }
+    l_run += psum;
+    u32x4 pop[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) pop[c][q] = pack2<T>(s[8 * c + 2 * q], s[8 * c + 2 * q + 1]);
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const char* const vb = c ? slot1 : slot0;
+        const u32x2 lo = lds_read_tr(vb, vrd + db * VBLOCK);
+        const u32x2 hi = lds_read_tr(vb, vrd + db * VBLOCK + 4 * 64);
+        o[db] = mfma32<T>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pop[c], o[db]);
+      }
+  };
+
+  // The ring starts full; stage i waits for its two groups (the NSLOT - 2
+  // later ones stay in flight), is computed, and its two slots, once its LDS
+  // reads are done, take groups 2 i + NSLOT and 2 i + NSLOT + 1.
+  const int ngroups = 2 * nst;
+  int issued = 0;
+  for (; issued < min(NSLOT, ngroups); ++issued) dma_group(issued);
+  for (int i = 0; i < nst; ++i) {
+    wait_dma_groups<DMA_PER_GROUP, NSLOT - 2>(issued - 2 * i - 2);
+    compute(i);
+    wait_lds();
+    for (; issued < min(2 * i + 2 + NSLOT, ngroups); ++issued) dma_group(issued);
+  }
+
+  // ---- Combine the four waves: per head m (log2 units), l and O^T through
+  // LDS (the stage buffers are done once every wave passes the barrier).
+  const float lt = sum_hh(l_run);
+  __syncthreads();
+  float* const cm = (float*)smem;                      // [4][32]
+  float* const cl = cm + 4 * GQA_HEADS;                // [4][32]
+  float* const co = cl + 4 * GQA_HEADS;                // [4][32][D]
+  if (hh == 0) {
+    cm[wave * GQA_HEADS + l32] = m_run;
+    cl[wave * GQA_HEADS + l32] = lt;
+  }
+  // o[db][4 g + j] = O^T[dim 32 db + 8 g + 4 hh + j][head l32].
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      *(float4*)(co + ((int64_t)wave * GQA_HEADS + l32) * D + 32 * db + 8 * g + 4 * hh) =
+          float4{o[db][4 * g], o[db][4 * g + 1], o[db][4 * g + 2], o[db][4 * g + 3]};
+  __syncthreads();
+  for (int idx = tid; idx < nheads * D; idx += GQA_THREADS) {
+    const int hc = idx / D, d = idx - hc * D;
+    float M = cm[hc];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) M = fmaxf(M, cm[w * GQA_HEADS + hc]);
+    const float ref = M == -INFINITY ? 0.0f : M;
+    float L = 0.0f, O = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float fw = fast_exp2(cm[w * GQA_HEADS + hc] - ref);
+      L += cl[w * GQA_HEADS + hc] * fw;
+      O += co[((int64_t)w * GQA_HEADS + hc) * D + d] * fw;
+    }
+    const float norm = L > 0.0f ? vdsc / L : 0.0f;
+    const float lse = L > 0.0f ? M * LN2 + logf(L) : -INFINITY;
+    const int h = h0 + hc;
+    if (S == 1) {
+      store_any(a.out, tq * a.out_stride[0] + (int64_t)h * a.out_stride[1] + (int64_t)d * a.out_stride[2], a.out_dtype,
+                O * norm);
+      if (d == 0) a.lse[(int64_t)h * a.lse_stride[0] + tq * a.lse_stride[1]] = lse;
+    } else {
+      const int64_t row = (b * a.heads_q + h) * S + split;
+      a.partial_out[row * D + d] = O * norm;
+      if (d == 0) a.partial_lse[row] = lse;
+    }
+  }
+}
+
+}  // namespace fa_decode_gqa
+
+#endif  // FA_DECODE_GQA_H

@@ -631,4 +631,15 @@ DecodeKernel pick_decode_f16(int64_t d, int64_t dv, int gt, bool cap, bool alibi
 DecodeKernel pick_decode_fp8_bf16(int64_t d, int64_t dv, int gt, bool cap, bool alibi);
 DecodeKernel pick_decode_fp8_f16(int64_t d, int64_t dv, int gt, bool cap, bool alibi);
 
+// The matrix-core decode for GQA groups of DECODE_GQA_MIN_GROUP or more query
+// heads per KV head (decode_gqa.h, decode_gqa.hip): its kernel and LDS bytes,
+// or a null kernel when the arguments need the VALU kernel.  Its workgroups
+// take 32 query heads of one KV head each.
+constexpr int DECODE_GQA_MIN_GROUP = 8;
+struct GqaChoice {
+  DecodeKernel kern;
+  size_t lds;
+};
+GqaChoice pick_decode_gqa(const fa_attn_args& a);
+
 }  // namespace fa_decode

@@ -161,10 +161,19 @@ DecodeKernel select_decode(const fa_attn_args& a, int* gt_out) {
   }
 }
 
+// Workgroups per (request, split): KV heads x head tiles of the kernel that
+// runs (32 query heads for the matrix-core GQA kernel, GT for the VALU one).
+int64_t decode_head_groups(const fa_attn_args& a, int gt) {
+  const int64_t group = a.heads_q / a.heads_k;
+  const int tile = pick_decode_gqa(a).kern ? 32 : gt;
+  return a.heads_k * fa_ceil_div(group, tile);
+}
+
 }  // namespace
 
 extern "C" int fa_decode_supported(const fa_attn_args* a) {
   if (!a) return 0;
+  if (pick_decode_gqa(*a).kern) return 1;
   int gt = 0;
   return select_decode(*a, &gt) != nullptr;
 }
@@ -175,7 +184,8 @@ namespace {
 // arguments that passed fa_validate_attn.
 int decode_launch(const fa_attn_args* a, void* stream, const char* who) {
   int gt = 1;
-  const DecodeKernel kern = select_decode(*a, &gt);
+  const GqaChoice gqa = pick_decode_gqa(*a);
+  const DecodeKernel kern = gqa.kern ? gqa.kern : select_decode(*a, &gt);
   if (!kern) {
     fa_set_error("%s: unsupported dtype/head-dim/stride combination", who);
     return FA_ERR_UNSUPPORTED;
@@ -188,11 +198,18 @@ int decode_launch(const fa_attn_args* a, void* stream, const char* who) {
              (long long)a->num_splits * a->split_span, (long long)decode_visible_max(*a));
   FA_REQUIRE(a->num_splits == 1 || (a->partial_out && a->partial_lse), "%s: splits need partial buffers", who);
   FA_REQUIRE(a->batch <= 65535, "%s: batch exceeds the grid limit", who);
-  const int64_t head_groups = a->heads_k * fa_ceil_div(a->heads_q / a->heads_k, gt);
+  const int64_t head_groups = decode_head_groups(*a, gt);
   FA_REQUIRE(a->num_splits <= 65535, "%s: too many splits", who);
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)head_groups, (unsigned)a->num_splits, (unsigned)a->batch);
-  hipLaunchKernelGGL(kern, grid, dim3(DEC_THREADS), 0, s, *a, (int)a->split_span);
+  if (gqa.kern) {
+    const hipError_t err = hipFuncSetAttribute((const void*)gqa.kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)gqa.lds);
+    if (err != hipSuccess) {
+      fa_set_error("%s: cannot reserve %zu bytes of LDS: %s", who, gqa.lds, hipGetErrorString(err));
+      return FA_ERR_LAUNCH;
+    }
+  }
+  hipLaunchKernelGGL(kern, grid, dim3(DEC_THREADS), gqa.kern ? gqa.lds : 0, s, *a, (int)a->split_span);
   int rc = fa_check_launch(who);
   if (rc || a->num_splits == 1) return rc;
   const int64_t rows = a->batch * a->heads_q;
@@ -220,7 +237,7 @@ void plan_splits(const fa_attn_args& a, int gt, int64_t cap_floats, int32_t* spl
     *span_out = 32;
     return;
   }
-  const int64_t groups = a.heads_k * fa_ceil_div(a.heads_q / a.heads_k, gt);
+  const int64_t groups = decode_head_groups(a, gt);
   int64_t span = 2048;
   while (span > 128 && a.batch * groups * fa_ceil_div(vis, span) < 2048) span /= 2;
   int64_t splits = fa_ceil_div(vis, span);
@@ -281,7 +298,7 @@ extern "C" int fa_decode_fwd_noalloc(const fa_attn_args* in, void* stream) {
   constexpr int64_t cap = FA_DECODE_SCRATCH_BYTES / (int64_t)sizeof(float);
   if (a.num_splits == 0) {
     int gt = 1;
-    if (!select_decode(a, &gt)) {
+    if (!pick_decode_gqa(a).kern && !select_decode(a, &gt)) {
       fa_set_error("fa_decode_fwd_noalloc: unsupported dtype/head-dim/stride combination");
       return FA_ERR_UNSUPPORTED;
     }

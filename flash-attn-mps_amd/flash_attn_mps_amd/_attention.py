@@ -162,9 +162,9 @@ def _mixed_batch(p, a):
     dec = _lib.AttnArgs.from_buffer_copy(a)
     if not _lib.supported("fa_decode_supported", dec):
         return False
-    from ._decode import split_plan, workgroups_per_token
-    splits, span = split_plan(p.batch, workgroups_per_token(p.heads, p.kv_heads, p.dim_qk, p.dim_v),
-                              p.max_k, 0)
+    from ._decode import split_plan, uses_gqa_kernel, workgroups_per_token
+    groups = workgroups_per_token(p.heads, p.kv_heads, p.dim_qk, p.dim_v, uses_gqa_kernel(p))
+    splits, span = split_plan(p.batch, groups, p.max_k, 0)
     dec.num_splits, dec.split_span = splits, span
     if splits > 1:
         _partials(p, dec, (p.batch, p.heads, splits, p.dim_v), (p.batch, p.heads, splits))

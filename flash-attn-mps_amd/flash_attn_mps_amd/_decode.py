@@ -50,9 +50,26 @@ def group_tile(heads, kv_heads, dim_qk, dim_v):
     return tile
 
 
-def workgroups_per_token(heads, kv_heads, dim_qk, dim_v):
+# Query heads per KV head from which the matrix-core GQA decode kernel runs
+# (DECODE_GQA_MIN_GROUP in decode_kernel.h); its workgroups take 32 heads.
+_GQA_MIN_GROUP = 8
+_GQA_TILE = 32
+
+
+def uses_gqa_kernel(p):
+    """Whether fa_decode_fwd runs Problem `p` on the matrix-core GQA kernel
+    (mirrors pick_decode_gqa in decode_gqa.hip, stride alignment aside, which
+    only changes the split plan's workgroup estimate)."""
+    page = p.k.shape[1] if p.paged else 0
+    return (p.heads // p.kv_heads >= _GQA_MIN_GROUP and p.q.dtype == p.k.dtype == p.v.dtype
+            and p.q.dtype in (torch.float16, torch.bfloat16) and p.dim_qk == p.dim_v and p.dim_qk in (64, 128)
+            and p.alibi is None and p.mask is None and page % 16 == 0)
+
+
+def workgroups_per_token(heads, kv_heads, dim_qk, dim_v, gqa=False):
     """Decode workgroups per (request, split): KV heads x ceil(group / tile)."""
-    return kv_heads * -(-(heads // kv_heads) // group_tile(heads, kv_heads, dim_qk, dim_v))
+    tile = _GQA_TILE if gqa else group_tile(heads, kv_heads, dim_qk, dim_v)
+    return kv_heads * -(-(heads // kv_heads) // tile)
 
 
 def decode(p, out):
@@ -67,7 +84,7 @@ def decode(p, out):
     a = build_args(p, out, lse, max_q=1)
     a.causal, a.causal_by_batch = 0, None   # a right-aligned single query has no future keys
     if _lib.supported("fa_decode_supported", a):
-        groups = workgroups_per_token(p.heads, p.kv_heads, p.dim_qk, p.dim_v)
+        groups = workgroups_per_token(p.heads, p.kv_heads, p.dim_qk, p.dim_v, uses_gqa_kernel(p))
         splits, span = split_plan(p.batch, groups, p.visible_max, p.splits)
         a.num_splits, a.split_span = splits, span
         if splits > 1:

@@ -1,0 +1,109 @@
+"""The matrix-core decode for GQA groups of 8 or more query heads per KV head
+(csrc/decode_gqa.h) against the CPU oracle.
+
+It runs for 16-bit Q/K/V of one type at Dqk = Dv in {64, 128}: 32 head
+columns per workgroup (groups of 48 and 64 take two), 4 waves each streaming
+their own 32-key stages.  The cases cover the stage edges (0, 1, 31, 32, 33
+keys and long contexts), split counts, sinks, softcap, left windows, left
+padding whose slots hold NaN (rows before a split's first key must never be
+read), NaN-poisoned slots past each request, packed and paged K/V (pages of
+16 and 48 tokens) and sentinels around a caller-owned output.  Parity bar:
+fp16 2e-3, bf16 1e-2, LSE 1e-4 max-abs.
+"""
+import pytest
+import torch
+
+from flash_attn_mps_amd import _lib
+from flash_attn_mps_amd._decode import uses_gqa_kernel
+from harness import assert_parity, decode_attention, kernel_args, oracle_attention, problem
+
+pytestmark = pytest.mark.gpu
+
+
+def _i32(values, device):
+    return torch.tensor(values, device=device, dtype=torch.int32)
+
+
+def _pool(stored, page, kv_heads, dim, dtype, device, seed, valid_from):
+    """Paged K/V of a permuted pool: slot j of request b is real for
+    valid_from[b] <= j < stored[b] and NaN elsewhere (padding and tails)."""
+    g = torch.Generator().manual_seed(seed)
+    cols = max(-(-n // page) for n in stored) + 1
+    pool = len(stored) * cols
+    table = torch.randperm(pool, generator=g).int().reshape(len(stored), cols)
+    kc = torch.randn(pool, page, kv_heads, dim, generator=g)
+    vc = torch.randn(pool, page, kv_heads, dim, generator=g) * 0.5
+    for b, n in enumerate(stored):
+        for pos in list(range(0, valid_from[b])) + list(range(n, cols * page)):
+            kc[table[b, pos // page], pos % page] = float("nan")
+            vc[table[b, pos // page], pos % page] = float("nan")
+    return kc.to(dtype).to(device), vc.to(dtype).to(device), table.to(device), cols
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(8, 1), (16, 2), (32, 1), (48, 1), (64, 2)])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("splits", [0, 1, 3])
+def test_groups_dims_and_splits(device, heads, kv_heads, d, dtype, splits):
+    lengths, page = [1, 31, 32, 33, 0, 300, 2049, 77], 16
+    kc, vc, table, cols = _pool(lengths, page, kv_heads, d, dtype, device, 700 + heads + d + splits,
+                                [0] * len(lengths))
+    g = torch.Generator().manual_seed(701 + heads + d)
+    q = torch.randn(len(lengths), heads, d, generator=g).to(dtype).to(device)
+    cu_q, used = torch.arange(len(lengths) + 1, device=device, dtype=torch.int32), _i32(lengths, device)
+    sinks = torch.linspace(-2, 2, heads, device=device)
+    buffer = torch.full((len(lengths), heads + 8, d), 7.0, device=device, dtype=dtype)
+    kw = dict(cu_seqlens_q=cu_q, seqused_k=used, block_table=table, s_aux=sinks)
+    p = problem(q, kc, vc, max_seqlen_q=1, max_seqlen_k=cols * page, **kw)
+    assert uses_gqa_kernel(p)
+    got, lse = decode_attention(q, kc, vc, max_seqlen_k=cols * page, num_splits=splits, out=buffer[:, :heads], **kw)
+    ref, ref_lse = oracle_attention(q, kc, vc, cu_q, used_k=used, block_table=table, sinks=sinks)
+    assert_parity(got, lse, ref, ref_lse)
+    assert (buffer[:, heads:] == 7.0).all(), "a head slot past the call was stored"
+
+
+@pytest.mark.parametrize("window", [(-1, -1), (0, 0), (45, 0), (1000, -1)])
+@pytest.mark.parametrize("splits", [0, 2])
+@pytest.mark.parametrize("page", [16, 48])
+def test_softcap_windows_and_left_padding(device, window, splits, page):
+    """Left padding of 0-17 slots holding NaN before each request's keys; a
+    left window then starts a split in the middle of a 16-key group."""
+    lengths, left = [1, 40, 777, 0, 1500, 33], [0, 5, 17, 3, 0, 16]
+    stored = [n + p for n, p in zip(lengths, left)]
+    heads, kv_heads, d = 32, 2, 128
+    kc, vc, table, cols = _pool(stored, page, kv_heads, d, torch.bfloat16, device, 710 + page + splits, left)
+    g = torch.Generator().manual_seed(711)
+    q = torch.randn(len(lengths), heads, d, generator=g).to(torch.bfloat16).to(device)
+    cu_q, used, pads = (torch.arange(len(lengths) + 1, device=device, dtype=torch.int32), _i32(lengths, device),
+                        _i32(left, device))
+    sinks = torch.linspace(-1, 1, heads, device=device)
+    kw = dict(cu_seqlens_q=cu_q, seqused_k=used, block_table=table, leftpad_k=pads, window_size=window,
+              softcap=30.0, s_aux=sinks)
+    keep = []
+    probe = kernel_args(q, kc, vc, torch.empty_like(q), torch.empty(heads, len(lengths), device=device), keep=keep,
+                        max_seqlen_q=1, max_seqlen_k=cols * page, **kw)
+    assert _lib.supported("fa_decode_supported", probe)
+    got, lse = decode_attention(q, kc, vc, max_seqlen_k=cols * page, num_splits=splits, **kw)
+    ref, ref_lse = oracle_attention(q, kc, vc, cu_q, used_k=used, block_table=table, leftpad=left, window=window,
+                                    softcap=30.0, sinks=sinks)
+    assert_parity(got, lse, ref, ref_lse)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_packed_keys_explicit_scale_and_descales(device, d):
+    """Packed K/V rows (cu_seqlens_k), softmax_scale 1/8 and per-(request,
+    KV head) descales of a 16-bit cache (they scale the scores and the output)."""
+    k_lens, heads, kv_heads = [3, 257, 0, 64, 129], 16, 2
+    g = torch.Generator().manual_seed(720 + d)
+    q = torch.randn(len(k_lens), heads, d, generator=g).to(torch.float16).to("cpu")
+    k = torch.randn(sum(k_lens), kv_heads, d, generator=g).to(torch.float16)
+    v = (torch.randn(sum(k_lens), kv_heads, d, generator=g) * 0.5).to(torch.float16)
+    kd = torch.rand(len(k_lens), kv_heads, generator=g) * 0.5 + 0.75
+    vd = torch.rand(len(k_lens), kv_heads, generator=g) * 0.5 + 0.5
+    cu_q = torch.arange(len(k_lens) + 1, dtype=torch.int32)
+    cu_k = torch.tensor([0] + list(torch.tensor(k_lens).cumsum(0)), dtype=torch.int32)
+    got, lse = decode_attention(q.to(device), k.to(device), v.to(device), cu_seqlens_q=cu_q.to(device),
+                                cu_seqlens_k=cu_k.to(device), max_seqlen_k=max(k_lens), softmax_scale=0.125,
+                                k_descale=kd.to(device), v_descale=vd.to(device))
+    ref, ref_lse = oracle_attention(q, k, v, cu_q, cu_k, scale=0.125, k_descale=kd, v_descale=vd)
+    assert_parity(got, lse, ref, ref_lse)
