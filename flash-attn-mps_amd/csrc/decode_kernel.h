@@ -635,7 +635,7 @@ DecodeKernel pick_decode_fp8_f16(int64_t d, int64_t dv, int gt, bool cap, bool a
 // heads per KV head (decode_gqa.h, decode_gqa.hip): its kernel and LDS bytes,
 // or a null kernel when the arguments need the VALU kernel.  Its workgroups
 // take 32 query heads of one KV head each.
-constexpr int DECODE_GQA_MIN_GROUP = 8;
+constexpr int DECODE_GQA_MIN_GROUP = 5;
 struct GqaChoice {
   DecodeKernel kern;
   size_t lds;

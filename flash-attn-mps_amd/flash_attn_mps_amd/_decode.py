@@ -52,7 +52,7 @@ def group_tile(heads, kv_heads, dim_qk, dim_v):
 
 # Query heads per KV head from which the matrix-core GQA decode kernel runs
 # (DECODE_GQA_MIN_GROUP in decode_kernel.h); its workgroups take 32 heads.
-_GQA_MIN_GROUP = 8
+_GQA_MIN_GROUP = 5
 _GQA_TILE = 32
 
 

@@ -1,4 +1,4 @@
-"""The matrix-core decode for GQA groups of 8 or more query heads per KV head
+"""The matrix-core decode for GQA groups of 5 or more query heads per KV head
 (csrc/decode_gqa.h) against the CPU oracle.
 
 It runs for 16-bit Q/K/V of one type at Dqk = Dv in {64, 128}: 32 head
@@ -40,7 +40,7 @@ def _pool(stored, page, kv_heads, dim, dtype, device, seed, valid_from):
     return kc.to(dtype).to(device), vc.to(dtype).to(device), table.to(device), cols
 
 
-@pytest.mark.parametrize("heads,kv_heads", [(8, 1), (16, 2), (32, 1), (48, 1), (64, 2)])
+@pytest.mark.parametrize("heads,kv_heads", [(5, 1), (8, 1), (14, 2), (32, 1), (48, 1), (64, 2)])
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("splits", [0, 1, 3])
@@ -95,7 +95,7 @@ def test_packed_keys_explicit_scale_and_descales(device, d):
     KV head) descales of a 16-bit cache (they scale the scores and the output)."""
     k_lens, heads, kv_heads = [3, 257, 0, 64, 129], 16, 2
     g = torch.Generator().manual_seed(720 + d)
-    q = torch.randn(len(k_lens), heads, d, generator=g).to(torch.float16).to("cpu")
+    q = torch.randn(len(k_lens), heads, d, generator=g).to(torch.float16)
     k = torch.randn(sum(k_lens), kv_heads, d, generator=g).to(torch.float16)
     v = (torch.randn(sum(k_lens), kv_heads, d, generator=g) * 0.5).to(torch.float16)
     kd = torch.rand(len(k_lens), kv_heads, generator=g) * 0.5 + 0.75
