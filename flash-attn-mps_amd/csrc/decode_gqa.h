@@ -20,10 +20,13 @@
 //   per wave (one workgroup per CU, the next stage in flight while one is
 //   computed) measured 4-25% slower at d128 and up to 36% at d64: fewer
 //   waves per CU cost more than the prefetch gains.
-// * LDS layouts as in the prefill kernel (prefill_kernel.h), per 16-key
-//   slot: K rows hold key sigma(r) with 16-byte chunks XOR-swizzled by
-//   (r / 2) % 8, 64-dim column groups of 16 rows x 128 bytes; V 32-dim blocks
-//   of 16 rows x 64 bytes.
+// * LDS layouts per 16-key slot: K as in the prefill kernel
+//   (prefill_kernel.h), rows holding key sigma(r) with 16-byte chunks
+//   XOR-swizzled by (r / 2) % 8, 64-dim column groups of 16 rows x 128
+//   bytes; V 64-dim column groups of 16 rows x 128 bytes, unswizzled, so
+//   that each DMA instruction reads whole 128-byte lines (the prefill's
+//   32-dim V blocks of 64-byte rows split each line over two instructions:
+//   2% slower at d128, 4% at d64).
 //   S^T = K Q^T (A = K from LDS, B = Q^T in registers), P rounded to the
 //   query type, O^T += V^T P^T with V^T read by ds_read_b64_tr_b16.
 // * Supports 16-bit Q/K/V of one type, head dims 64 and 128 (Dqk = Dv),
@@ -44,8 +47,8 @@ constexpr int GQA_THREADS = 256;   // 4 waves
 constexpr int GQA_HEADS = 32;      // head columns per workgroup (one MFMA tile)
 constexpr int GQA_STAGE = 32;      // keys per wave stage
 
-// One 16-key slot: K (D / 64 column groups of 16 rows x 128 bytes) then V
-// (D / 32 blocks of 16 rows x 64 bytes); slots per wave.
+// One 16-key slot: K then V, each D / 64 column groups of 16 rows x 128
+// bytes; slots per wave.
 template <int D> constexpr int gqa_slot_bytes() { return 64 * D; }
 template <int D> constexpr int gqa_slots() { return 2; }
 template <int D> constexpr int gqa_lds_bytes() {
@@ -55,20 +58,12 @@ template <int D> constexpr int gqa_lds_bytes() {
 }
 
 // One 8-row block of each of N 64-dim column groups (16 rows x 128 bytes
-// apart), and one 16-key group of each of N 32-dim V blocks (16 rows x 64
-// bytes apart): the prefill kernel's DMA shapes on 16-row slots.
+// apart): one DMA instruction per 8 rows x 128 bytes.
 template <int N, int I = 0>
 FA_DEV void dma_columns_gqa(__amdgpu_buffer_rsrc_t rsrc, char* lds, int voffset) {
   if constexpr (I < N) {
     dma16<128 * I>(rsrc, lds + I * 16 * 128, voffset);
     dma_columns_gqa<N, I + 1>(rsrc, lds, voffset);
-  }
-}
-template <int N, int I = 0>
-FA_DEV void dma_blocks_gqa(__amdgpu_buffer_rsrc_t rsrc, char* lds, int voffset) {
-  if constexpr (I < N) {
-    dma16<64 * I>(rsrc, lds + I * 16 * 64, voffset);
-    dma_blocks_gqa<N, I + 1>(rsrc, lds, voffset);
   }
 }
 
@@ -97,9 +92,8 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   static_assert(D == 64 || D == 128, "head dims 64 and 128");
   constexpr int KSTEPS = D / 16;          // k-steps of S^T = K Q^T
   constexpr int KG = D / 64;              // 64-dim column groups of a K slot
-  constexpr int DB = D / 32;              // 32-dim blocks of O^T / of a V slot
+  constexpr int DB = D / 32;              // 32-dim blocks of O^T
   constexpr int KGROUP = 16 * 128;        // one column group: 16 rows x 128 bytes
-  constexpr int VBLOCK = 16 * 64;         // one V block: 16 rows x 64 bytes
   constexpr int KBYTES = KG * KGROUP, SLOT = gqa_slot_bytes<D>(), NSLOT = gqa_slots<D>();
   static_assert(NSLOT >= 2, "a stage's two slots");
 
@@ -165,8 +159,8 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   // host requires a page size that is a multiple of 16).  K: one instruction
   // moves one 8-row block of one column group (lane p -> LDS row 8 rb + p / 8,
   // slot p % 8 holding chunk (p % 8) ^ ((row / 2) % 8); row r holds key
-  // sigma(r) of its group); V: one instruction moves one 16-key group of one
-  // 32-dim block (lane p -> row p / 4, chunk p % 4).
+  // sigma(r) of its group); V likewise, unswizzled and unpermuted (lane p ->
+  // row 8 rb + p / 8, chunk p % 8).
   const int P = (int)a.page_size;
   const int pos_lo = r.k_base + r.left + begin, pos_hi = r.k_base + r.left + end;   // this split's keys
   const int pos_end = r.k_base + r.left + r.k_len;                                   // the request's end
@@ -181,7 +175,9 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
     const int drow = 8 * rb + (lane >> 3);   // row within the 16-key group
     kdoff[rb] = (int)(sigma(drow) * krow_b) + (((lane & 7) ^ ((drow >> 1) & 7)) * 16);
   }
-  const int vdoff = (int)((lane >> 2) * vrow_b) + (lane & 3) * 16;
+  int vdoff[2];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) vdoff[rb] = (int)((8 * rb + (lane >> 3)) * vrow_b) + (lane & 7) * 16;
   // Buffer descriptor of the 16-key group at storage position pos (a
   // multiple of 16), covering only its keys in [pos_lo, pos_end): the base is
   // the row of the first such key (row `first` of the group) and the size
@@ -189,13 +185,39 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   // that base (voffset - first * row_b), so rows before pos_lo get negative,
   // i.e. out-of-range offsets and are never read (they may be left padding
   // holding anything); rows past the request are out of range at the top.
-  auto group_rsrc = [&](const char* head, uint32_t row_b, uint32_t page_b, int pos, int row_bytes, int& shift) {
+  // Stage i of this wave: storage positions st_pos(i) .. +32, its 16-key
+  // groups 2 i and 2 i + 1; group j lives in slot j % NSLOT.
+  const int pos0 = pos_lo & ~(GQA_STAGE - 1);
+  auto st_pos = [&](int i) { return pos0 + GQA_STAGE * (wave + 4 * i); };
+  const int nst = pos_hi > pos0 + GQA_STAGE * wave ? (pos_hi - pos0 - GQA_STAGE * wave + 4 * GQA_STAGE - 1) / (4 * GQA_STAGE) : 0;
+  const int ngroups = 2 * nst;
+  auto group_pos = [&](int j) { return st_pos(j >> 1) + 16 * (j & 1); };
+  // Pages of this wave's groups, 64 at a time: lane l of `pages` holds the
+  // block-table entry of group 64 chunk + l (0 for groups with no key of the
+  // split), read once per chunk with one vector load; each group then takes
+  // its entry with v_readlane instead of a scalar load and its wait.  Every
+  // load of the wave has landed when a chunk is read (before the first DMA,
+  // or after a stage's DMAs were waited for), so the wait is free.
+  int chunk = -1;
+  uint32_t pages = 0;
+  auto page_of_group = [&](int j) {
+    if ((j >> 6) != chunk) {
+      chunk = j >> 6;
+      const int jj = 64 * chunk + lane, pos = group_pos(jj);
+      const bool need = jj < ngroups && pos + 16 > pos_lo && pos < pos_end;
+      pages = need ? (uint32_t)trow[(int64_t)(pos / P) * a.bt_stride[1]] : 0u;
+      wait_dma_older_than<0>();
+    }
+    return (uint32_t)__builtin_amdgcn_readlane((int)pages, j & 63);
+  };
+  auto group_rsrc = [&](const char* head, uint32_t row_b, uint32_t page_b, int j, int row_bytes, int& shift) {
+    const int pos = group_pos(j);
     const int first = min(max(pos_lo - pos, 0), 16);
     const int nvalid = min(max(pos_end - pos, 0), 16) - first;
     const char* g = head;
     if (nvalid > 0) {
       if (P) {
-        const uint32_t blk = (uint32_t)load_invariant_i32(trow, (int64_t)(pos / P) * a.bt_stride[1]);
+        const uint32_t blk = page_of_group(j);
         g = head + (uint64_t)blk * page_b + (uint64_t)(uint32_t)(pos % P + first) * row_b;
       } else {
         g = head + (uint64_t)(uint32_t)(pos + first) * row_b;
@@ -205,35 +227,32 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
     const int bytes = __builtin_amdgcn_readfirstlane(nvalid > 0 ? (nvalid - 1) * (int)row_b + row_bytes : 0);
     return __builtin_amdgcn_make_buffer_rsrc((void*)g, (short)0, bytes, 0x00020000);
   };
-  // Stage i of this wave: storage positions st_pos(i) .. +32, its 16-key
-  // groups 2 i and 2 i + 1; group j lives in slot j % NSLOT.
-  const int pos0 = pos_lo & ~(GQA_STAGE - 1);
-  auto st_pos = [&](int i) { return pos0 + GQA_STAGE * (wave + 4 * i); };
-  const int nst = pos_hi > pos0 + GQA_STAGE * wave ? (pos_hi - pos0 - GQA_STAGE * wave + 4 * GQA_STAGE - 1) / (4 * GQA_STAGE) : 0;
-  // 2 KG + DB DMA instructions per group.
-  constexpr int DMA_PER_GROUP = 2 * KG + DB;
+  // 2 KG DMA instructions per group for K, 2 KG for V.
+  constexpr int DMA_PER_GROUP = 4 * KG;
   auto dma_group = [&](int j) {
     char* const kb = ring + (j % NSLOT) * SLOT;
     char* const vb = kb + KBYTES;
-    const int pos = st_pos(j >> 1) + 16 * (j & 1);
     int kshift, vshift;
-    const auto kr = group_rsrc(khead, krow_b, kpage_b, pos, 2 * D, kshift);
+    const auto kr = group_rsrc(khead, krow_b, kpage_b, j, 2 * D, kshift);
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) dma_columns_gqa<KG>(kr, kb + 8 * rb * 128, kdoff[rb] - kshift);
-    const auto vr = group_rsrc(vhead, vrow_b, vpage_b, pos, 2 * D, vshift);
-    dma_blocks_gqa<DB>(vr, vb, vdoff - vshift);
+    const auto vr = group_rsrc(vhead, vrow_b, vpage_b, j, 2 * D, vshift);
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) dma_columns_gqa<KG>(vr, vb + 8 * rb * 128, vdoff[rb] - vshift);
   };
 
   // Operand read offsets (bytes within a slot): K (A of S^T) row l32 % 16 of
   // the stage's slot l32 / 16, chunk 2 (kk % 4) + hh of column group kk / 4;
-  // V^T through ds_read_b64_tr_b16 as in the prefill kernel, keys 16 c ..
-  // +16 from the stage's slot c.
+  // V^T through ds_read_b64_tr_b16 with the prefill kernel's lane pattern
+  // (16-lane group g, lane a + 4 t': row 8 (g / 2) + t' (+ 4 for the second
+  // read), dims 16 (g % 2) + 4 a of 32-dim block db, which is half db % 2 of
+  // column group db / 2), keys 16 c .. +16 from the stage's slot c.
   const int r16 = l32 & 15;
   int krd[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) krd[s] = r16 * 128 + (((2 * s + hh) ^ ((r16 >> 1) & 7)) * 16);
   const int vg16 = lane >> 4, vi = lane & 15, va = vi & 3, vt = vi >> 2;
-  const int vrd = KBYTES + (8 * (vg16 >> 1) + vt) * 64 + (4 * (vg16 & 1) + va) * 8;
+  const int vrd = KBYTES + (8 * (vg16 >> 1) + vt) * 128 + (4 * (vg16 & 1) + va) * 8;
 
   auto compute = [&](int i) {
     const char* const slot0 = ring + ((2 * i) % NSLOT) * SLOT;
@@ -287,8 +306,8 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         const char* const vb = c ? slot1 : slot0;
-        const u32x2 lo = lds_read_tr(vb, vrd + db * VBLOCK);
-        const u32x2 hi = lds_read_tr(vb, vrd + db * VBLOCK + 4 * 64);
+        const u32x2 lo = lds_read_tr(vb, vrd + (db >> 1) * 2048 + (db & 1) * 64);
+        const u32x2 hi = lds_read_tr(vb, vrd + (db >> 1) * 2048 + (db & 1) * 64 + 4 * 128);
         o[db] = mfma32<T>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pop[c], o[db]);
       }
   };
@@ -296,7 +315,6 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   // The ring starts full; stage i waits for its two groups (the NSLOT - 2
   // later ones stay in flight), is computed, and its two slots, once its LDS
   // reads are done, take groups 2 i + NSLOT and 2 i + NSLOT + 1.
-  const int ngroups = 2 * nst;
   int issued = 0;
   for (; issued < min(NSLOT, ngroups); ++issued) dma_group(issued);
   for (int i = 0; i < nst; ++i) {
