@@ -87,9 +87,16 @@ FA_DEV void wait_dma_groups(int n) {
   }
 }
 
-template <typename T, int D, bool CAP>
+// KT: K/V storage type, T or E4M3.  E4M3 slots hold the raw K rows (16 rows
+// x D bytes, rows at sigma(r), 16-byte chunks XOR-swizzled), the raw V rows
+// (staging) and the V rows widened exactly to T (the 16-bit slot's V part):
+// K operands widen in registers after an 8-byte LDS read, V is widened in
+// LDS once per group, and the descales scale the scores and the output.
+template <typename T, int D, bool CAP, typename KT = T>
 __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_attn_args a, const int span) {
   static_assert(D == 64 || D == 128, "head dims 64 and 128");
+  constexpr bool FP8 = KT::id == FA_E4M3;
+  constexpr int EB = KT::bytes;           // bytes per K/V element
   constexpr int KSTEPS = D / 16;          // k-steps of S^T = K Q^T
   constexpr int KG = D / 64;              // 64-dim column groups of a K slot
   constexpr int DB = D / 32;              // 32-dim blocks of O^T
@@ -124,7 +131,7 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   // stores land before this wave's first DMA is issued.
   for (int i = lane; i < NSLOT * SLOT / 16; i += 64) {
     const int off = 16 * i;
-    if ((off % SLOT) >= KBYTES) *(u32x4*)(ring + off) = u32x4{0u, 0u, 0u, 0u};
+    if ((off % SLOT) >= (FP8 ? 16 * D : KBYTES)) *(u32x4*)(ring + off) = u32x4{0u, 0u, 0u, 0u};
   }
   wait_lds();
 
@@ -164,10 +171,10 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   const int P = (int)a.page_size;
   const int pos_lo = r.k_base + r.left + begin, pos_hi = r.k_base + r.left + end;   // this split's keys
   const int pos_end = r.k_base + r.left + r.k_len;                                   // the request's end
-  const uint32_t krow_b = (uint32_t)(2 * a.k_stride[1]), vrow_b = (uint32_t)(2 * a.v_stride[1]);
-  const uint32_t kpage_b = (uint32_t)(2 * a.k_stride[0]), vpage_b = (uint32_t)(2 * a.v_stride[0]);
-  const char* const khead = (const char*)a.k + 2 * (int64_t)kh * a.k_stride[2];
-  const char* const vhead = (const char*)a.v + 2 * (int64_t)kh * a.v_stride[2];
+  const uint32_t krow_b = (uint32_t)(EB * a.k_stride[1]), vrow_b = (uint32_t)(EB * a.v_stride[1]);
+  const uint32_t kpage_b = (uint32_t)(EB * a.k_stride[0]), vpage_b = (uint32_t)(EB * a.v_stride[0]);
+  const char* const khead = (const char*)a.k + EB * (int64_t)kh * a.k_stride[2];
+  const char* const vhead = (const char*)a.v + EB * (int64_t)kh * a.v_stride[2];
   const int32_t* const trow = P ? a.block_table + b * a.bt_stride[0] : nullptr;
   int kdoff[2];
 #pragma unroll
@@ -178,6 +185,19 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   int vdoff[2];
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) vdoff[rb] = (int)((8 * rb + (lane >> 3)) * vrow_b) + (lane & 7) * 16;
+  // E4M3 rows of D bytes: one instruction moves 1024 / D rows (lane p -> row
+  // 1024 / D * ib + p / NCH, 16-byte position p % NCH of NCH = D / 16); K
+  // rows hold key sigma(row) and position q holds chunk q ^ swz8(row), which
+  // spreads the 8-byte K operand reads of 16 rows over distinct bank slots.
+  constexpr int NCH = D / 16;
+  auto swz8 = [](int row) { return D == 128 ? (row >> 1) & 7 : (row >> 2) & 3; };
+  int kdoff8[KG], vdoff8[KG];
+#pragma unroll
+  for (int ib = 0; ib < KG; ++ib) {
+    const int row = (1024 / D) * ib + lane / NCH, q = lane % NCH;
+    kdoff8[ib] = (int)(sigma(row) * krow_b) + ((q ^ swz8(row)) * 16);
+    vdoff8[ib] = (int)(row * vrow_b) + q * 16;
+  }
   // Buffer descriptor of the 16-key group at storage position pos (a
   // multiple of 16), covering only its keys in [pos_lo, pos_end): the base is
   // the row of the first such key (row `first` of the group) and the size
@@ -225,20 +245,32 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
     }
     shift = __builtin_amdgcn_readfirstlane(first * (int)row_b);
     const int bytes = __builtin_amdgcn_readfirstlane(nvalid > 0 ? (nvalid - 1) * (int)row_b + row_bytes : 0);
-    return __builtin_amdgcn_make_buffer_rsrc((void*)g, (short)0, bytes, 0x00020000);
+    // The base is wave-uniform; readfirstlane states it, so the descriptor
+    // stays in scalar registers as the DMA instruction requires.
+    const uint64_t gi = (uint64_t)(uintptr_t)g;
+    const uint64_t gu = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(gi >> 32)) << 32) |
+                        (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)gi);
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)gu, (short)0, bytes, 0x00020000);
   };
-  // 2 KG DMA instructions per group for K, 2 KG for V.
-  constexpr int DMA_PER_GROUP = 4 * KG;
+  // DMA instructions per group: 2 KG each for 16-bit K and V, KG each for
+  // E4M3 K and V.
+  constexpr int DMA_PER_GROUP = FP8 ? 2 * KG : 4 * KG;
   auto dma_group = [&](int j) {
     char* const kb = ring + (j % NSLOT) * SLOT;
-    char* const vb = kb + KBYTES;
     int kshift, vshift;
-    const auto kr = group_rsrc(khead, krow_b, kpage_b, j, 2 * D, kshift);
+    const auto kr = group_rsrc(khead, krow_b, kpage_b, j, EB * D, kshift);
+    const auto vr = group_rsrc(vhead, vrow_b, vpage_b, j, EB * D, vshift);
+    if constexpr (FP8) {
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) dma_columns_gqa<KG>(kr, kb + 8 * rb * 128, kdoff[rb] - kshift);
-    const auto vr = group_rsrc(vhead, vrow_b, vpage_b, j, 2 * D, vshift);
+      for (int ib = 0; ib < KG; ++ib) dma16<0>(kr, kb + 1024 * ib, kdoff8[ib] - kshift);
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) dma_columns_gqa<KG>(vr, vb + 8 * rb * 128, vdoff[rb] - vshift);
+      for (int ib = 0; ib < KG; ++ib) dma16<0>(vr, kb + 16 * D + 1024 * ib, vdoff8[ib] - vshift);
+    } else {
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) dma_columns_gqa<KG>(kr, kb + 8 * rb * 128, kdoff[rb] - kshift);
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) dma_columns_gqa<KG>(vr, kb + KBYTES + 8 * rb * 128, vdoff[rb] - vshift);
+    }
   };
 
   // Operand read offsets (bytes within a slot): K (A of S^T) row l32 % 16 of
@@ -253,16 +285,49 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   for (int s = 0; s < 4; ++s) krd[s] = r16 * 128 + (((2 * s + hh) ^ ((r16 >> 1) & 7)) * 16);
   const int vg16 = lane >> 4, vi = lane & 15, va = vi & 3, vt = vi >> 2;
   const int vrd = KBYTES + (8 * (vg16 >> 1) + vt) * 128 + (4 * (vg16 & 1) + va) * 8;
+  // E4M3: K operand k-step kk = 8 bytes of raw row r16 (dims 16 kk + 8 hh
+  // .. +8, chunk kk at position kk ^ swz8(r16)).
+  int krd8[FP8 ? KSTEPS : 1];
+#pragma unroll
+  for (int kk = 0; kk < (FP8 ? KSTEPS : 1); ++kk) krd8[kk] = r16 * D + ((kk ^ swz8(r16)) * 16) + 8 * hh;
+  // E4M3: lane p widens raw V row p / 4, dims D / 4 * (p % 4) .. + D / 4, into
+  // the slot's 16-bit V rows.
+  const int wrow = lane >> 2, wq = lane & 3;
+  const int wsrc = 16 * D + wrow * D + (D / 4) * wq;
+  const int wdst = KBYTES + ((D / 4) * wq / 64) * KGROUP + wrow * 128 + ((D / 4) * wq % 64) * 2;
+  auto widen_v = [&](char* slot) {
+#pragma unroll
+    for (int c = 0; c < D / 64; ++c) {
+      u32x4 lo, hi;
+      widen_fp8_16<T>(*(const u32x4*)(slot + wsrc + 16 * c), lo, hi);
+      *(u32x4*)(slot + wdst + 32 * c) = lo;
+      *(u32x4*)(slot + wdst + 32 * c + 16) = hi;
+    }
+  };
 
   auto compute = [&](int i) {
-    const char* const slot0 = ring + ((2 * i) % NSLOT) * SLOT;
-    const char* const slot1 = ring + ((2 * i + 1) % NSLOT) * SLOT;
+    char* const slot0 = ring + ((2 * i) % NSLOT) * SLOT;
+    char* const slot1 = ring + ((2 * i + 1) % NSLOT) * SLOT;
+    if constexpr (FP8) {
+      widen_v(slot0);
+      widen_v(slot1);
+    }
     const char* const kb = l32 < 16 ? slot0 : slot1;
     f32x16 s;
 #pragma unroll
     for (int e = 0; e < 16; ++e) s[e] = 0.0f;
 #pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) s = mfma32<T>(lds_read16(kb, krd[kk % 4] + (kk / 4) * KGROUP), qop[kk], s);
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+      u32x4 av;
+      if constexpr (FP8) {
+        const u32x2 w = *(const u32x2*)(kb + krd8[kk]);
+        av = u32x4{widen_fp8_pair<T, false>(w[0]), widen_fp8_pair<T, true>(w[0]), widen_fp8_pair<T, false>(w[1]),
+                   widen_fp8_pair<T, true>(w[1])};
+      } else {
+        av = lds_read16(kb, krd[kk % 4] + (kk / 4) * KGROUP);
+      }
+      s = mfma32<T>(av, qop[kk], s);
+    }
     // s[e] = score of storage position st_pos(i) + 16 (e >> 3) + 8 hh + (e & 7).
     const int p0 = st_pos(i) + 8 * hh;
     float mx = -INFINITY;

@@ -1,6 +1,6 @@
 // Variants of the matrix-core GQA decode kernel (decode_gqa.h) and their
-// selection: 16-bit Q/K/V of one type, Dqk = Dv in {64, 128}, with and
-// without softcap.
+// selection: 16-bit queries over K/V of the same type or E4M3, Dqk = Dv in
+// {64, 128}, with and without softcap.
 #include "decode_gqa.h"
 
 namespace fa_decode {
@@ -10,23 +10,30 @@ namespace {
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // Every 16-byte chunk the kernel loads starts on a 16-byte boundary: row,
-// head and page strides of K/V and the query's token and head strides.
-bool chunks_aligned(const fa_attn_args& a) {
+// head and page strides of K/V (`kvb` bytes per element) and the query's
+// token and head strides.
+bool chunks_aligned(const fa_attn_args& a, int kvb) {
   if (!aligned16(a.q) || !aligned16(a.k) || !aligned16(a.v)) return false;
   if (a.q_stride[2] != 1 || a.k_stride[3] != 1 || a.v_stride[3] != 1) return false;
   for (int i = 0; i < 2; ++i)
     if ((a.q_stride[i] * 2) % 16) return false;
   for (int i = 0; i < 3; ++i)
-    if ((a.k_stride[i] * 2) % 16 || (a.v_stride[i] * 2) % 16 || a.k_stride[i] < 0 || a.v_stride[i] < 0) return false;
+    if ((a.k_stride[i] * kvb) % 16 || (a.v_stride[i] * kvb) % 16 || a.k_stride[i] < 0 || a.v_stride[i] < 0)
+      return false;
   return true;
 }
 
-template <typename T, int D>
+template <typename T, typename KT, int D>
 GqaChoice choose(bool cap) {
   GqaChoice c;
-  c.kern = cap ? fa_decode_gqa::decode_gqa_kernel<T, D, true> : fa_decode_gqa::decode_gqa_kernel<T, D, false>;
+  c.kern = cap ? fa_decode_gqa::decode_gqa_kernel<T, D, true, KT> : fa_decode_gqa::decode_gqa_kernel<T, D, false, KT>;
   c.lds = fa_decode_gqa::gqa_lds_bytes<D>();
   return c;
+}
+
+template <typename T, typename KT>
+GqaChoice choose_dim(int64_t d, bool cap) {
+  return d == 64 ? choose<T, KT, 64>(cap) : choose<T, KT, 128>(cap);
 }
 
 }  // namespace
@@ -35,18 +42,20 @@ GqaChoice pick_decode_gqa(const fa_attn_args& a) {
   const GqaChoice none{nullptr, 0};
   if (a.heads_k <= 0 || a.heads_q % a.heads_k) return none;
   if (a.heads_q / a.heads_k < DECODE_GQA_MIN_GROUP) return none;
-  if (a.q_dtype != a.k_dtype || a.k_dtype != a.v_dtype) return none;
   if (a.q_dtype != FA_BF16 && a.q_dtype != FA_F16) return none;
+  if (a.k_dtype != a.v_dtype || (a.k_dtype != a.q_dtype && a.k_dtype != FA_E4M3)) return none;
   if (a.head_dim_qk != a.head_dim_v || (a.head_dim_qk != 64 && a.head_dim_qk != 128)) return none;
   if (a.alibi || a.mask_kind != 0) return none;
   if (a.page_size && a.page_size % 16) return none;
-  if (!chunks_aligned(a)) return none;
+  const int kvb = a.k_dtype == FA_E4M3 ? 1 : 2;
+  if (!chunks_aligned(a, kvb)) return none;
   // Row and page offsets are 32-bit byte counts in the kernel's addressing.
   for (int i = 0; i < 2; ++i)
-    if (a.k_stride[i] * 2 >= (1ll << 31) / 16 || a.v_stride[i] * 2 >= (1ll << 31) / 16) return none;
-  const bool cap = a.softcap > 0.0f;
-  if (a.q_dtype == FA_BF16) return a.head_dim_qk == 64 ? choose<BF16T, 64>(cap) : choose<BF16T, 128>(cap);
-  return a.head_dim_qk == 64 ? choose<F16T, 64>(cap) : choose<F16T, 128>(cap);
+    if (a.k_stride[i] * kvb >= (1ll << 31) / 16 || a.v_stride[i] * kvb >= (1ll << 31) / 16) return none;
+  const bool cap = a.softcap > 0.0f, fp8 = a.k_dtype == FA_E4M3;
+  if (a.q_dtype == FA_BF16)
+    return fp8 ? choose_dim<BF16T, E4M3T>(a.head_dim_qk, cap) : choose_dim<BF16T, BF16T>(a.head_dim_qk, cap);
+  return fp8 ? choose_dim<F16T, E4M3T>(a.head_dim_qk, cap) : choose_dim<F16T, F16T>(a.head_dim_qk, cap);
 }
 
 }  // namespace fa_decode

@@ -61,9 +61,10 @@ def uses_gqa_kernel(p):
     (mirrors pick_decode_gqa in decode_gqa.hip, stride alignment aside, which
     only changes the split plan's workgroup estimate)."""
     page = p.k.shape[1] if p.paged else 0
-    return (p.heads // p.kv_heads >= _GQA_MIN_GROUP and p.q.dtype == p.k.dtype == p.v.dtype
-            and p.q.dtype in (torch.float16, torch.bfloat16) and p.dim_qk == p.dim_v and p.dim_qk in (64, 128)
-            and p.alibi is None and p.mask is None and page % 16 == 0)
+    return (p.heads // p.kv_heads >= _GQA_MIN_GROUP and p.q.dtype in (torch.float16, torch.bfloat16)
+            and p.k.dtype == p.v.dtype and p.k.dtype in (p.q.dtype, torch.float8_e4m3fn)
+            and p.dim_qk == p.dim_v and p.dim_qk in (64, 128) and p.alibi is None and p.mask is None
+            and page % 16 == 0)
 
 
 def workgroups_per_token(heads, kv_heads, dim_qk, dim_v, gqa=False):

@@ -1,7 +1,8 @@
 """The matrix-core decode for GQA groups of 5 or more query heads per KV head
 (csrc/decode_gqa.h) against the CPU oracle.
 
-It runs for 16-bit Q/K/V of one type at Dqk = Dv in {64, 128}: 32 head
+It runs for 16-bit queries over K/V of their type or E4M3 (with descales)
+at Dqk = Dv in {64, 128}: 32 head
 columns per workgroup (groups of 48 and 64 take two), 4 waves each streaming
 their own 32-key stages.  The cases cover the stage edges (0, 1, 31, 32, 33
 keys and long contexts), split counts, sinks, softcap, left windows, left
@@ -106,4 +107,39 @@ def test_packed_keys_explicit_scale_and_descales(device, d):
                                 cu_seqlens_k=cu_k.to(device), max_seqlen_k=max(k_lens), softmax_scale=0.125,
                                 k_descale=kd.to(device), v_descale=vd.to(device))
     ref, ref_lse = oracle_attention(q, k, v, cu_q, cu_k, scale=0.125, k_descale=kd, v_descale=vd)
+    assert_parity(got, lse, ref, ref_lse)
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(8, 1), (16, 2), (64, 2)])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("q_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("splits", [0, 3])
+def test_e4m3_caches_with_descales(device, heads, kv_heads, d, q_dtype, splits):
+    """E4M3 K/V (widened exactly to the query type in LDS / registers) with
+    per-(request, KV head) k/v descales, sinks and softcap 30; NaN-free E4M3
+    codes of N(0, 1) values, NaN-poisoned slots past each request."""
+    lengths, page = [1, 31, 33, 0, 300, 2049, 77], 16
+    g = torch.Generator().manual_seed(730 + heads + d + splits)
+    cols = max(-(-n // page) for n in lengths) + 1
+    pool = len(lengths) * cols
+    table = torch.randperm(pool, generator=g).int().reshape(len(lengths), cols)
+    kc = torch.randn(pool, page, kv_heads, d, generator=g).to(torch.float8_e4m3fn)
+    vc = torch.randn(pool, page, kv_heads, d, generator=g).to(torch.float8_e4m3fn)
+    for b, n in enumerate(lengths):
+        for pos in range(n, cols * page):
+            kc[table[b, pos // page], pos % page] = float("nan")
+            vc[table[b, pos // page], pos % page] = float("nan")
+    q = torch.randn(len(lengths), heads, d, generator=g).to(q_dtype)
+    kd = torch.rand(len(lengths), kv_heads, generator=g) * 0.1 + 0.05
+    vd = torch.rand(len(lengths), kv_heads, generator=g) * 0.25 + 0.25
+    sinks = torch.linspace(-2, 2, heads)
+    cu_q, used = torch.arange(len(lengths) + 1, dtype=torch.int32), torch.tensor(lengths, dtype=torch.int32)
+    kw = dict(cu_seqlens_q=cu_q.to(device), seqused_k=used.to(device), block_table=table.to(device),
+              s_aux=sinks.to(device), softcap=30.0, k_descale=kd.to(device), v_descale=vd.to(device))
+    p = problem(q.to(device), kc.to(device), vc.to(device), max_seqlen_q=1, max_seqlen_k=cols * page, **kw)
+    assert uses_gqa_kernel(p)
+    got, lse = decode_attention(q.to(device), kc.to(device), vc.to(device), max_seqlen_k=cols * page,
+                                num_splits=splits, **kw)
+    ref, ref_lse = oracle_attention(q, kc, vc, cu_q, used_k=used, block_table=table, sinks=sinks, softcap=30.0,
+                                    k_descale=kd, v_descale=vd)
     assert_parity(got, lse, ref, ref_lse)
