@@ -66,10 +66,13 @@ def paged_cache(ctx, page, hkv, dq, dv, dtype, device, gen, scale=None):
     return kc, vc, table.to(device)
 
 
-def test_graph_kvcache_decode_with_growing_lengths(device):
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (64, 4)])
+def test_graph_kvcache_decode_with_growing_lengths(device, hq, hkv):
+    """32/8 heads run the VALU decode kernel, 64/4 (groups of 16) the
+    matrix-core GQA decode."""
     gen = torch.Generator().manual_seed(71)
     ctx = [2900, 17, 1500, 2048, 640, 1, 3000, 999]
-    hq, hkv, d, page = 32, 8, 128, 16
+    d, page = 128, 16
     kc, vc, table = paged_cache(ctx, page, hkv, d, d, torch.bfloat16, device, gen)
     lens = torch.tensor([c - REPLAYS for c in ctx], dtype=torch.int32, device=device).clamp_(min=0)
     q = torch.randn(len(ctx), 1, hq, d, generator=gen).to(torch.bfloat16).to(device)

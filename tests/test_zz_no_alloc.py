@@ -13,8 +13,8 @@ import pytest
 import torch
 
 from flash_attn_mps_amd import _lib
-from flash_attn_mps_amd._decode import split_plan, workgroups_per_token
-from harness import kernel_args
+from flash_attn_mps_amd._decode import split_plan, uses_gqa_kernel, workgroups_per_token
+from harness import kernel_args, problem
 
 pytestmark = pytest.mark.gpu
 
@@ -65,7 +65,9 @@ def _outputs(t):
 
 def _python_plan(t):
     batch, heads, dim = t["q"].shape
-    groups = workgroups_per_token(heads, t["k"].shape[2], dim, dim)
+    p = problem(t["q"], t["k"], t["v"], cu_seqlens_q=t["cu_q"], seqused_k=t["used"], max_seqlen_q=1,
+                max_seqlen_k=t["max_ctx"], block_table=t["table"])
+    groups = workgroups_per_token(heads, t["k"].shape[2], dim, dim, uses_gqa_kernel(p))
     wl = t["window"][0]
     visible = min(t["max_ctx"], wl + 1) if wl >= 0 else t["max_ctx"]
     return split_plan(batch, groups, visible, 0)
@@ -114,6 +116,11 @@ CASES = {
     "fp8_16x8_d256_window_softcap": dict(batch=20, heads=16, kvheads=8, dim=256, max_ctx=6000,
                                          pool_pages=400, kv_dtype=torch.float8_e4m3fn,
                                          window=(4095, 0), softcap=50.0),
+    # GQA groups of 16 and 5: the matrix-core decode (bf16, and FP8 with descales).
+    "bf16_64x4_d128_gqa": dict(batch=24, heads=64, kvheads=4, dim=128, max_ctx=9000, pool_pages=700,
+                               kv_dtype=torch.bfloat16, sinks=True),
+    "fp8_40x8_d128_gqa_softcap": dict(batch=16, heads=40, kvheads=8, dim=128, max_ctx=5000, pool_pages=400,
+                                      kv_dtype=torch.float8_e4m3fn, softcap=30.0),
 }
 
 
