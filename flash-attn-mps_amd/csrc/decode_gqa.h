@@ -53,7 +53,7 @@ template <int D> constexpr int gqa_slot_bytes() { return 64 * D; }
 template <int D> constexpr int gqa_slots() { return 2; }
 template <int D> constexpr int gqa_lds_bytes() {
   const int ring = 4 * gqa_slots<D>() * gqa_slot_bytes<D>();
-  const int combine = 4 * GQA_HEADS * (D + 2) * 4;
+  const int combine = 4 * GQA_HEADS * (D + 4 + 2) * 4;
   return ring > combine ? ring : combine;
 }
 
@@ -182,9 +182,18 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
     const int drow = 8 * rb + (lane >> 3);   // row within the 16-key group
     kdoff[rb] = (int)(sigma(drow) * krow_b) + (((lane & 7) ^ ((drow >> 1) & 7)) * 16);
   }
+  // V rows (16-bit, 128 bytes): 16-byte chunk j of row r at position j ^
+  // vswz(r), which swaps the row's 64-byte halves on rows with bit 1 set, so
+  // the four rows {t, t + 1, t + 2, t + 3} (t = 0, 4, 8, 12) that one half
+  // of a transposed read touches fall on the four distinct 64-byte bank
+  // quarters (unswizzled 128-byte rows put two of them on the same quarter).
+  auto vswz = [](int row) { return 4 * ((row >> 1) & 1); };
   int vdoff[2];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) vdoff[rb] = (int)((8 * rb + (lane >> 3)) * vrow_b) + (lane & 7) * 16;
+  for (int rb = 0; rb < 2; ++rb) {
+    const int row = 8 * rb + (lane >> 3);
+    vdoff[rb] = (int)(row * vrow_b) + (((lane & 7) ^ vswz(row)) * 16);
+  }
   // E4M3 rows of D bytes: one instruction moves 1024 / D rows (lane p -> row
   // 1024 / D * ib + p / NCH, 16-byte position p % NCH of NCH = D / 16); K
   // rows hold key sigma(row) and position q holds chunk q ^ swz8(row), which
@@ -284,7 +293,9 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
 #pragma unroll
   for (int s = 0; s < 4; ++s) krd[s] = r16 * 128 + (((2 * s + hh) ^ ((r16 >> 1) & 7)) * 16);
   const int vg16 = lane >> 4, vi = lane & 15, va = vi & 3, vt = vi >> 2;
-  const int vrd = KBYTES + (8 * (vg16 >> 1) + vt) * 128 + (4 * (vg16 & 1) + va) * 8;
+  const int vrow = 8 * (vg16 >> 1) + vt;   // (+ 4 for the second read: same swizzle)
+  const int vrd0 = KBYTES + vrow * 128 + 64 * (vswz(vrow) >> 2) + (4 * (vg16 & 1) + va) * 8;   // even blocks
+  const int vrd1 = vrd0 + 64 - 128 * (vswz(vrow) >> 2);                                        // odd blocks
   // E4M3: K operand k-step kk = 8 bytes of raw row r16 (dims 16 kk + 8 hh
   // .. +8, chunk kk at position kk ^ swz8(r16)).
   int krd8[FP8 ? KSTEPS : 1];
@@ -294,7 +305,7 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   // the slot's 16-bit V rows.
   const int wrow = lane >> 2, wq = lane & 3;
   const int wsrc = 16 * D + wrow * D + (D / 4) * wq;
-  const int wdst = KBYTES + ((D / 4) * wq / 64) * KGROUP + wrow * 128 + ((D / 4) * wq % 64) * 2;
+  const int wdst = KBYTES + ((D / 4) * wq / 64) * KGROUP + wrow * 128 + ((((D / 4) * wq % 64) / 8) ^ vswz(wrow)) * 16;
   auto widen_v = [&](char* slot) {
 #pragma unroll
     for (int c = 0; c < D / 64; ++c) {
@@ -371,8 +382,9 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         const char* const vb = c ? slot1 : slot0;
-        const u32x2 lo = lds_read_tr(vb, vrd + (db >> 1) * 2048 + (db & 1) * 64);
-        const u32x2 hi = lds_read_tr(vb, vrd + (db >> 1) * 2048 + (db & 1) * 64 + 4 * 128);
+        const int vrd = ((db & 1) ? vrd1 : vrd0) + (db >> 1) * KGROUP;
+        const u32x2 lo = lds_read_tr(vb, vrd);
+        const u32x2 hi = lds_read_tr(vb, vrd + 4 * 128);
         o[db] = mfma32<T>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pop[c], o[db]);
       }
   };
@@ -395,7 +407,10 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   __syncthreads();
   float* const cm = (float*)smem;                      // [4][32]
   float* const cl = cm + 4 * GQA_HEADS;                // [4][32]
-  float* const co = cl + 4 * GQA_HEADS;                // [4][32][D]
+  // [4][32][D + 4]: the 4-float pad puts the 32 head columns' 16-byte
+  // stores of one instruction on distinct bank groups.
+  constexpr int CO_ROW = D + 4;
+  float* const co = cl + 4 * GQA_HEADS;
   if (hh == 0) {
     cm[wave * GQA_HEADS + l32] = m_run;
     cl[wave * GQA_HEADS + l32] = lt;
@@ -405,7 +420,7 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   for (int db = 0; db < DB; ++db)
 #pragma unroll
     for (int g = 0; g < 4; ++g)
-      *(float4*)(co + ((int64_t)wave * GQA_HEADS + l32) * D + 32 * db + 8 * g + 4 * hh) =
+      *(float4*)(co + ((int64_t)wave * GQA_HEADS + l32) * CO_ROW + 32 * db + 8 * g + 4 * hh) =
           float4{o[db][4 * g], o[db][4 * g + 1], o[db][4 * g + 2], o[db][4 * g + 3]};
   __syncthreads();
   for (int idx = tid; idx < nheads * D; idx += GQA_THREADS) {
@@ -419,7 +434,7 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
     for (int w = 0; w < 4; ++w) {
       const float fw = fast_exp2(cm[w * GQA_HEADS + hc] - ref);
       L += cl[w * GQA_HEADS + hc] * fw;
-      O += co[((int64_t)w * GQA_HEADS + hc) * D + d] * fw;
+      O += co[((int64_t)w * GQA_HEADS + hc) * CO_ROW + d] * fw;
     }
     const float norm = L > 0.0f ? vdsc / L : 0.0f;
     const float lse = L > 0.0f ? M * LN2 + logf(L) : -INFINITY;
