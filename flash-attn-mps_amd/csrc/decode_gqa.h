@@ -109,22 +109,29 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   char* const ring = smem + wave * NSLOT * SLOT;   // this wave's slots
 
+  // Columns: ntok = max_seqlen_q query rows (tokens) per request, nh =
+  // 32 / ntok query heads per workgroup; column c is head h0 + c / ntok,
+  // token c % ntok (one token: column c = head h0 + c).  A request's tokens
+  // are its last q_len key positions.
   // Grid: x = KV head * head tiles + tile, y = split, z = request.
+  const int ntok = a.max_seqlen_q > 1 ? (int)a.max_seqlen_q : 1, nh = GQA_HEADS / ntok;
   const int group = (int)(a.heads_q / a.heads_k);
-  const int tiles = (group + GQA_HEADS - 1) / GQA_HEADS;
-  const int kh = blockIdx.x / tiles, t0 = (blockIdx.x % tiles) * GQA_HEADS;
-  const int nheads = min(GQA_HEADS, group - t0);
+  const int tiles = (group + nh - 1) / nh;
+  const int kh = blockIdx.x / tiles, t0 = (blockIdx.x % tiles) * nh;
+  const int nheads = min(nh, group - t0);
   const int h0 = kh * group + t0;
   const int split = blockIdx.y;
   const int64_t b = blockIdx.z;
   const RequestInfo r = load_request(a, b);
-  if (r.q_len != 1) return;
-  const int vis_begin = fa_decode::decode_vis_begin(a, r.k_len);
+  if (r.q_len < 1 || r.q_len > ntok) return;
+  const int vis_begin = fa_decode::decode_vis_begin(a, r.k_len, r.q_len);
   const int begin = vis_begin + split * span;
   const int end = min(r.k_len, begin + span);
   if (split > 0 && begin >= end) return;
   const int S = a.num_splits;
-  const int64_t tq = r.q_begin;
+  // This lane's column.
+  const int chead = l32 / ntok, ctok = l32 - chead * ntok;
+  const bool col_ok = chead < nheads && ctok < r.q_len;
 
   // Zeroed V buffers: rows the DMA does not write (past the request) then
   // hold finite values, which a zero probability keeps out of O.  The
@@ -135,14 +142,15 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   }
   wait_lds();
 
-  // Q^T operands: k-step kk, lane (l32, hh) holds head h0 + l32, dims 16 kk +
-  // 8 hh .. +8 (zeros for columns past the group).
+  // Q^T operands: k-step kk, lane (l32, hh) holds its column's query
+  // (token ctok, head h0 + chead), dims 16 kk + 8 hh .. +8 (zeros for
+  // columns past the group or the request's tokens).
   u32x4 qop[KSTEPS];
   {
-    const bool ok = l32 < nheads;
-    const uint16_t* qp = (const uint16_t*)a.q + tq * a.q_stride[0] + (int64_t)(h0 + (ok ? l32 : 0)) * a.q_stride[1] + 8 * hh;
+    const uint16_t* qp = (const uint16_t*)a.q + (int64_t)(r.q_begin + (col_ok ? ctok : 0)) * a.q_stride[0] +
+                         (int64_t)(h0 + (col_ok ? chead : 0)) * a.q_stride[1] + 8 * hh;
 #pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) qop[kk] = ok ? *(const u32x4*)(qp + 16 * kk) : u32x4{0u, 0u, 0u, 0u};
+    for (int kk = 0; kk < KSTEPS; ++kk) qop[kk] = col_ok ? *(const u32x4*)(qp + 16 * kk) : u32x4{0u, 0u, 0u, 0u};
   }
 
   const float kdsc = descale_of(a.q_descale, a.q_descale_stride, b, kh) * descale_of(a.k_descale, a.k_descale_stride, b, kh);
@@ -152,7 +160,7 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   const float cap_out = a.softcap * LOG2E;
   // A sink logit seeds the state of one wave of split 0 (max = sink, sum = 1).
   const bool seed = a.sinks && split == 0 && wave == 0;
-  float m_run = seed && l32 < nheads ? a.sinks[(int64_t)(h0 + l32) * a.sink_stride] * LOG2E : -INFINITY;
+  float m_run = seed && col_ok ? a.sinks[(int64_t)(h0 + chead) * a.sink_stride] * LOG2E : -INFINITY;
   float l_run = seed && hh == 0 ? 1.0f : 0.0f;
   f32x16 o[DB];
 #pragma unroll
@@ -170,6 +178,20 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   // row 8 rb + p / 8, chunk p % 8).
   const int P = (int)a.page_size;
   const int pos_lo = r.k_base + r.left + begin, pos_hi = r.k_base + r.left + end;   // this split's keys
+  // Keys this lane's column sees, as storage positions [col_lo, col_hi):
+  // the split's, clipped to the token's window (left: position - WL; right:
+  // the position itself when causal, + WR with a right window); none for
+  // columns without a query.
+  int col_lo = INT_MAX, col_hi = INT_MIN;
+  if (col_ok) {
+    const int qpos = r.k_len - r.q_len + ctok;
+    int hi = r.k_len;
+    if (r.causal) hi = qpos + 1;
+    else if (a.window_right >= 0) hi = min(hi, qpos + a.window_right + 1);
+    const int lo = a.window_left >= 0 ? max(qpos - a.window_left, 0) : 0;
+    col_lo = max(pos_lo, r.k_base + r.left + lo);
+    col_hi = min(pos_hi, r.k_base + r.left + hi);
+  }
   const int pos_end = r.k_base + r.left + r.k_len;                                   // the request's end
   const uint32_t krow_b = (uint32_t)(EB * a.k_stride[1]), vrow_b = (uint32_t)(EB * a.v_stride[1]);
   const uint32_t kpage_b = (uint32_t)(EB * a.k_stride[0]), vpage_b = (uint32_t)(EB * a.v_stride[0]);
@@ -348,7 +370,7 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
       if constexpr (CAP) v = cap_out * (1.0f - 2.0f * __builtin_amdgcn_rcpf(fast_exp2(cap_in * v) + 1.0f));
       else v *= c_scale;
       const int pos = p0 + 16 * (e >> 3) + (e & 7);
-      v = (pos >= pos_lo && pos < pos_hi) ? v : -INFINITY;
+      v = (pos >= col_lo && pos < col_hi) ? v : -INFINITY;
       s[e] = v;
       mx = fmaxf(mx, v);
     }
@@ -423,8 +445,10 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
       *(float4*)(co + ((int64_t)wave * GQA_HEADS + l32) * CO_ROW + 32 * db + 8 * g + 4 * hh) =
           float4{o[db][4 * g], o[db][4 * g + 1], o[db][4 * g + 2], o[db][4 * g + 3]};
   __syncthreads();
-  for (int idx = tid; idx < nheads * D; idx += GQA_THREADS) {
-    const int hc = idx / D, d = idx - hc * D;
+  for (int idx = tid; idx < nh * ntok * D; idx += GQA_THREADS) {
+    const int hc = idx / D, d = idx - hc * D;   // column hc: head h0 + hc / ntok, token hc % ntok
+    const int th = hc / ntok, tt = hc - th * ntok;
+    if (th >= nheads || tt >= r.q_len) continue;
     float M = cm[hc];
 #pragma unroll
     for (int w = 1; w < 4; ++w) M = fmaxf(M, cm[w * GQA_HEADS + hc]);
@@ -438,13 +462,15 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
     }
     const float norm = L > 0.0f ? vdsc / L : 0.0f;
     const float lse = L > 0.0f ? M * LN2 + logf(L) : -INFINITY;
-    const int h = h0 + hc;
+    const int h = h0 + th;
+    const int64_t tq = r.q_begin + tt;
     if (S == 1) {
       store_any(a.out, tq * a.out_stride[0] + (int64_t)h * a.out_stride[1] + (int64_t)d * a.out_stride[2], a.out_dtype,
                 O * norm);
       if (d == 0) a.lse[(int64_t)h * a.lse_stride[0] + tq * a.lse_stride[1]] = lse;
     } else {
-      const int64_t row = (b * a.heads_q + h) * S + split;
+      // Partial rows [batch][ntok][Hq][S] (one token: [batch][Hq][S]).
+      const int64_t row = ((b * ntok + tt) * a.heads_q + h) * S + split;
       a.partial_out[row * D + d] = O * norm;
       if (d == 0) a.partial_lse[row] = lse;
     }

@@ -41,7 +41,11 @@ GqaChoice choose_dim(int64_t d, bool cap) {
 GqaChoice pick_decode_gqa(const fa_attn_args& a) {
   const GqaChoice none{nullptr, 0};
   if (a.heads_k <= 0 || a.heads_q % a.heads_k) return none;
-  if (a.heads_q / a.heads_k < DECODE_GQA_MIN_GROUP) return none;
+  // One query row per request: groups of DECODE_GQA_MIN_GROUP or more (the
+  // VALU kernel is faster below); 2..DECODE_GQA_MAX_ROWS rows: any group
+  // (nothing else runs a few rows per request as decode).
+  if (a.max_seqlen_q > DECODE_GQA_MAX_ROWS) return none;
+  if (a.max_seqlen_q <= 1 && a.heads_q / a.heads_k < DECODE_GQA_MIN_GROUP) return none;
   if (a.q_dtype != FA_BF16 && a.q_dtype != FA_F16) return none;
   if (a.k_dtype != a.v_dtype || (a.k_dtype != a.q_dtype && a.k_dtype != FA_E4M3)) return none;
   if (a.head_dim_qk != a.head_dim_v || (a.head_dim_qk != 64 && a.head_dim_qk != 128)) return none;

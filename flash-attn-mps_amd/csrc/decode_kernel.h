@@ -195,8 +195,10 @@ FA_DEV uint32_t pack_pair_bits(float lo, float hi) {
   else return (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
 }
 
-FA_DEV int decode_vis_begin(const fa_attn_args& a, int k_len) {
-  return a.window_left >= 0 ? max(0, k_len - a.window_left - 1) : 0;
+// First key any of a request's q_len query rows sees (the rows are the last
+// q_len positions; a left window starts at the first row's position - WL).
+FA_DEV int decode_vis_begin(const fa_attn_args& a, int k_len, int q_len = 1) {
+  return a.window_left >= 0 ? max(0, k_len - q_len - a.window_left) : 0;
 }
 
 // D / DV: the tile's head dims; DT / DVT <= them: the tensors' own.  Lanes
@@ -636,6 +638,9 @@ DecodeKernel pick_decode_fp8_f16(int64_t d, int64_t dv, int gt, bool cap, bool a
 // or a null kernel when the arguments need the VALU kernel.  Its workgroups
 // take 32 query heads of one KV head each.
 constexpr int DECODE_GQA_MIN_GROUP = 5;
+// Most query rows per request the matrix-core decode takes (its 32 columns
+// hold 32 / rows query heads).
+constexpr int DECODE_GQA_MAX_ROWS = 16;
 struct GqaChoice {
   DecodeKernel kern;
   size_t lds;

@@ -17,24 +17,30 @@ namespace {
 
 using namespace fa_decode;
 
-// One wavefront merges the valid splits of one (request, head) row into the
-// caller's output.  Splits past the request's last key were never written.
+// One wavefront merges the valid splits of one (request, token, head) row
+// into the caller's output.  Splits past the request's last key were never
+// written.
 // Split weights exp(lse_s - max) are computed once, 64 splits at a time (split
 // s0 + j on lane j), and broadcast with readlane; every lane accumulates the
 // dims lane, lane + 64, ... so each partial row is one coalesced read.
 constexpr int MERGE_DIMS = 256 / 64;   // dims per lane: the decode kernels cover Dv <= 256
 constexpr int MERGE_GROUP = 8;         // splits whose loads are in flight together
 
+// Rows are (request, token, head) with max_seqlen_q tokens per request (the
+// multi-token GQA decode) or one; rows past a request's tokens, and requests
+// with more tokens than that, do nothing.
 __global__ __launch_bounds__(256) void decode_merge_kernel(const fa_attn_args a, const int span) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int ntok = a.max_seqlen_q > 1 ? (int)a.max_seqlen_q : 1;
   const int64_t row = (int64_t)blockIdx.x * 4 + wave;
-  if (row >= a.batch * a.heads_q) return;
-  const int64_t b = row / a.heads_q, h = row - b * a.heads_q;
+  if (row >= a.batch * ntok * a.heads_q) return;
+  const int64_t b = row / (ntok * a.heads_q), bt = row / a.heads_q, h = row - bt * a.heads_q;
+  const int t = (int)(bt - b * ntok);
   const RequestInfo r = load_request(a, b);
-  if (r.q_len != 1) return;
+  if (r.q_len < 1 || r.q_len > ntok || t >= r.q_len) return;   // the decode kernel skipped the request
   const int S = a.num_splits;
   const int DV = (int)a.head_dim_v;
-  const int n = r.k_len - decode_vis_begin(a, r.k_len);
+  const int n = r.k_len - decode_vis_begin(a, r.k_len, r.q_len);
   const int nv = n > 0 ? min(S, (n + span - 1) / span) : 1;
   const float* plse = a.partial_lse + row * S;
   const float* po = a.partial_out + row * S * DV;
@@ -80,7 +86,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const fa_attn_args a,
     }
   }
   denom = wave_sum(denom);
-  const int64_t tq = r.q_begin;
+  const int64_t tq = r.q_begin + t;
   const float inv = denom > 0.0f ? 1.0f / denom : 0.0f;
 #pragma unroll
   for (int k = 0; k < MERGE_DIMS; ++k) {
@@ -98,7 +104,8 @@ int elem_size(int dt) { return dt == FA_F32 ? 4 : dt == FA_E4M3 ? 1 : 2; }
 // (the query sits at the last key, so it sees window_left + 1 keys).
 int64_t decode_visible_max(const fa_attn_args& a) {
   const int64_t m = a.max_seqlen_k > 0 ? a.max_seqlen_k : 0;
-  return a.window_left >= 0 && a.window_left + 1 < m ? a.window_left + 1 : m;
+  const int64_t q = a.max_seqlen_q > 1 ? a.max_seqlen_q : 1;   // the first row sees window_left + q keys
+  return a.window_left >= 0 && a.window_left + q < m ? a.window_left + q : m;
 }
 
 // Query heads per workgroup (GT).  Every workgroup of a KV head reads it
@@ -128,6 +135,7 @@ bool chunk_aligned(const void* p, const int64_t* st, int nstrides, int esz, int 
 }
 
 DecodeKernel select_decode(const fa_attn_args& a, int* gt_out) {
+  if (a.max_seqlen_q > 1) return nullptr;   // one query row per request
   if (a.k_dtype != a.v_dtype) return nullptr;
   if (a.mask_kind != 0) return nullptr;
   if (a.page_size && a.page_size % DEC_PAGE_ALIGN) return nullptr;
@@ -162,10 +170,12 @@ DecodeKernel select_decode(const fa_attn_args& a, int* gt_out) {
 }
 
 // Workgroups per (request, split): KV heads x head tiles of the kernel that
-// runs (32 query heads for the matrix-core GQA kernel, GT for the VALU one).
+// runs (32 / max_seqlen_q query heads for the matrix-core GQA kernel, GT for
+// the VALU one).
 int64_t decode_head_groups(const fa_attn_args& a, int gt) {
   const int64_t group = a.heads_q / a.heads_k;
-  const int tile = pick_decode_gqa(a).kern ? 32 : gt;
+  const int64_t ntok = a.max_seqlen_q > 1 ? a.max_seqlen_q : 1;
+  const int64_t tile = pick_decode_gqa(a).kern ? 32 / ntok : gt;
   return a.heads_k * fa_ceil_div(group, tile);
 }
 
@@ -179,6 +189,11 @@ extern "C" int fa_decode_supported(const fa_attn_args* a) {
 }
 
 namespace {
+
+// Partial rows: [batch][max_seqlen_q][Hq] (x [splits][Dv] and x [splits]).
+int64_t partial_rows(const fa_attn_args& a) {
+  return a.batch * (a.max_seqlen_q > 1 ? a.max_seqlen_q : 1) * a.heads_q;
+}
 
 // Launch the decode kernel (and the merge when there are several splits) for
 // arguments that passed fa_validate_attn.
@@ -212,18 +227,18 @@ int decode_launch(const fa_attn_args* a, void* stream, const char* who) {
   hipLaunchKernelGGL(kern, grid, dim3(DEC_THREADS), gqa.kern ? gqa.lds : 0, s, *a, (int)a->split_span);
   int rc = fa_check_launch(who);
   if (rc || a->num_splits == 1) return rc;
-  const int64_t rows = a->batch * a->heads_q;
+  const int64_t rows = partial_rows(*a);
   hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)fa_ceil_div(rows, 4)), dim3(256), 0, s, *a, (int)a->split_span);
   return fa_check_launch(who);
 }
 
 // Floats of the partial rows; the LSE rows start at the next 256-byte boundary.
 int64_t partial_out_floats(const fa_attn_args& a, int64_t splits) {
-  return fa_ceil_div(a.batch * a.heads_q * splits * a.head_dim_v, 64) * 64;
+  return fa_ceil_div(partial_rows(a) * splits * a.head_dim_v, 64) * 64;
 }
 
 int64_t partial_floats(const fa_attn_args& a, int64_t splits) {
-  return partial_out_floats(a, splits) + a.batch * a.heads_q * splits;
+  return partial_out_floats(a, splits) + partial_rows(a) * splits;
 }
 
 // The split plan of the Python host layer (flash_attn_mps_amd/_decode.py

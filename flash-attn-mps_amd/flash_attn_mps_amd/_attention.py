@@ -160,10 +160,11 @@ def _mixed_batch(p, a):
     Returns False (nothing launched) when the decode kernel cannot take the
     single-query rows."""
     dec = _lib.AttnArgs.from_buffer_copy(a)
+    dec.max_seqlen_q = 1   # the decode kernel takes the one-row requests only
     if not _lib.supported("fa_decode_supported", dec):
         return False
     from ._decode import split_plan, uses_gqa_kernel, workgroups_per_token
-    groups = workgroups_per_token(p.heads, p.kv_heads, p.dim_qk, p.dim_v, uses_gqa_kernel(p))
+    groups = workgroups_per_token(p.heads, p.kv_heads, p.dim_qk, p.dim_v, uses_gqa_kernel(p, 1))
     splits, span = split_plan(p.batch, groups, p.max_k, 0)
     dec.num_splits, dec.split_span = splits, span
     if splits > 1:
@@ -193,6 +194,13 @@ def solve(p):
     if p.max_q == 1 and not p.deterministic and p.mask is None:
         from ._decode import decode
         return decode(p, out)
+    if p.max_q > 1 and not p.deterministic and p.mask is None:
+        # A few query rows per request (speculative / multi-token decode):
+        # the matrix-core decode with (head, row) columns when it takes them.
+        from ._decode import decode_rows
+        done = decode_rows(p, out)
+        if done is not None:
+            return done
     lse = torch.empty((p.heads, p.tokens), device=p.device, dtype=torch.float32)
     a = build_args(p, out, lse)
     if _fits_prefill(p, out) and _lib.supported("fa_prefill_supported", a):

@@ -50,47 +50,46 @@ def group_tile(heads, kv_heads, dim_qk, dim_v):
     return tile
 
 
-# Query heads per KV head from which the matrix-core GQA decode kernel runs
-# (DECODE_GQA_MIN_GROUP in decode_kernel.h); its workgroups take 32 heads.
+# The matrix-core decode (decode_gqa.h): one query row per request from
+# DECODE_GQA_MIN_GROUP query heads per KV head, or 2..DECODE_GQA_MAX_ROWS rows
+# per request with any group (decode_kernel.h); its workgroups take 32 columns,
+# i.e. 32 // rows query heads.
 _GQA_MIN_GROUP = 5
-_GQA_TILE = 32
+_GQA_MAX_ROWS = 16
 
 
-def uses_gqa_kernel(p):
-    """Whether fa_decode_fwd runs Problem `p` on the matrix-core GQA kernel
-    (mirrors pick_decode_gqa in decode_gqa.hip, stride alignment aside, which
-    only changes the split plan's workgroup estimate)."""
+def uses_gqa_kernel(p, rows=None):
+    """Whether fa_decode_fwd runs Problem `p` with `rows` query rows per
+    request (default p.max_q) on the matrix-core GQA kernel (mirrors
+    pick_decode_gqa in decode_gqa.hip, stride alignment aside, which only
+    changes the split plan's workgroup estimate)."""
     page = p.k.shape[1] if p.paged else 0
-    return (p.heads // p.kv_heads >= _GQA_MIN_GROUP and p.q.dtype in (torch.float16, torch.bfloat16)
+    rows = p.max_q if rows is None else rows
+    rows_ok = (p.heads // p.kv_heads >= _GQA_MIN_GROUP) if rows <= 1 else rows <= _GQA_MAX_ROWS
+    return (rows_ok and p.q.dtype in (torch.float16, torch.bfloat16)
             and p.k.dtype == p.v.dtype and p.k.dtype in (p.q.dtype, torch.float8_e4m3fn)
             and p.dim_qk == p.dim_v and p.dim_qk in (64, 128) and p.alibi is None and p.mask is None
             and page % 16 == 0)
 
 
-def workgroups_per_token(heads, kv_heads, dim_qk, dim_v, gqa=False):
+def workgroups_per_token(heads, kv_heads, dim_qk, dim_v, gqa=False, rows=1):
     """Decode workgroups per (request, split): KV heads x ceil(group / tile)."""
-    tile = _GQA_TILE if gqa else group_tile(heads, kv_heads, dim_qk, dim_v)
+    tile = 32 // max(rows, 1) if gqa else group_tile(heads, kv_heads, dim_qk, dim_v)
     return kv_heads * -(-(heads // kv_heads) // tile)
 
 
 def decode(p, out):
     """One query per request of Problem `p` (cu_seqlens_q steps of 0 or 1).
 
-    Returns (out, lse).  The split-KV kernel handles 16-bit queries over
-    16-bit or FP8 caches at its compiled head dims; other dtype/dim/stride
+    Returns (out, lse).  The split-KV kernels handle 16-bit queries over
+    16-bit or FP8 caches at their compiled head dims; other dtype/dim/stride
     combinations run the generic kernel with the reference's split rule
     (_decode.py:63-64).
     """
     lse = torch.empty((p.heads, p.tokens), dtype=torch.float32, device=p.device)
     a = build_args(p, out, lse, max_q=1)
     a.causal, a.causal_by_batch = 0, None   # a right-aligned single query has no future keys
-    if _lib.supported("fa_decode_supported", a):
-        groups = workgroups_per_token(p.heads, p.kv_heads, p.dim_qk, p.dim_v, uses_gqa_kernel(p))
-        splits, span = split_plan(p.batch, groups, p.visible_max, p.splits)
-        a.num_splits, a.split_span = splits, span
-        if splits > 1:
-            _partials(p, a, (p.batch, p.heads, splits, p.dim_v), (p.batch, p.heads, splits))
-        _lib.call("fa_decode_fwd", a, p.device)
+    if _run_split_kv(p, a, 1):
         return out, lse
     splits = p.splits or max(1, min(32, -(-p.visible_max // 256)))
     if splits > 1:
@@ -98,3 +97,32 @@ def decode(p, out):
     a.num_splits = splits
     _lib.call("fa_attn_fwd", a, p.device)
     return out, lse
+
+
+def decode_rows(p, out):
+    """2..16 query rows per request (speculative / multi-token decode): the
+    matrix-core decode with (head, row) columns, split over the keys like the
+    one-row decode.  Each request's rows are its last key positions.  Returns
+    (out, lse), or None (nothing launched) when the kernel does not take the
+    arguments."""
+    if not uses_gqa_kernel(p):
+        return None
+    lse = torch.empty((p.heads, p.tokens), dtype=torch.float32, device=p.device)
+    a = build_args(p, out, lse)
+    return (out, lse) if _run_split_kv(p, a, p.max_q) else None
+
+
+def _run_split_kv(p, a, rows):
+    """fa_decode_fwd with the split plan and partials [batch][rows][Hq][S];
+    False when the decode kernels do not take the arguments."""
+    if not _lib.supported("fa_decode_supported", a):
+        return False
+    groups = workgroups_per_token(p.heads, p.kv_heads, p.dim_qk, p.dim_v, uses_gqa_kernel(p, rows), rows)
+    left = p.window[0]
+    visible = min(p.max_k, left + rows) if left >= 0 else p.max_k   # the first row's window
+    splits, span = split_plan(p.batch, groups, visible, p.splits)
+    a.num_splits, a.split_span = splits, span
+    if splits > 1:
+        _partials(p, a, (p.batch, rows, p.heads, splits, p.dim_v), (p.batch, rows, p.heads, splits))
+    _lib.call("fa_decode_fwd", a, p.device)
+    return True

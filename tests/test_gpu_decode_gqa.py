@@ -10,12 +10,16 @@ padding whose slots hold NaN (rows before a split's first key must never be
 read), NaN-poisoned slots past each request, packed and paged K/V (pages of
 16 and 48 tokens) and sentinels around a caller-owned output.  Parity bar:
 fp16 2e-3, bf16 1e-2, LSE 1e-4 max-abs.
+
+The same kernel takes 2-16 query rows per request (speculative decode) with
+any group: 32 (head, row) columns per workgroup, each column with its own
+causal/window key range.
 """
 import pytest
 import torch
 
 from flash_attn_mps_amd import _lib
-from flash_attn_mps_amd._decode import uses_gqa_kernel
+from flash_attn_mps_amd._decode import decode_rows, uses_gqa_kernel
 from harness import assert_parity, decode_attention, kernel_args, oracle_attention, problem
 
 pytestmark = pytest.mark.gpu
@@ -141,5 +145,91 @@ def test_e4m3_caches_with_descales(device, heads, kv_heads, d, q_dtype, splits):
     got, lse = decode_attention(q.to(device), kc.to(device), vc.to(device), max_seqlen_k=cols * page,
                                 num_splits=splits, **kw)
     ref, ref_lse = oracle_attention(q, kc, vc, cu_q, used_k=used, block_table=table, sinks=sinks, softcap=30.0,
+                                    k_descale=kd, v_descale=vd)
+    assert_parity(got, lse, ref, ref_lse)
+
+
+def _rows_call(q, kc, vc, q_lens, *, max_seqlen_k, **kw):
+    """The multi-row decode (decode_rows) of requests with q_lens query rows;
+    fails if the matrix-core kernel does not take the call."""
+    device = q.device
+    cu_q = torch.tensor([0] + list(torch.tensor(q_lens).cumsum(0)), dtype=torch.int32, device=device)
+    p = problem(q, kc, vc, cu_seqlens_q=cu_q, max_seqlen_q=max(q_lens), max_seqlen_k=max_seqlen_k, **kw).validate()
+    assert uses_gqa_kernel(p)
+    out = torch.empty((p.tokens, p.heads, p.dim_v), dtype=p.output_dtype, device=device)
+    done = decode_rows(p, out)
+    assert done is not None, "the matrix-core decode did not take the call"
+    return done, cu_q.cpu()
+
+
+@pytest.mark.parametrize("q_lens", [[2, 1, 2, 0, 2], [4, 3, 1, 4, 2], [8, 8, 5, 1, 7], [16, 9, 1, 16]])
+@pytest.mark.parametrize("heads,kv_heads", [(8, 8), (32, 8), (16, 1), (40, 4)])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("splits", [0, 1, 3])
+def test_rows_per_request(device, q_lens, heads, kv_heads, causal, splits):
+    """2-16 query rows per request at the end of each context (speculative
+    decode): rows of one request see bottom-right-aligned causal prefixes (or
+    every key), requests have fewer rows than max_seqlen_q or none, and
+    contexts run 0-2049 keys (a causal row may see no key at all)."""
+    d = 128
+    lengths = [max(n, 1) + x for n, x in zip(q_lens, [0, 40, 2000, 7, 300, 33])]
+    lengths[0] = q_lens[0] - 1 if q_lens[0] > 1 else 0   # fewer keys than rows
+    page = 16
+    kc, vc, table, cols = _pool(lengths, page, kv_heads, d, torch.bfloat16, device, 740 + heads + splits,
+                                [0] * len(lengths))
+    g = torch.Generator().manual_seed(741 + sum(q_lens))
+    q = torch.randn(sum(q_lens), heads, d, generator=g).to(torch.bfloat16).to(device)
+    used = _i32(lengths, device)
+    sinks = torch.linspace(-2, 2, heads, device=device)
+    kw = dict(seqused_k=used, block_table=table, s_aux=sinks, causal=causal, num_splits=splits)
+    (got, lse), cu_q = _rows_call(q, kc, vc, q_lens, max_seqlen_k=cols * page, **kw)
+    ref, ref_lse = oracle_attention(q, kc, vc, cu_q, used_k=used, block_table=table, sinks=sinks, causal=causal)
+    assert_parity(got, lse, ref, ref_lse)
+
+
+@pytest.mark.parametrize("window", [(0, 0), (45, 0), (20, 3), (1000, -1)])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("splits", [0, 2])
+def test_rows_windows_softcap_leftpad(device, window, d, splits):
+    """Multi-row decode with left/right windows (each row's own window),
+    softcap 30, descales of a 16-bit cache and NaN left padding."""
+    q_lens, left = [3, 4, 1, 4, 2], [0, 5, 17, 3, 16]
+    lengths = [3, 40, 777, 1500, 33]
+    stored = [n + p for n, p in zip(lengths, left)]
+    heads, kv_heads = 16, 4
+    kc, vc, table, cols = _pool(stored, 48, kv_heads, d, torch.float16, device, 750 + d + splits, left)
+    g = torch.Generator().manual_seed(751 + d)
+    q = torch.randn(sum(q_lens), heads, d, generator=g).to(torch.float16).to(device)
+    kd = torch.rand(len(q_lens), kv_heads, generator=g) * 0.5 + 0.75
+    vd = torch.rand(len(q_lens), kv_heads, generator=g) * 0.5 + 0.5
+    used, pads = _i32(lengths, device), _i32(left, device)
+    kw = dict(seqused_k=used, block_table=table, leftpad_k=pads, window_size=window, causal=window[1] == 0,
+              softcap=30.0, k_descale=kd.to(device), v_descale=vd.to(device), num_splits=splits)
+    (got, lse), cu_q = _rows_call(q, kc, vc, q_lens, max_seqlen_k=cols * 48, **kw)
+    ref, ref_lse = oracle_attention(q, kc, vc, cu_q, used_k=used, block_table=table, leftpad=left, window=window,
+                                    causal=window[1] == 0, softcap=30.0, k_descale=kd, v_descale=vd)
+    assert_parity(got, lse, ref, ref_lse)
+
+
+@pytest.mark.parametrize("q_lens", [[2, 2, 1], [5, 8, 3]])
+@pytest.mark.parametrize("q_dtype", [torch.bfloat16, torch.float16])
+def test_rows_e4m3_cache(device, q_lens, q_dtype):
+    """Multi-row decode over an E4M3 paged cache with descales and sinks."""
+    heads, kv_heads, d, page = 32, 8, 128, 16
+    lengths = [300, 2049, 77]
+    g = torch.Generator().manual_seed(760 + sum(q_lens))
+    cols = max(-(-n // page) for n in lengths) + 1
+    table = torch.randperm(len(lengths) * cols, generator=g).int().reshape(len(lengths), cols)
+    kc = torch.randn(len(lengths) * cols, page, kv_heads, d, generator=g).to(torch.float8_e4m3fn)
+    vc = torch.randn(len(lengths) * cols, page, kv_heads, d, generator=g).to(torch.float8_e4m3fn)
+    q = torch.randn(sum(q_lens), heads, d, generator=g).to(q_dtype)
+    kd = torch.rand(len(lengths), kv_heads, generator=g) * 0.1 + 0.05
+    vd = torch.rand(len(lengths), kv_heads, generator=g) * 0.25 + 0.25
+    sinks = torch.linspace(-2, 2, heads)
+    used = torch.tensor(lengths, dtype=torch.int32)
+    kw = dict(seqused_k=used.to(device), block_table=table.to(device), s_aux=sinks.to(device), causal=True,
+              k_descale=kd.to(device), v_descale=vd.to(device))
+    (got, lse), cu_q = _rows_call(q.to(device), kc.to(device), vc.to(device), q_lens, max_seqlen_k=cols * page, **kw)
+    ref, ref_lse = oracle_attention(q, kc, vc, cu_q, used_k=used, block_table=table, sinks=sinks, causal=True,
                                     k_descale=kd, v_descale=vd)
     assert_parity(got, lse, ref, ref_lse)
