@@ -160,11 +160,12 @@ typedef struct fa_attn_args {
   int32_t split_span;                /* fa_decode_fwd: keys per split (>= 1); the splits
                                         must cover every visible key:
                                         num_splits * split_span >= min(max_seqlen_k,
-                                        window_left + 1) (window_left < 0: max_seqlen_k) */
+                                        window_left + R) (window_left < 0: max_seqlen_k),
+                                        R = max(1, max_seqlen_q) */
   float* partial_out;                /* num_splits > 1: caller-owned fp32 workspace,
-                                        fa_decode_fwd [batch, Hq, S, Dv] contiguous,
+                                        fa_decode_fwd [batch, R, Hq, S, Dv] contiguous,
                                         fa_attn_fwd [S, total_q, Hq, Dv] contiguous */
-  float* partial_lse;                /* fa_decode_fwd [batch, Hq, S], fa_attn_fwd [S, Hq, total_q] */
+  float* partial_lse;                /* fa_decode_fwd [batch, R, Hq, S], fa_attn_fwd [S, Hq, total_q] */
 
   int32_t flags;                     /* FA_FLAG_* bits */
   int32_t _pad1;
@@ -207,9 +208,16 @@ int fa_store_kvcache(const fa_store_args* args, void* stream);
 int fa_append_kvcache(const fa_append_args* args, void* stream);
 int fa_rotary(const fa_rotary_args* args, void* stream);
 
-/* Single-query split-KV decode (rows with cu_seqlens_q difference 1; others
- * are skipped).  Writes out/lse directly when num_splits == 1, otherwise
- * fills partial_out [batch, Hq, S, Dv] / partial_lse [batch, Hq, S] and merges. */
+/* Split-KV decode.  With max_seqlen_q <= 1: one query row per request (rows
+ * with cu_seqlens_q difference 1; others are skipped).  With max_seqlen_q = R
+ * in 2..16 (speculative / multi-token decode; no counterpart in the
+ * reference, which runs such rows through its prefill kernel): requests of
+ * 1..R rows, the rows being the request's last key positions (causal and
+ * windows bottom-right aligned), on the matrix-core kernel only --
+ * fa_decode_supported says whether it takes the arguments.  Writes out/lse
+ * directly when num_splits == 1, otherwise fills partial_out
+ * [batch, R, Hq, S, Dv] / partial_lse [batch, R, Hq, S] (R = 1 for one row)
+ * and merges. */
 int fa_decode_supported(const fa_attn_args* args);
 int fa_decode_fwd(const fa_attn_args* args, void* stream);
 
@@ -223,7 +231,7 @@ int fa_decode_fwd(const fa_attn_args* args, void* stream);
  * workgroups -- the plan of the Python host layer -- then the split count is
  * reduced until the partials fit; one split needs none); otherwise the
  * caller's num_splits/split_span are used and
- * batch * Hq * num_splits * (Dv + 1) * 4 bytes must fit, else FA_ERR_INVALID.
+ * batch * R * Hq * num_splits * (Dv + 1) * 4 bytes must fit, else FA_ERR_INVALID.
  * Every call on one GPU shares that GPU's array and the array keeps the last
  * call's partials (nothing in it needs clearing: each split writes its own
  * rows before the merge reads them); calls that overlap in time on one GPU

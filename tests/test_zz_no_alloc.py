@@ -176,3 +176,32 @@ def test_noalloc_rejects_plans_that_do_not_fit_and_caller_buffers(device):
     a.partial_out = a.partial_lse = out.data_ptr()
     rc = _lib.load().fa_decode_fwd_noalloc(ctypes.byref(a), _lib.stream_of(device))
     assert rc == 1 and b"library-owned" in _lib.load().fa_last_error()
+
+
+def test_noalloc_multi_row_decode_matches_decode_rows(device):
+    """Speculative-decode rows (1-4 per request, causal): the library's plan
+    equals the Python layer's, so fa_decode_fwd_noalloc and decode_rows (with
+    caller-allocated partials) give bit-identical results; then a smaller call."""
+    from flash_attn_mps_amd._decode import decode_rows
+    for seed, (batch, max_ctx) in enumerate([(24, 9000), (3, 700)]):
+        t = _paged_case(device, seed=40 + seed, batch=batch, heads=32, kvheads=8, dim=128, max_ctx=max_ctx,
+                        pool_pages=700, kv_dtype=torch.bfloat16, sinks=True)
+        g = torch.Generator().manual_seed(50 + seed)
+        q_lens = torch.randint(1, 5, (batch,), generator=g).tolist()
+        q_lens[0] = 4
+        cu_q = torch.tensor([0] + list(torch.tensor(q_lens).cumsum(0)), dtype=torch.int32, device=device)
+        q = torch.randn(sum(q_lens), 32, 128, generator=g).to(torch.bfloat16).to(device)
+        kw = dict(cu_seqlens_q=cu_q, seqused_k=t["used"], max_seqlen_q=4, max_seqlen_k=max_ctx,
+                  block_table=t["table"], s_aux=t["s_aux"], causal=True)
+        p = problem(q, t["k"], t["v"], **kw).validate()
+        ref_out, ref_lse = decode_rows(p, torch.full_like(q, float("nan")))
+        splits, _ = split_plan(batch, workgroups_per_token(32, 8, 128, 128, True, 4), max_ctx, 0)
+        assert splits > 1, "the case should exercise the partials"
+        keep = []
+        out, lse = torch.full_like(q, float("nan")), torch.full_like(ref_lse, float("nan"))
+        a = kernel_args(q, t["k"], t["v"], out, lse, keep=keep, **kw)
+        a.num_splits, a.split_span = 0, 0
+        _lib.call("fa_decode_fwd_noalloc", a, device)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref_out.view(torch.int16))
+        assert torch.equal(lse, ref_lse)
