@@ -418,6 +418,19 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   const int n_tiles = kv_end > 0 ? (kv_end + PF_BN - 1) / PF_BN : 0;
   const int tile0 = kv_begin / PF_BN;   // first tile with a visible key
 
+  // Descales (per request and KV head, 1 when absent): score = scale *
+  // q_descale * k_descale * q.k, output * v_descale
+  // (flash_attn_mps/kernels/attention.metal:47-51, 170-180).  A negative
+  // score scale is carried by Q's sign bits (flipped once below), so the
+  // kernel's scale is positive and the row max of the raw dot products is
+  // the row max of the scores.
+  const float kdsc = descale_of(a.q_descale, a.q_descale_stride, b, kh) *
+                     descale_of(a.k_descale, a.k_descale_stride, b, kh);
+  const float vdsc = descale_of(a.v_descale, a.v_descale_stride, b, kh);
+  const bool q_flip = a.softmax_scale * kdsc < 0.0f;
+  const float kscale = q_flip ? -(a.softmax_scale * kdsc) : a.softmax_scale * kdsc;
+  const uint32_t q_flip16 = q_flip ? 0x80008000u : 0u, q_flip8 = q_flip ? 0x80808080u : 0u;   // sign bits
+
   // Q^T operands for the whole kernel: block nb, lane holds
   // Q[wq0 + 32 nb + l32][16 kk + 8 hh .. +8].
   const int wq0 = q0 + (wave_u % wph) * 32 * NB;
@@ -438,6 +451,11 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
           lo = *(const u32x4*)(qp + 64 * j);
           hi = *(const u32x4*)(qp + 64 * j + 16);
         }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          lo[e] ^= q_flip8;
+          hi[e] ^= q_flip8;
+        }
         qop8[nb][j] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
       }
     } else {
@@ -447,6 +465,8 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
       for (int kk = 0; kk < KST; ++kk) {
         u32x4 v = {0u, 0u, 0u, 0u};
         if (ok && 16 * kk + 8 * hh + 8 <= DQT) v = *(const u32x4*)(qp + 16 * kk);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] ^= q_flip16;
         qop[nb][kk] = v;
       }
     }
@@ -660,19 +680,13 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   const int vg16 = lane >> 4, vi = lane & 15, va = vi & 3, vt = vi >> 2;
   const int vrd = (8 * (vg16 >> 1) + vt) * 64 + (4 * (vg16 & 1) + va) * 8;
 
-  // Descales (per request and KV head, 1 when absent): score = scale *
-  // q_descale * k_descale * q.k, output * v_descale
-  // (flash_attn_mps/kernels/attention.metal:47-51, 170-180).
-  const float kdsc = descale_of(a.q_descale, a.q_descale_stride, b, kh) *
-                     descale_of(a.k_descale, a.k_descale_stride, b, kh);
-  const float vdsc = descale_of(a.v_descale, a.v_descale_stride, b, kh);
-  const float c_scale = a.softmax_scale * kdsc * LOG2E;   // raw dot -> log2 units
-  const float cap_in = CAP ? 2.0f * LOG2E * a.softmax_scale * kdsc / a.softcap : 0.0f;
+  const float c_scale = kscale * LOG2E;   // raw dot -> log2 units
+  const float cap_in = CAP ? 2.0f * LOG2E * kscale / a.softcap : 0.0f;
   const float cap_out = a.softcap * LOG2E;
   // ALiBi slope in raw dot-product units: the score's bias -slope |qa - key|
   // becomes -sl |qa - key| before the scale (the host requires scale > 0).
   const float sl = ALIBI ? a.alibi[b * a.alibi_stride[0] + (int64_t)h * a.alibi_stride[1]] /
-                               (a.softmax_scale * kdsc)
+                               kscale
                          : 0.0f;
   // A sink logit seeds the running state (max = sink, sum = 1) of every row.
   const float sink2 = a.sinks ? a.sinks[(int64_t)h * a.sink_stride] * LOG2E : -INFINITY;
@@ -889,7 +903,28 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     phase_b(sc, pop);
     qk(st + 1, sn);
     pv(st, pop);
-    phase_a(std::integral_constant<bool, false>(), st + 1, sn, true, f);
+    if constexpr (!CAP) {
+      // Phase A proper (the row max across the lane pair, the rescale factor,
+      // the running max and sum) runs only when some lane holds a score past
+      // the rescale threshold or has no running max yet; otherwise it would
+      // leave the state as it is (+2% on config 2).
+      bool over = false;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        float mx = fmaxf(sn[nb][0], sn[nb][1]);
+#pragma unroll
+        for (int i = 2; i < 16; ++i) mx = fmaxf(mx, sn[nb][i]);
+        over |= !(mx * c_scale <= m_run[nb] + PF_RESCALE);
+      }
+      if (__builtin_expect(__any(over), 0)) {
+        phase_a(std::integral_constant<bool, false>(), st + 1, sn, true, f);
+      } else {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) f[nb] = 1.0f;
+      }
+    } else {
+      phase_a(std::integral_constant<bool, false>(), st + 1, sn, true, f);
+    }
     // Scheduling strategy of the AMDGPU backend that interleaves LDS reads
     // with the MFMAs (the default schedule issues each K operand read one
     // MFMA ahead): +1-2.5% on config 2, measured on two boxes; hand-written

@@ -418,3 +418,47 @@ def test_prefill_window_route_is_mfma(device):
                       max_seqlen_k=300, block_table=None, softmax_scale=None, causal=True, window_size=(63, 0),
                       alibi_slopes=None, softcap=0., s_aux=None, q_descale=None, k_descale=None, v_descale=None,
                       mask_mod=None, aux_tensors=None, leftpad_k=None)
+
+
+@pytest.mark.parametrize("dtype,spread", [(torch.bfloat16, 4.0), (torch.float16, 1.0)])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("d", [64, 128])
+def test_prefill_negative_scale(device, dtype, spread, causal, d):
+    """A negative softmax_scale (the score is scale * q.k for any sign): the
+    row max must be that of the scaled scores, and masked keys must stay at
+    zero weight (a -inf raw score times a negative scale is +inf).  With x4
+    inputs a 64-key tile spans more than 2^128 in probability, so a max taken
+    on the raw dot products overflows."""
+    q_lens, k_lens = [5, 300, 1000, 64], [5, 300, 1100, 64]
+    q, k, v, cuq, cuk = _case(device, dtype, d, 8, 2, q_lens, k_lens, scale=spread, seed=31 + d)
+    v = v * 0.5   # peaked rows output single V rows: |out| < 1 keeps one bf16 ulp under the bar
+    scale = -d ** -0.5
+    kw = dict(cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=max(q_lens), max_seqlen_k=max(k_lens),
+              causal=causal, softmax_scale=scale)
+    out = torch.empty_like(q)
+    assert _uses_mfma(q, k, v, out, torch.empty(8, q.shape[0], device=device), **kw)
+    out, lse = attention(q, k, v, **kw)
+    ref, ref_lse = oracle_attention(q, k, v, cuq, cuk, causal=causal, scale=scale)
+    assert torch.isfinite(out).all()
+    assert_parity(out, lse, ref, ref_lse)
+
+
+def test_prefill_negative_descale_e4m3_cache(device):
+    """E4M3 K/V with a negative k_descale on some (request, KV head) pairs:
+    the score scale's sign differs per workgroup."""
+    q_lens, k_lens = [40, 700, 129], [40, 900, 129]
+    g = torch.Generator().manual_seed(41)
+    q = (torch.randn(sum(q_lens), 8, 128, generator=g) * 2.0).to(torch.bfloat16)
+    k = (torch.randn(sum(k_lens), 2, 128, generator=g) * 2.0).to(torch.float8_e4m3fn)
+    v = (torch.randn(sum(k_lens), 2, 128, generator=g) * 0.5).to(torch.float8_e4m3fn)
+    kd = torch.tensor([[1.5, -1.0], [-0.75, 1.0], [-1.25, -0.5]])
+    vd = torch.rand(3, 2, generator=g) * 0.5 + 0.5
+    cuq, cuk = offsets(q_lens), offsets(k_lens)
+    kw = dict(cu_seqlens_q=cuq.to(device), cu_seqlens_k=cuk.to(device), max_seqlen_q=max(q_lens),
+              max_seqlen_k=max(k_lens), causal=True, k_descale=kd.to(device), v_descale=vd.to(device))
+    qd, kdv, vdv = q.to(device), k.to(device), v.to(device)
+    assert _uses_mfma(qd, kdv, vdv, torch.empty_like(qd), torch.empty(8, qd.shape[0], device=device), **kw)
+    out, lse = attention(qd, kdv, vdv, **kw)
+    ref, ref_lse = oracle_attention(q, k, v, cuq, cuk, causal=True, k_descale=kd, v_descale=vd)
+    assert torch.isfinite(out).all()
+    assert_parity(out, lse, ref, ref_lse)

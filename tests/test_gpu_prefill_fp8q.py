@@ -234,3 +234,24 @@ def test_fp8q_unsupported_dims_take_the_generic_kernel(device):
     out, lse = attention(q, k, v, **kw)
     ref, ref_lse = oracle_attention(q, k, v, cuq, cuk, causal=True, q_descale=qs, k_descale=ks, v_descale=vs)
     assert_parity(out, lse, ref, ref_lse, torch.float16)
+
+
+def test_fp8q_negative_scale_and_descales(device):
+    """E4M3 queries with a negative softmax_scale and negative q descales on
+    some (request, KV head) pairs: each workgroup's score scale takes its own
+    sign, and the row max is that of the scaled scores."""
+    q_lens, k_lens = [37, 300, 513], [37, 400, 700]
+    q, k, v, qs, ks, vs, cuq, cuk = _packed(device, 128, 8, 2, q_lens, k_lens, seed=77, qscale=2.0)
+    qs = qs.clone()
+    qs[0, 1] *= -1
+    qs[2, 0] *= -1
+    kw = dict(cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=max(q_lens), max_seqlen_k=max(k_lens),
+              causal=True, softmax_scale=-(128 ** -0.5), q_descale=qs, k_descale=ks, v_descale=vs)
+    assert _route_is_mfma(q, k, v, torch.bfloat16, **kw)
+    out = torch.empty(q.shape[0], 8, 128, dtype=torch.bfloat16, device=device)
+    out, lse = attention(q, k, v, out=out, **kw)
+    ref, ref_lse = oracle_attention(q, k, v, cuq, cuk, causal=True, scale=-(128 ** -0.5), q_descale=qs,
+                                    k_descale=ks, v_descale=vs)
+    assert torch.isfinite(out).all()
+    assert_parity(out, None, ref, None, torch.bfloat16)
+    assert_parity(out, lse, ref, ref_lse, torch.bfloat16, rows=_rows_with_keys(q_lens, k_lens))
