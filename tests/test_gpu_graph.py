@@ -96,6 +96,40 @@ def test_graph_kvcache_decode_with_growing_lengths(device, hq, hkv):
         assert torch.equal(g_lse, e_lse), f"replay {it}"
 
 
+def test_graph_speculative_decode_rows(device):
+    """Four query rows per request (a speculative-decode step) on the
+    matrix-core decode with (head, row) columns; the cache lengths grow by
+    four keys between replays."""
+    from flash_attn_mps_amd._decode import uses_gqa_kernel
+    from harness import problem
+    gen = torch.Generator().manual_seed(74)
+    ctx = [2900, 21, 1500, 2048, 640, 4, 3000, 999]
+    hq, hkv, d, page, rows = 32, 8, 128, 16, 4
+    kc, vc, table = paged_cache(ctx, page, hkv, d, d, torch.bfloat16, device, gen)
+    lens = torch.tensor([c - rows * REPLAYS for c in ctx], dtype=torch.int32, device=device).clamp_(min=rows)
+    q = torch.randn(len(ctx), rows, hq, d, generator=gen).to(torch.bfloat16).to(device)
+    cq = torch.arange(0, rows * len(ctx) + 1, rows, dtype=torch.int32)
+    assert uses_gqa_kernel(problem(q.flatten(0, 1), kc, vc, cu_seqlens_q=cq.to(device), max_seqlen_q=rows,
+                                   max_seqlen_k=table.shape[1] * page, seqused_k=lens, block_table=table))
+
+    def call():
+        return fa.flash_attn_with_kvcache(q, kc, vc, cache_seqlens=lens, block_table=table,
+                                          causal=True, return_softmax_lse=True)
+
+    graph, (g_out, g_lse) = capture(call)
+    for it in range(REPLAYS):
+        q.copy_(torch.randn(q.shape, generator=gen).to(torch.bfloat16))
+        lens.copy_(torch.minimum(lens + rows, torch.tensor(ctx, dtype=torch.int32, device=device)))
+        e_out, e_lse = call()
+        if it == 0:
+            ref, _ = oracle_attention(q.flatten(0, 1), kc, vc, cq, used_k=lens, block_table=table, causal=True)
+            assert_parity(e_out.flatten(0, 1), None, ref, None, torch.bfloat16)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(g_out, e_out), f"replay {it}"
+        assert torch.equal(g_lse, e_lse), f"replay {it}"
+
+
 def test_graph_vllm_fp8_decode_into_caller_out(device):
     gen = torch.Generator().manual_seed(72)
     ctx = [4100, 1024, 6000, 333, 2500, 4096]
