@@ -289,6 +289,9 @@ def config3_inputs(device):
 
 
 def config3(device, steps, warmup):
+    """Config 3, then on the same cache a speculative-decode step: 4 query rows per
+    request (the last 4 positions, causal), whose rows share each request's K/V reads."""
+    import torch
     import flash_attn_mps_amd as fa
     c = config3_inputs(device)
 
@@ -298,9 +301,19 @@ def config3(device, steps, warmup):
 
     ms, call_ms, kernel_ms = time_calls(step, steps, warmup, kernel="fa_decode_fwd")
     kv_bytes = c["kv_bytes"]
+    g = torch.Generator().manual_seed(123 + 30)
+    q4 = torch.randn(64, 4, c["heads"], c["dim"], generator=g).to(torch.bfloat16).to(device)
+
+    def step4():
+        fa.flash_attn_with_kvcache(q4, c["k_cache"], c["v_cache"], cache_seqlens=c["lengths"],
+                                   block_table=c["table"], causal=True)
+
+    ms4, call_ms4, kernel_ms4 = time_calls(step4, steps, warmup, kernel="fa_decode_fwd")
     del c
+    rows4 = dict(kv_bytes=kv_bytes, ms=ms4, call_ms=call_ms4, kernel_ms=kernel_ms4, gbs=kv_bytes / (ms4 * 1e-3) / 1e9,
+                 call_gbs=kv_bytes / (call_ms4 * 1e-3) / 1e9)
     return dict(kv_bytes=kv_bytes, ms=ms, call_ms=call_ms, kernel_ms=kernel_ms, gbs=kv_bytes / (ms * 1e-3) / 1e9,
-                call_gbs=kv_bytes / (call_ms * 1e-3) / 1e9)
+                call_gbs=kv_bytes / (call_ms * 1e-3) / 1e9, rows4=rows4)
 
 
 def config4_inputs(device):
@@ -511,6 +524,11 @@ def main():
                 pending = r
                 continue
             secondary["config" + name if name[0].isdigit() else name] = secondary_entry(name, r, warmup)
+            if "rows4" in r:
+                entry = secondary_entry(name, r["rows4"], warmup)
+                entry["what"] = ("config 3's cache with 4 query rows per request (speculative decode), "
+                                 "causal; KV bytes counted once per request and KV head")
+                secondary["config3_rows4"] = entry
             torch.cuda.empty_cache()
     c2 = config2(device, args.steps, args.warmup, c=c2_inputs)
     if pending is not None:
