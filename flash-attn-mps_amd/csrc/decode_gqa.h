@@ -46,6 +46,10 @@ using namespace fa_prefill;
 constexpr int GQA_THREADS = 256;   // 4 waves
 constexpr int GQA_HEADS = 32;      // head columns per workgroup (one MFMA tile)
 constexpr int GQA_STAGE = 32;      // keys per wave stage
+#ifndef FA_GQA_NT
+#define FA_GQA_NT 1
+#endif
+constexpr bool GQA_NT = FA_GQA_NT;  // non-temporal K/V DMA
 
 // One 16-key slot: K then V, each D / 64 column groups of 16 rows x 128
 // bytes; slots per wave.
@@ -62,7 +66,7 @@ template <int D> constexpr int gqa_lds_bytes() {
 template <int N, int I = 0>
 FA_DEV void dma_columns_gqa(__amdgpu_buffer_rsrc_t rsrc, char* lds, int voffset) {
   if constexpr (I < N) {
-    dma16<128 * I>(rsrc, lds + I * 16 * 128, voffset);
+    dma16<128 * I, GQA_NT>(rsrc, lds + I * 16 * 128, voffset);
     dma_columns_gqa<N, I + 1>(rsrc, lds, voffset);
   }
 }
@@ -283,24 +287,39 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
                         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)gi);
     return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)gu, (short)0, bytes, 0x00020000);
   };
-  // DMA instructions per group: 2 KG each for 16-bit K and V, KG each for
-  // E4M3 K and V.
-  constexpr int DMA_PER_GROUP = FP8 ? 2 * KG : 4 * KG;
-  auto dma_group = [&](int j) {
-    char* const kb = ring + (j % NSLOT) * SLOT;
-    int kshift, vshift;
-    const auto kr = group_rsrc(khead, krow_b, kpage_b, j, EB * D, kshift);
-    const auto vr = group_rsrc(vhead, vrow_b, vpage_b, j, EB * D, vshift);
-    if constexpr (FP8) {
+  // DMA instructions per stage (two groups): 4 KG each for 16-bit K and V,
+  // 2 KG each for E4M3 K and V.  K and V of a stage are issued separately,
+  // each as soon as the previous stage's reads of that half of the slots are
+  // done.
+  constexpr int KD = FP8 ? 2 * KG : 4 * KG, VD = KD;
+  auto dma_k_stage = [&](int i) {
 #pragma unroll
-      for (int ib = 0; ib < KG; ++ib) dma16<0>(kr, kb + 1024 * ib, kdoff8[ib] - kshift);
+    for (int c = 0; c < 2; ++c) {
+      char* const kb = ring + c * SLOT;
+      int kshift;
+      const auto kr = group_rsrc(khead, krow_b, kpage_b, 2 * i + c, EB * D, kshift);
+      if constexpr (FP8) {
 #pragma unroll
-      for (int ib = 0; ib < KG; ++ib) dma16<0>(vr, kb + 16 * D + 1024 * ib, vdoff8[ib] - vshift);
-    } else {
+        for (int ib = 0; ib < KG; ++ib) dma16<0, GQA_NT>(kr, kb + 1024 * ib, kdoff8[ib] - kshift);
+      } else {
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) dma_columns_gqa<KG>(kr, kb + 8 * rb * 128, kdoff[rb] - kshift);
+        for (int rb = 0; rb < 2; ++rb) dma_columns_gqa<KG>(kr, kb + 8 * rb * 128, kdoff[rb] - kshift);
+      }
+    }
+  };
+  auto dma_v_stage = [&](int i) {
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) dma_columns_gqa<KG>(vr, kb + KBYTES + 8 * rb * 128, vdoff[rb] - vshift);
+    for (int c = 0; c < 2; ++c) {
+      char* const kb = ring + c * SLOT;
+      int vshift;
+      const auto vr = group_rsrc(vhead, vrow_b, vpage_b, 2 * i + c, EB * D, vshift);
+      if constexpr (FP8) {
+#pragma unroll
+        for (int ib = 0; ib < KG; ++ib) dma16<0, GQA_NT>(vr, kb + 16 * D + 1024 * ib, vdoff8[ib] - vshift);
+      } else {
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) dma_columns_gqa<KG>(vr, kb + KBYTES + 8 * rb * 128, vdoff[rb] - vshift);
+      }
     }
   };
 
@@ -338,12 +357,23 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
     }
   };
 
-  auto compute = [&](int i) {
-    char* const slot0 = ring + ((2 * i) % NSLOT) * SLOT;
-    char* const slot1 = ring + ((2 * i + 1) % NSLOT) * SLOT;
+  // Stage i in the wave's two slots.  16-bit: K(i) landed (V(i) may still
+  // be in flight) -> S^T -> K(i + 1) DMA into the K halves -> softmax ->
+  // V(i) landed (K(i + 1) may be in flight) -> P.V -> V(i + 1) DMA.  E4M3:
+  // K(i) and V(i) landed -> V widened -> V(i + 1) DMA into the raw V halves
+  // -> S^T -> K(i + 1) DMA -> softmax -> P.V from the widened rows.  Each
+  // load overlaps the wave's own arithmetic instead of following it.
+  auto stage = [&](int i, bool more) {
+    char* const slot0 = ring;
+    char* const slot1 = ring + SLOT;
     if constexpr (FP8) {
+      wait_dma_older_than<0>();
       widen_v(slot0);
       widen_v(slot1);
+      wait_lds();
+      if (more) dma_v_stage(i + 1);
+    } else {
+      wait_dma_older_than<VD>();
     }
     const char* const kb = l32 < 16 ? slot0 : slot1;
     f32x16 s;
@@ -361,6 +391,8 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
       }
       s = mfma32<T>(av, qop[kk], s);
     }
+    wait_lds();   // K reads of stage i done
+    if (more) dma_k_stage(i + 1);
     // s[e] = score of storage position st_pos(i) + 16 (e >> 3) + 8 hh + (e & 7).
     const int p0 = st_pos(i) + 8 * hh;
     float mx = -INFINITY;
@@ -399,6 +431,10 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
     for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int q = 0; q < 4; ++q) pop[c][q] = pack2<T>(s[8 * c + 2 * q], s[8 * c + 2 * q + 1]);
+    if constexpr (!FP8) {
+      if (more) wait_dma_older_than<KD>();
+      else wait_dma_older_than<0>();
+    }
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -409,19 +445,15 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
         const u32x2 hi = lds_read_tr(vb, vrd + 4 * 128);
         o[db] = mfma32<T>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pop[c], o[db]);
       }
+    wait_lds();   // V reads of stage i done
+    if (!FP8 && more) dma_v_stage(i + 1);
   };
 
-  // The ring starts full; stage i waits for its two groups (the NSLOT - 2
-  // later ones stay in flight), is computed, and its two slots, once its LDS
-  // reads are done, take groups 2 i + NSLOT and 2 i + NSLOT + 1.
-  int issued = 0;
-  for (; issued < min(NSLOT, ngroups); ++issued) dma_group(issued);
-  for (int i = 0; i < nst; ++i) {
-    wait_dma_groups<DMA_PER_GROUP, NSLOT - 2>(issued - 2 * i - 2);
-    compute(i);
-    wait_lds();
-    for (; issued < min(2 * i + 2 + NSLOT, ngroups); ++issued) dma_group(issued);
+  if (nst > 0) {
+    dma_k_stage(0);
+    dma_v_stage(0);
   }
+  for (int i = 0; i < nst; ++i) stage(i, i + 1 < nst);
 
   // ---- Combine the four waves: per head m (log2 units), l and O^T through
   // LDS (the stage buffers are done once every wave passes the barrier).

@@ -165,21 +165,34 @@ FA_DEV float sum_hh(float x) {
 // target buffers no wave reads until then).  m0 (a register the compiler
 // reserves, so it cannot be declared clobbered) is saved and restored
 // around the load, with the one wait state the hardware needs between
-// writing m0 and the load.
-template <int IMM>
+// writing m0 and the load.  NT marks the load non-temporal (streamed data
+// read once, as in decode).
+template <int IMM, bool NT = false>
 FA_DEV void dma16(__amdgpu_buffer_rsrc_t rsrc, char* lds, int voffset) {
 #if __HIP_DEVICE_COMPILE__
   const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)(lds - IMM));
   uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "s_nop 0\n\t"
-      "buffer_load_dwordx4 %2, %3, 0 offen offset:%4 lds\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(base), "v"(voffset), "s"(rsrc), "i"(IMM)
-      : "memory");
+  if constexpr (NT) {
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %3, 0 offen offset:%4 nt lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(base), "v"(voffset), "s"(rsrc), "i"(IMM)
+        : "memory");
+  } else {
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %3, 0 offen offset:%4 lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(base), "v"(voffset), "s"(rsrc), "i"(IMM)
+        : "memory");
+  }
 #endif
 }
 
