@@ -2,10 +2,10 @@
 // takes up to 32 query heads of one KV head (one query token each) and a
 // split of its keys, so every K/V byte read from HBM feeds MFMAs for all of
 // them.  The VALU decode kernel (decode_kernel.h) spends per head and key a
-// 16-lane dot product and P.V FMAs; with 5 or more query heads per KV head
-// that arithmetic, not HBM, sets its pace (Hq/Hkv = 128/8 at d128: 2.3
-// TB/s, 40/8: 4.5; this kernel: 4.9 and 5.2; at 32/8 the VALU kernel's 5.9
-// stays ahead of this one's 5.2).  Here the scores of 32 keys x 32 head columns are one
+// 16-lane dot product and P.V FMAs; with large groups that arithmetic, not
+// HBM, sets its pace (Hq/Hkv = 128/8 at d128: 2.3 TB/s, 40/8: 4.5; this
+// kernel: 5.2-5.3 and 5.7), and from 3 query heads per KV head this kernel
+// is the faster one.  Here the scores of 32 keys x 32 head columns are one
 // v_mfma_f32_32x32x16 chain, exactly as in the prefill kernel with the
 // group's heads in place of query rows (counterpart of the reference's decode
 // route, flash_attn_mps/_decode.py:40-99 and

@@ -47,6 +47,9 @@ GqaChoice pick_decode_gqa(const fa_attn_args& a) {
   if (a.max_seqlen_q > DECODE_GQA_MAX_ROWS) return none;
   if (a.max_seqlen_q <= 1 && a.heads_q / a.heads_k < DECODE_GQA_MIN_GROUP) return none;
   if (a.q_dtype != FA_BF16 && a.q_dtype != FA_F16) return none;
+  // P.V runs on probabilities rounded to the query's type: fp32 outputs
+  // (held to fp32 accuracy) take the VALU kernel, which keeps P in fp32.
+  if (a.out_dtype != a.q_dtype) return none;
   if (a.k_dtype != a.v_dtype || (a.k_dtype != a.q_dtype && a.k_dtype != FA_E4M3)) return none;
   if (a.head_dim_qk != a.head_dim_v || (a.head_dim_qk != 64 && a.head_dim_qk != 128)) return none;
   if (a.alibi || a.mask_kind != 0) return none;

@@ -636,8 +636,10 @@ DecodeKernel pick_decode_fp8_f16(int64_t d, int64_t dv, int gt, bool cap, bool a
 // The matrix-core decode for GQA groups of DECODE_GQA_MIN_GROUP or more query
 // heads per KV head (decode_gqa.h, decode_gqa.hip): its kernel and LDS bytes,
 // or a null kernel when the arguments need the VALU kernel.  Its workgroups
-// take 32 query heads of one KV head each.
-constexpr int DECODE_GQA_MIN_GROUP = 5;
+// take 32 query heads of one KV head each.  From 3 heads per KV head it
+// outruns the VALU kernel (32/8 at d128: 5.70 vs 5.55-5.67 TB/s, 24/8 E4M3
+// 4.26-4.35 vs 4.08); at 2 the VALU kernel is as fast or faster.
+constexpr int DECODE_GQA_MIN_GROUP = 3;
 // Most query rows per request the matrix-core decode takes (its 32 columns
 // hold 32 / rows query heads).
 constexpr int DECODE_GQA_MAX_ROWS = 16;

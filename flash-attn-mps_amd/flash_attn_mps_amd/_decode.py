@@ -54,7 +54,7 @@ def group_tile(heads, kv_heads, dim_qk, dim_v):
 # DECODE_GQA_MIN_GROUP query heads per KV head, or 2..DECODE_GQA_MAX_ROWS rows
 # per request with any group (decode_kernel.h); its workgroups take 32 columns,
 # i.e. 32 // rows query heads.
-_GQA_MIN_GROUP = 5
+_GQA_MIN_GROUP = 3
 _GQA_MAX_ROWS = 16
 
 
@@ -66,7 +66,8 @@ def uses_gqa_kernel(p, rows=None):
     page = p.k.shape[1] if p.paged else 0
     rows = p.max_q if rows is None else rows
     rows_ok = (p.heads // p.kv_heads >= _GQA_MIN_GROUP) if rows <= 1 else rows <= _GQA_MAX_ROWS
-    return (rows_ok and p.q.dtype in (torch.float16, torch.bfloat16)
+    out_dtype = p.out.dtype if p.out is not None else p.output_dtype
+    return (rows_ok and p.q.dtype in (torch.float16, torch.bfloat16) and out_dtype == p.q.dtype
             and p.k.dtype == p.v.dtype and p.k.dtype in (p.q.dtype, torch.float8_e4m3fn)
             and p.dim_qk == p.dim_v and p.dim_qk in (64, 128) and p.alibi is None and p.mask is None
             and page % 16 == 0)

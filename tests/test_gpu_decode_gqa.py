@@ -1,4 +1,4 @@
-"""The matrix-core decode for GQA groups of 5 or more query heads per KV head
+"""The matrix-core decode for GQA groups of 3 or more query heads per KV head
 (csrc/decode_gqa.h) against the CPU oracle.
 
 It runs for 16-bit queries over K/V of their type or E4M3 (with descales)
@@ -45,7 +45,7 @@ def _pool(stored, page, kv_heads, dim, dtype, device, seed, valid_from):
     return kc.to(dtype).to(device), vc.to(dtype).to(device), table.to(device), cols
 
 
-@pytest.mark.parametrize("heads,kv_heads", [(5, 1), (8, 1), (14, 2), (32, 1), (48, 1), (64, 2)])
+@pytest.mark.parametrize("heads,kv_heads", [(3, 1), (8, 2), (5, 1), (8, 1), (14, 2), (32, 1), (48, 1), (64, 2)])
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("splits", [0, 1, 3])
@@ -232,4 +232,21 @@ def test_rows_e4m3_cache(device, q_lens, q_dtype):
     (got, lse), cu_q = _rows_call(q.to(device), kc.to(device), vc.to(device), q_lens, max_seqlen_k=cols * page, **kw)
     ref, ref_lse = oracle_attention(q, kc, vc, cu_q, used_k=used, block_table=table, sinks=sinks, causal=True,
                                     k_descale=kd, v_descale=vd)
+    assert_parity(got, lse, ref, ref_lse)
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(8, 2), (32, 8), (64, 4)])
+def test_fp32_output_keeps_fp32_accuracy(device, heads, kv_heads):
+    """An fp32 output is held to the fp32 bar (1e-4): such calls skip the
+    matrix-core decode, whose P.V rounds probabilities to 16 bits."""
+    lengths, page, d = [1, 300, 2049, 0, 77], 16, 128
+    kc, vc, table, cols = _pool(lengths, page, kv_heads, d, torch.bfloat16, device, 780 + heads, [0] * len(lengths))
+    g = torch.Generator().manual_seed(781)
+    q = torch.randn(len(lengths), heads, d, generator=g).to(torch.bfloat16).to(device)
+    cu_q, used = torch.arange(len(lengths) + 1, device=device, dtype=torch.int32), _i32(lengths, device)
+    out = torch.empty(len(lengths), heads, d, device=device, dtype=torch.float32)
+    kw = dict(cu_seqlens_q=cu_q, seqused_k=used, block_table=table)
+    assert not uses_gqa_kernel(problem(q, kc, vc, max_seqlen_q=1, max_seqlen_k=cols * page, out=out, **kw))
+    got, lse = decode_attention(q, kc, vc, max_seqlen_k=cols * page, out=out, **kw)
+    ref, ref_lse = oracle_attention(q, kc, vc, cu_q, used_k=used, block_table=table)
     assert_parity(got, lse, ref, ref_lse)

@@ -269,9 +269,11 @@ def test_query_head_tiles(device, kv_dtype, heads, kv_heads, d, tile, splits):
     """`tile` query heads of one KV head per workgroup (8 for 128-wide tiles,
     4 for 64-wide); groups of 16 take two workgroups, groups of 5-7 end in a
     partial tile whose spare slots must store nothing.  Spare table entries
-    point at a NaN page; sinks, softcap 20, FP8 descales."""
+    point at a NaN page; sinks, softcap 20, FP8 descales.  Pages of 8 tokens
+    keep these groups on the VALU kernel (the matrix-core decode needs pages
+    of a multiple of 16)."""
     assert group_tile(heads, kv_heads, d, d) == tile
-    lengths, page = [1, 300, 2049, 0, 77], 16
+    lengths, page = [1, 300, 2049, 0, 77], 8
     g = torch.Generator().manual_seed(610 + heads + d + splits)
     cols = max(-(-n // page) for n in lengths) + 1
     pool = len(lengths) * cols + 1

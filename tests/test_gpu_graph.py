@@ -66,10 +66,10 @@ def paged_cache(ctx, page, hkv, dq, dv, dtype, device, gen, scale=None):
     return kc, vc, table.to(device)
 
 
-@pytest.mark.parametrize("hq,hkv", [(32, 8), (64, 4)])
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 8), (64, 4)])
 def test_graph_kvcache_decode_with_growing_lengths(device, hq, hkv):
-    """32/8 heads run the VALU decode kernel, 64/4 (groups of 16) the
-    matrix-core GQA decode."""
+    """16/8 heads (groups of 2) run the VALU decode kernel, 32/8 and 64/4
+    the matrix-core GQA decode."""
     gen = torch.Generator().manual_seed(71)
     ctx = [2900, 17, 1500, 2048, 640, 1, 3000, 999]
     d, page = 128, 16

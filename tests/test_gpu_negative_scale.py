@@ -24,7 +24,7 @@ def _paged(lengths, kv_heads, d, dtype, seed, spread=1.0, page=16):
     return kc, vc, table, cols * page
 
 
-@pytest.mark.parametrize("heads,kv_heads", [(16, 8), (32, 4)])
+@pytest.mark.parametrize("heads,kv_heads", [(16, 8), (32, 4), (24, 8)])
 @pytest.mark.parametrize("window", [(-1, -1), (100, 0)])
 def test_decode_negative_scale(device, heads, kv_heads, window):
     lengths = [1, 40, 777, 2049, 300]
@@ -35,7 +35,7 @@ def test_decode_negative_scale(device, heads, kv_heads, window):
     kw = dict(cu_seqlens_q=cu_q.to(device), seqused_k=used.to(device), block_table=table.to(device),
               softmax_scale=SCALE, window_size=window)
     p = problem(q.to(device), kc.to(device), vc.to(device), max_seqlen_q=1, max_seqlen_k=max_k, **kw)
-    assert uses_gqa_kernel(p) == (heads // kv_heads >= 5)
+    assert uses_gqa_kernel(p) == (heads // kv_heads >= 3)
     out, lse = decode_attention(q.to(device), kc.to(device), vc.to(device), max_seqlen_k=max_k, **kw)
     ref, ref_lse = oracle_attention(q, kc, vc, cu_q, used_k=used, block_table=table, scale=SCALE, window=window)
     assert_parity(out, lse, ref, ref_lse)
