@@ -1,8 +1,11 @@
-"""Single-query split-KV decode on gfx950 (counterpart of flash_attn_mps/_decode.py:40-99).
+"""Split-KV decode on gfx950 (counterpart of flash_attn_mps/_decode.py:40-99): one
+query row per request, and 2..16 rows per request (speculative decode) on the
+matrix-core kernel.
 
 The split plan uses only host-known sizes: the most keys a query can see
-(max_seqlen_k clipped by a left window, _decode.py:63) and the number of
-(request, query-head group) work units.  A split covers `span` keys; the span
+(max_seqlen_k clipped by a left window, _decode.py:63; with R rows the first
+row's window, R - 1 keys wider) and the number of (request, query-head group)
+work units.  A split covers `span` keys; the span
 starts at 2048 and halves (down to 128) until the grid holds at least 2048
 workgroups, so small batches still fill the 256 compute units.  An explicit
 num_splits is honoured.  fa_decode_fwd_noalloc plans the same way in C.
