@@ -53,10 +53,10 @@ constexpr bool GQA_NT = FA_GQA_NT;  // non-temporal K/V DMA
 
 // One 16-key slot: K then V, each D / 64 column groups of 16 rows x 128
 // bytes; slots per wave.
-template <int D> constexpr int gqa_slot_bytes() { return 64 * D; }
-template <int D> constexpr int gqa_slots() { return 2; }
-template <int D> constexpr int gqa_lds_bytes() {
-  const int ring = 4 * gqa_slots<D>() * gqa_slot_bytes<D>();
+template <int D, bool FP8> constexpr int gqa_slot_bytes() { return FP8 ? 32 * D : 64 * D; }
+template <int D, bool FP8> constexpr int gqa_slots() { return FP8 ? 4 : 2; }
+template <int D, bool FP8> constexpr int gqa_lds_bytes() {
+  const int ring = 4 * gqa_slots<D, FP8>() * gqa_slot_bytes<D, FP8>();
   const int combine = 4 * GQA_HEADS * (D + 4 + 2) * 4;
   return ring > combine ? ring : combine;
 }
@@ -69,6 +69,14 @@ FA_DEV void dma_columns_gqa(__amdgpu_buffer_rsrc_t rsrc, char* lds, int voffset)
     dma16<128 * I, GQA_NT>(rsrc, lds + I * 16 * 128, voffset);
     dma_columns_gqa<N, I + 1>(rsrc, lds, voffset);
   }
+}
+
+// ds_read_b64_tr_b8: 8 bytes, transposed across the lanes of each 16-lane
+// group (see the E4M3 V^T reads below).
+FA_DEV u32x2 lds_read_tr8(const char* base, int off) {
+  typedef __attribute__((ext_vector_type(2))) int i32x2_t;
+  typedef __attribute__((address_space(3))) i32x2_t lds_i32x2;
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(base + off)));
 }
 
 // s_waitcnt vmcnt(N) (the LDS DMAs of all but the N most recent
@@ -105,7 +113,7 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   constexpr int KG = D / 64;              // 64-dim column groups of a K slot
   constexpr int DB = D / 32;              // 32-dim blocks of O^T
   constexpr int KGROUP = 16 * 128;        // one column group: 16 rows x 128 bytes
-  constexpr int KBYTES = KG * KGROUP, SLOT = gqa_slot_bytes<D>(), NSLOT = gqa_slots<D>();
+  constexpr int KBYTES = KG * KGROUP, SLOT = gqa_slot_bytes<D, FP8>(), NSLOT = gqa_slots<D, FP8>();
   static_assert(NSLOT >= 2, "a stage's two slots");
 
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -226,12 +234,16 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   // spreads the 8-byte K operand reads of 16 rows over distinct bank slots.
   constexpr int NCH = D / 16;
   auto swz8 = [](int row) { return D == 128 ? (row >> 1) & 7 : (row >> 2) & 3; };
+  // Raw E4M3 V rows: 16-byte chunk q at position q ^ vswz8(row), so the 16
+  // lanes of one transposed read (8 rows x two 8-byte halves of one chunk)
+  // fall on 16 distinct bank pairs.
+  auto vswz8 = [](int row) { return D == 128 ? row & 7 : (row >> 2) & 3; };
   int kdoff8[KG], vdoff8[KG];
 #pragma unroll
   for (int ib = 0; ib < KG; ++ib) {
     const int row = (1024 / D) * ib + lane / NCH, q = lane % NCH;
     kdoff8[ib] = (int)(sigma(row) * krow_b) + ((q ^ swz8(row)) * 16);
-    vdoff8[ib] = (int)(row * vrow_b) + q * 16;
+    vdoff8[ib] = (int)(row * vrow_b) + ((q ^ vswz8(row)) * 16);
   }
   // Buffer descriptor of the 16-key group at storage position pos (a
   // multiple of 16), covering only its keys in [pos_lo, pos_end): the base is
@@ -287,15 +299,16 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
                         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)gi);
     return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)gu, (short)0, bytes, 0x00020000);
   };
+  // Slot of group c of stage i: 16-bit K and V of one stage (slots 0, 1);
+  // E4M3 raw K and V rows of two stages (slots 2 (i % 2) + c).
+  auto slot_of = [&](int i, int c) -> char* { return ring + (FP8 ? 2 * (i & 1) + c : c) * SLOT; };
   // DMA instructions per stage (two groups): 4 KG each for 16-bit K and V,
-  // 2 KG each for E4M3 K and V.  K and V of a stage are issued separately,
-  // each as soon as the previous stage's reads of that half of the slots are
-  // done.
+  // 2 KG each for E4M3 K and V.
   constexpr int KD = FP8 ? 2 * KG : 4 * KG, VD = KD;
   auto dma_k_stage = [&](int i) {
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      char* const kb = ring + c * SLOT;
+      char* const kb = slot_of(i, c);
       int kshift;
       const auto kr = group_rsrc(khead, krow_b, kpage_b, 2 * i + c, EB * D, kshift);
       if constexpr (FP8) {
@@ -310,7 +323,7 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   auto dma_v_stage = [&](int i) {
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      char* const kb = ring + c * SLOT;
+      char* const kb = slot_of(i, c);
       int vshift;
       const auto vr = group_rsrc(vhead, vrow_b, vpage_b, 2 * i + c, EB * D, vshift);
       if constexpr (FP8) {
@@ -342,39 +355,30 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   int krd8[FP8 ? KSTEPS : 1];
 #pragma unroll
   for (int kk = 0; kk < (FP8 ? KSTEPS : 1); ++kk) krd8[kk] = r16 * D + ((kk ^ swz8(r16)) * 16) + 8 * hh;
-  // E4M3: lane p widens raw V row p / 4, dims D / 4 * (p % 4) .. + D / 4, into
-  // the slot's 16-bit V rows.
-  const int wrow = lane >> 2, wq = lane & 3;
-  const int wsrc = 16 * D + wrow * D + (D / 4) * wq;
-  const int wdst = KBYTES + ((D / 4) * wq / 64) * KGROUP + wrow * 128 + ((((D / 4) * wq % 64) / 8) ^ vswz(wrow)) * 16;
-  auto widen_v = [&](char* slot) {
+  // E4M3 V^T straight from the raw rows through ds_read_b64_tr_b8, widened in
+  // registers: in each 16-lane group g the hardware hands lane i byte i % 8
+  // of the 8 bytes read by lanes i / 8, i / 8 + 2, ..., i / 8 + 14, in that
+  // order.  Lane s of group g reads row 8 (g / 2) + s / 2, dims 32 db + 16
+  // (g % 2) + 8 (s % 2) .. +8, so lane 16 g + i receives dim 32 db + 16 (g %
+  // 2) + i of keys 8 (g / 2) .. +8: the A operand of O^T += V^T P^T.
+  const int v8row = 8 * (vg16 >> 1) + (vi >> 1);
+  int vrd8[FP8 ? DB : 1];
 #pragma unroll
-    for (int c = 0; c < D / 64; ++c) {
-      u32x4 lo, hi;
-      widen_fp8_16<T>(*(const u32x4*)(slot + wsrc + 16 * c), lo, hi);
-      *(u32x4*)(slot + wdst + 32 * c) = lo;
-      *(u32x4*)(slot + wdst + 32 * c + 16) = hi;
-    }
-  };
+  for (int db = 0; db < (FP8 ? DB : 1); ++db)
+    vrd8[db] = 16 * D + v8row * D + (((2 * db + (vg16 & 1)) ^ vswz8(v8row)) * 16) + 8 * (vi & 1);
 
-  // Stage i in the wave's two slots.  16-bit: K(i) landed (V(i) may still
-  // be in flight) -> S^T -> K(i + 1) DMA into the K halves -> softmax ->
-  // V(i) landed (K(i + 1) may be in flight) -> P.V -> V(i + 1) DMA.  E4M3:
-  // K(i) and V(i) landed -> V widened -> V(i + 1) DMA into the raw V halves
-  // -> S^T -> K(i + 1) DMA -> softmax -> P.V from the widened rows.  Each
-  // load overlaps the wave's own arithmetic instead of following it.
+  // Stage i.  K(i) landed (V(i) may still be in flight) -> S^T -> the next
+  // K DMA into the K halves just read -> softmax -> V(i) landed -> P.V ->
+  // the next V DMA into the V halves just read.  16-bit slots hold one
+  // stage, so the refills are stage i + 1's; E4M3 slots hold two, so they
+  // are stage i + 2's while stage i + 1 is already in flight.  Each load
+  // overlaps the wave's own arithmetic instead of following it.
   auto stage = [&](int i, bool more) {
-    char* const slot0 = ring;
-    char* const slot1 = ring + SLOT;
-    if constexpr (FP8) {
-      wait_dma_older_than<0>();
-      widen_v(slot0);
-      widen_v(slot1);
-      wait_lds();
-      if (more) dma_v_stage(i + 1);
-    } else {
-      wait_dma_older_than<VD>();
-    }
+    char* const slot0 = slot_of(i, 0);
+    char* const slot1 = slot_of(i, 1);
+    // K(i) landed; newer: V(i), and for E4M3 also stage i + 1.
+    if (FP8 && more) wait_dma_older_than<2 * VD + KD>();
+    else wait_dma_older_than<VD>();
     const char* const kb = l32 < 16 ? slot0 : slot1;
     f32x16 s;
 #pragma unroll
@@ -392,7 +396,11 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
       s = mfma32<T>(av, qop[kk], s);
     }
     wait_lds();   // K reads of stage i done
-    if (more) dma_k_stage(i + 1);
+    if constexpr (FP8) {
+      if (i + 2 < nst) dma_k_stage(i + 2);
+    } else {
+      if (more) dma_k_stage(i + 1);
+    }
     // s[e] = score of storage position st_pos(i) + 16 (e >> 3) + 8 hh + (e & 7).
     const int p0 = st_pos(i) + 8 * hh;
     float mx = -INFINITY;
@@ -431,7 +439,12 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
     for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int q = 0; q < 4; ++q) pop[c][q] = pack2<T>(s[8 * c + 2 * q], s[8 * c + 2 * q + 1]);
-    if constexpr (!FP8) {
+    // V(i) landed; newer: 16-bit K(i + 1); E4M3 stage i + 1 and K(i + 2).
+    if constexpr (FP8) {
+      if (i + 2 < nst) wait_dma_older_than<2 * KD + VD>();
+      else if (more) wait_dma_older_than<KD + VD>();
+      else wait_dma_older_than<0>();
+    } else {
       if (more) wait_dma_older_than<KD>();
       else wait_dma_older_than<0>();
     }
@@ -440,18 +453,34 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         const char* const vb = c ? slot1 : slot0;
-        const int vrd = ((db & 1) ? vrd1 : vrd0) + (db >> 1) * KGROUP;
-        const u32x2 lo = lds_read_tr(vb, vrd);
-        const u32x2 hi = lds_read_tr(vb, vrd + 4 * 128);
-        o[db] = mfma32<T>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pop[c], o[db]);
+        u32x4 av;
+        if constexpr (FP8) {
+          const u32x2 w = lds_read_tr8(vb, vrd8[db]);
+          av = u32x4{widen_fp8_pair<T, false>(w[0]), widen_fp8_pair<T, true>(w[0]), widen_fp8_pair<T, false>(w[1]),
+                     widen_fp8_pair<T, true>(w[1])};
+        } else {
+          const int vrd = ((db & 1) ? vrd1 : vrd0) + (db >> 1) * KGROUP;
+          const u32x2 lo = lds_read_tr(vb, vrd);
+          const u32x2 hi = lds_read_tr(vb, vrd + 4 * 128);
+          av = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
+        o[db] = mfma32<T>(av, pop[c], o[db]);
       }
     wait_lds();   // V reads of stage i done
-    if (!FP8 && more) dma_v_stage(i + 1);
+    if constexpr (FP8) {
+      if (i + 2 < nst) dma_v_stage(i + 2);
+    } else {
+      if (more) dma_v_stage(i + 1);
+    }
   };
 
   if (nst > 0) {
     dma_k_stage(0);
     dma_v_stage(0);
+  }
+  if (FP8 && nst > 1) {
+    dma_k_stage(1);
+    dma_v_stage(1);
   }
   for (int i = 0; i < nst; ++i) stage(i, i + 1 < nst);
 

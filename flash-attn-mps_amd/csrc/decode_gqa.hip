@@ -27,7 +27,7 @@ template <typename T, typename KT, int D>
 GqaChoice choose(bool cap) {
   GqaChoice c;
   c.kern = cap ? fa_decode_gqa::decode_gqa_kernel<T, D, true, KT> : fa_decode_gqa::decode_gqa_kernel<T, D, false, KT>;
-  c.lds = fa_decode_gqa::gqa_lds_bytes<D>();
+  c.lds = fa_decode_gqa::gqa_lds_bytes<D, KT::id == FA_E4M3>();
   return c;
 }
 
