@@ -474,7 +474,8 @@ def secondary_entry(name, r, warmup):
         entry.update(kv_GBps=round(r["gbs"], 1), roofline_ms=round(r["roofline_ms"], 4),
                      frac=round(r["frac"], 4), chunk_flops=r["flops"])
         if name == "5_fixed_order":
-            entry["what"] = "config 5 with num_splits=1: every request in the MFMA prefill, batch-invariant"
+            entry["what"] = ("config 5 with num_splits=1 (batch-invariant): chunks in the MFMA prefill, "
+                             "single-query requests in the decode kernel with one split")
     else:
         entry.update(kv_GBps=round(r["gbs"], 1), frac_of_hbm=round(r["gbs"] / PEAK_HBM_GBS, 4),
                      kv_bytes=r["kv_bytes"], call_median_kv_GBps=round(r["call_gbs"], 1),

@@ -149,7 +149,7 @@ def _side_stream(device):
     return stream
 
 
-def _mixed_batch(p, a):
+def _mixed_batch(p, a, fixed_order=False):
     """A batch of several requests with single-query ones among them: the
     decode kernel takes the single-query requests (it skips the others) and
     fa_prefill_fwd the rest (FA_FLAG_SKIP_SINGLE_QUERY).  The two kernels
@@ -158,14 +158,16 @@ def _mixed_batch(p, a):
     after the caller's earlier work; the caller's stream then waits for it.
     The memory-bound decode fills the CUs the compute-bound prefill leaves.
     Returns False (nothing launched) when the decode kernel cannot take the
-    single-query rows."""
+    single-query rows.  With `fixed_order` the decode runs one split per
+    request, so each single-query row is reduced in an order of its own
+    request only (the batch-invariant route)."""
     dec = _lib.AttnArgs.from_buffer_copy(a)
     dec.max_seqlen_q = 1   # the decode kernel takes the one-row requests only
     if not _lib.supported("fa_decode_supported", dec):
         return False
     from ._decode import split_plan, uses_gqa_kernel, workgroups_per_token
     groups = workgroups_per_token(p.heads, p.kv_heads, p.dim_qk, p.dim_v, uses_gqa_kernel(p, 1))
-    splits, span = split_plan(p.batch, groups, p.max_k, 0)
+    splits, span = split_plan(p.batch, groups, p.max_k, 1 if fixed_order else 0)
     dec.num_splits, dec.split_span = splits, span
     if splits > 1:
         _partials(p, dec, (p.batch, p.heads, splits, p.dim_v), (p.batch, p.heads, splits))
@@ -178,6 +180,25 @@ def _mixed_batch(p, a):
         _lib.call("fa_decode_fwd", dec, p.device)
     main.wait_stream(side)
     return True
+
+
+def _fixed_order_decode(p, out):
+    """A fixed-order (deterministic / vLLM num_splits=1) call whose requests
+    all hold one query row: the decode kernel with one split per request, on
+    paged K/V, exactly when a batch holding these requests next to longer
+    ones would route them to it (_mixed_batch), so a request's result does
+    not depend on its neighbours.  Packed K/V keep the MFMA prefill: the
+    matrix-core decode aligns its key stages to storage rows, which move
+    with a request's place in the batch.  None when this route does not
+    apply (nothing launched)."""
+    if not p.paged or not _fits_prefill(p, out):
+        return None
+    lse = torch.empty((p.heads, p.tokens), device=p.device, dtype=torch.float32)
+    a = build_args(p, out, lse)
+    if not (_lib.supported("fa_prefill_supported", a) and _lib.supported("fa_decode_supported", a)):
+        return None
+    from ._decode import decode
+    return decode(p, out, splits=1)
 
 
 def solve(p):
@@ -194,6 +215,10 @@ def solve(p):
     if p.max_q == 1 and not p.deterministic and p.mask is None:
         from ._decode import decode
         return decode(p, out)
+    if p.max_q == 1 and p.deterministic and p.mask is None:
+        done = _fixed_order_decode(p, out)
+        if done is not None:
+            return done
     if p.max_q > 1 and not p.deterministic and p.mask is None:
         # A few query rows per request (speculative / multi-token decode):
         # the matrix-core decode with (head, row) columns when it takes them.
@@ -212,7 +237,8 @@ def solve(p):
         # keep every request in this kernel (the decode kernel's split count
         # follows the batch).
         self_attention = p.cu_k is p.cu_q and p.used_k is None and not p.paged
-        if not (p.batch > 1 and not self_attention and not p.deterministic and _mixed_batch(p, a)):
+        mixed = p.batch > 1 and not self_attention and (not p.deterministic or p.paged)
+        if not (mixed and _mixed_batch(p, a, fixed_order=p.deterministic)):
             _lib.call("fa_prefill_fwd", a, p.device)
         return out, lse
     per_row = p.deterministic or p.max_q == 1 or max(p.dim_qk, p.dim_v) > 256

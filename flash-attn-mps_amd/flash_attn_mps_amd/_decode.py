@@ -82,8 +82,9 @@ def workgroups_per_token(heads, kv_heads, dim_qk, dim_v, gqa=False, rows=1):
     return kv_heads * -(-(heads // kv_heads) // tile)
 
 
-def decode(p, out):
-    """One query per request of Problem `p` (cu_seqlens_q steps of 0 or 1).
+def decode(p, out, splits=None):
+    """One query per request of Problem `p` (cu_seqlens_q steps of 0 or 1);
+    `splits` overrides the split count (1: the fixed-order route).
 
     Returns (out, lse).  The split-KV kernels handle 16-bit queries over
     16-bit or FP8 caches at their compiled head dims; other dtype/dim/stride
@@ -93,9 +94,9 @@ def decode(p, out):
     lse = torch.empty((p.heads, p.tokens), dtype=torch.float32, device=p.device)
     a = build_args(p, out, lse, max_q=1)
     a.causal, a.causal_by_batch = 0, None   # a right-aligned single query has no future keys
-    if _run_split_kv(p, a, 1):
+    if _run_split_kv(p, a, 1, splits):
         return out, lse
-    splits = p.splits or max(1, min(32, -(-p.visible_max // 256)))
+    splits = splits or p.splits or max(1, min(32, -(-p.visible_max // 256)))
     if splits > 1:
         _partials(p, a, (splits, p.tokens, p.heads, p.dim_v), (splits, p.heads, p.tokens))
     a.num_splits = splits
@@ -116,15 +117,16 @@ def decode_rows(p, out):
     return (out, lse) if _run_split_kv(p, a, p.max_q) else None
 
 
-def _run_split_kv(p, a, rows):
-    """fa_decode_fwd with the split plan and partials [batch][rows][Hq][S];
-    False when the decode kernels do not take the arguments."""
+def _run_split_kv(p, a, rows, splits=None):
+    """fa_decode_fwd with the split plan (or `splits` splits) and partials
+    [batch][rows][Hq][S]; False when the decode kernels do not take the
+    arguments."""
     if not _lib.supported("fa_decode_supported", a):
         return False
     groups = workgroups_per_token(p.heads, p.kv_heads, p.dim_qk, p.dim_v, uses_gqa_kernel(p, rows), rows)
     left = p.window[0]
     visible = min(p.max_k, left + rows) if left >= 0 else p.max_k   # the first row's window
-    splits, span = split_plan(p.batch, groups, visible, p.splits)
+    splits, span = split_plan(p.batch, groups, visible, splits or p.splits)
     a.num_splits, a.split_span = splits, span
     if splits > 1:
         _partials(p, a, (p.batch, rows, p.heads, splits, p.dim_v), (p.batch, rows, p.heads, splits))

@@ -8,9 +8,10 @@ full config-5 batch (8 chunks of 512 new tokens on prefixes U[0, 4096] plus
 120 single-query requests with contexts U[256, 16384]; DIFFKV Dqk 192 / Dv
 128, Hq = Hkv = 16, bf16, 16-token pages, per-head sinks), or in a reordered
 sub-batch with other neighbours; and the fixed-order results must still meet
-the parity bar against the fp64 oracle.  Every request of the call takes the
-MFMA prefill kernel (fa_prefill_supported holds for the deterministic
-arguments), single-query ones included.
+the parity bar against the fp64 oracle.  The chunks take the MFMA prefill
+kernel (fa_prefill_supported holds for the deterministic arguments) and the
+single-query requests the decode kernel with one split, alone or batched, so
+each row is reduced in an order of its own request only.
 """
 import pytest
 import torch
@@ -69,7 +70,7 @@ def _rows(c, requests, b):
     return slice(start, start + c["q_lens"][b])
 
 
-def test_fixed_order_route_is_the_mfma_kernel(config5, device):
+def test_fixed_order_route_kernels(config5, device):
     c = config5
     q_lens, k_lens = c["q_lens"], c["k_lens"]
     out = torch.empty(sum(q_lens), HQ, DV, dtype=torch.bfloat16, device=device)
@@ -80,6 +81,8 @@ def test_fixed_order_route_is_the_mfma_kernel(config5, device):
                        max_seqlen_k=max(k_lens), block_table=c["table"], causal=True, s_aux=c["sinks"],
                        deterministic=True, num_splits=1)
     assert _lib.supported("fa_prefill_supported", args)
+    args.max_seqlen_q = 1
+    assert _lib.supported("fa_decode_supported", args)
 
 
 def test_requests_are_bit_identical_alone_and_batched(config5):
