@@ -12,26 +12,31 @@
 // kernels/attention_decode.metal:18-149).
 //
 // * Each of the 4 waves owns the 32-key stages w, w + 4, ... of the split and
-//   streams their 16-key groups (global -> LDS DMA) through private slots,
-//   so the waves never wait on each other inside the loop; at the end they
-//   combine (m, l, O) through LDS.  A wave loads a stage, waits for it and
-//   computes it: the latency is hidden by the other waves, and two slots per
-//   wave (16 KiB at d128) let two workgroups share a CU.  Rings of 3-5 slots
-//   per wave (one workgroup per CU, the next stage in flight while one is
-//   computed) measured 4-25% slower at d128 and up to 36% at d64: fewer
-//   waves per CU cost more than the prefetch gains.
+//   streams their 16-key groups (global -> LDS DMA, non-temporal: every K/V
+//   byte is read once per head tile) through private slots, so the waves
+//   never wait on each other inside the loop; at the end they combine (m, l,
+//   O) through LDS.  16-bit slots hold one stage (16 KiB at d128, so two
+//   workgroups share a CU); each refill is issued as soon as the current
+//   stage has read its half (K after S^T, V after P.V), so a wave's loads
+//   overlap its own arithmetic.  E4M3 slots hold raw rows only, half the
+//   size, so they hold two stages.  Rings of 3-5 16-bit slots per wave (one
+//   workgroup per CU) measured 4-25% slower at d128 and up to 36% at d64:
+//   fewer waves per CU cost more than the prefetch gains.
 // * LDS layouts per 16-key slot: K as in the prefill kernel
 //   (prefill_kernel.h), rows holding key sigma(r) with 16-byte chunks
 //   XOR-swizzled by (r / 2) % 8, 64-dim column groups of 16 rows x 128
-//   bytes; V 64-dim column groups of 16 rows x 128 bytes, unswizzled, so
-//   that each DMA instruction reads whole 128-byte lines (the prefill's
-//   32-dim V blocks of 64-byte rows split each line over two instructions:
-//   2% slower at d128, 4% at d64).
-//   S^T = K Q^T (A = K from LDS, B = Q^T in registers), P rounded to the
-//   query type, O^T += V^T P^T with V^T read by ds_read_b64_tr_b16.
-// * Supports 16-bit Q/K/V of one type, head dims 64 and 128 (Dqk = Dv),
-//   packed or paged K/V (page size a multiple of 16), sinks, softcap, left
-//   windows and descales; the host keeps other combinations on the VALU
+//   bytes; 16-bit V in 64-dim column groups of 16 rows x 128 bytes with the
+//   64-byte halves of every other row pair swapped, so that each DMA
+//   instruction reads whole 128-byte lines and the transposed reads are
+//   conflict-free.  S^T = K Q^T (A = K from LDS, B = Q^T in registers), P
+//   rounded to the query type, O^T += V^T P^T with V^T read by
+//   ds_read_b64_tr_b16.  E4M3: K and V stay raw (rows of D bytes, chunks
+//   XOR-swizzled); K operands are widened in registers after 8-byte reads,
+//   V^T comes through ds_read_b64_tr_b8 and is widened the same way.
+// * Supports 16-bit queries over K/V of their type or E4M3 (with descales),
+//   head dims 64 and 128 (Dqk = Dv), outputs of the query's type, packed or
+//   paged K/V (page size a multiple of 16), sinks, softcap, windows, 1-16
+//   query rows per request; the host keeps other combinations on the VALU
 //   kernel.
 #ifndef FA_DECODE_GQA_H
 #define FA_DECODE_GQA_H
