@@ -22,14 +22,18 @@ using namespace fa_decode;
 // written.
 // Split weights exp(lse_s - max) are computed once, 64 splits at a time (split
 // s0 + j on lane j), and broadcast with readlane; every lane accumulates the
-// dims lane, lane + 64, ... so each partial row is one coalesced read.
-constexpr int MERGE_DIMS = 256 / 64;   // dims per lane: the decode kernels cover Dv <= 256
-constexpr int MERGE_GROUP = 8;         // splits whose loads are in flight together
-
+// dims lane, lane + 64, ... (DIMS of them, Dv <= 64 DIMS) so each partial row
+// is one coalesced read.  The first GROUP partial rows are loaded together
+// with the LSEs, before the weights are known, so a row with at most GROUP
+// splits costs one round trip to memory before its store; further splits
+// follow GROUP at a time.  Splits are added in order, whatever GROUP is.
+//
 // Rows are (request, token, head) with max_seqlen_q tokens per request (the
 // multi-token GQA decode) or one; rows past a request's tokens, and requests
 // with more tokens than that, do nothing.
+template <int DIMS, int GROUP>
 __global__ __launch_bounds__(256) void decode_merge_kernel(const fa_attn_args a, const int span) {
+  static_assert(GROUP <= 64, "the first group's weights sit on lanes 0 .. GROUP - 1");
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int ntok = a.max_seqlen_q > 1 ? (int)a.max_seqlen_q : 1;
   const int64_t row = (int64_t)blockIdx.x * 4 + wave;
@@ -44,43 +48,57 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const fa_attn_args a,
   const int nv = n > 0 ? min(S, (n + span - 1) / span) : 1;
   const float* plse = a.partial_lse + row * S;
   const float* po = a.partial_out + row * S * DV;
-  float peak = -INFINITY;
-  for (int s = lane; s < nv; s += 64) peak = fmaxf(peak, plse[s]);
+  // A zero-weight split (empty, its partial never written) is read like the
+  // others but dropped by a select, so its contents never reach the sum.
+  float x0[GROUP][DIMS];
+#pragma unroll
+  for (int u = 0; u < GROUP; ++u)
+#pragma unroll
+    for (int k = 0; k < DIMS; ++k)
+      x0[u][k] = u < nv && lane + 64 * k < DV ? po[(int64_t)u * DV + lane + 64 * k] : 0.0f;
+  const float lse0 = lane < nv ? plse[lane] : -INFINITY;
+  float peak = lse0;
+  for (int s = lane + 64; s < nv; s += 64) peak = fmaxf(peak, plse[s]);
   peak = wave_max(peak);
   const float ref = peak == -INFINITY ? 0.0f : peak;
-  float acc[MERGE_DIMS];
+  float acc[DIMS];
 #pragma unroll
-  for (int k = 0; k < MERGE_DIMS; ++k) acc[k] = 0.0f;
-  float denom = 0.0f;
+  for (int k = 0; k < DIMS; ++k) acc[k] = 0.0f;
+  float w = lane < nv ? expf(lse0 - ref) : 0.0f;
+  float denom = w;
+#pragma unroll
+  for (int u = 0; u < GROUP; ++u) {
+    const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), u));
+#pragma unroll
+    for (int k = 0; k < DIMS; ++k) acc[k] = ws > 0.0f ? fmaf(ws, x0[u][k], acc[k]) : acc[k];
+  }
   for (int s0 = 0; s0 < nv; s0 += 64) {
-    const float w = s0 + lane < nv ? expf(plse[s0 + lane] - ref) : 0.0f;
-    denom += w;
+    if (s0) {
+      w = s0 + lane < nv ? expf(plse[s0 + lane] - ref) : 0.0f;
+      denom += w;
+    }
     const int cnt = min(64, nv - s0);
-    // Splits in groups of MERGE_GROUP: all their loads are issued before any
-    // is used.  A zero-weight split (empty, its partial never written) is
-    // read like the others but dropped by a select, so its contents never
-    // reach the sum.
-    int j = 0;
-    for (; j + MERGE_GROUP <= cnt; j += MERGE_GROUP) {
-      float ws[MERGE_GROUP], x[MERGE_GROUP][MERGE_DIMS];
+    int j = s0 ? 0 : GROUP;
+    for (; j + GROUP <= cnt; j += GROUP) {
+      float ws[GROUP], x[GROUP][DIMS];
 #pragma unroll
-      for (int u = 0; u < MERGE_GROUP; ++u) {
+      for (int u = 0; u < GROUP; ++u) {
         ws[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j + u));
         const float* src = po + (int64_t)(s0 + j + u) * DV;
 #pragma unroll
-        for (int k = 0; k < MERGE_DIMS; ++k) x[u][k] = lane + 64 * k < DV ? src[lane + 64 * k] : 0.0f;
+        for (int k = 0; k < DIMS; ++k) x[u][k] = lane + 64 * k < DV ? src[lane + 64 * k] : 0.0f;
       }
 #pragma unroll
-      for (int u = 0; u < MERGE_GROUP; ++u)
+      for (int u = 0; u < GROUP; ++u)
 #pragma unroll
-        for (int k = 0; k < MERGE_DIMS; ++k) acc[k] = ws[u] > 0.0f ? fmaf(ws[u], x[u][k], acc[k]) : acc[k];
+        for (int k = 0; k < DIMS; ++k) acc[k] = ws[u] > 0.0f ? fmaf(ws[u], x[u][k], acc[k]) : acc[k];
     }
     for (; j < cnt; ++j) {
       const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
       if (ws > 0.0f) {   // zero-weight splits are never read
         const float* src = po + (int64_t)(s0 + j) * DV;
 #pragma unroll
-        for (int k = 0; k < MERGE_DIMS; ++k)
+        for (int k = 0; k < DIMS; ++k)
           if (lane + 64 * k < DV) acc[k] = fmaf(ws, src[lane + 64 * k], acc[k]);
       }
     }
@@ -89,7 +107,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const fa_attn_args a,
   const int64_t tq = r.q_begin + t;
   const float inv = denom > 0.0f ? 1.0f / denom : 0.0f;
 #pragma unroll
-  for (int k = 0; k < MERGE_DIMS; ++k) {
+  for (int k = 0; k < DIMS; ++k) {
     const int d = lane + 64 * k;
     if (d < DV)
       store_any(a.out, tq * a.out_stride[0] + h * a.out_stride[1] + (int64_t)d * a.out_stride[2], a.out_dtype,
@@ -228,7 +246,11 @@ int decode_launch(const fa_attn_args* a, void* stream, const char* who) {
   int rc = fa_check_launch(who);
   if (rc || a->num_splits == 1) return rc;
   const int64_t rows = partial_rows(*a);
-  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)fa_ceil_div(rows, 4)), dim3(256), 0, s, *a, (int)a->split_span);
+  // Dims per lane: the decode kernels cover Dv <= 256.
+  void (*merge)(const fa_attn_args, const int) = a->head_dim_v <= 64    ? decode_merge_kernel<1, 16>
+                                               : a->head_dim_v <= 128 ? decode_merge_kernel<2, 16>
+                                                                      : decode_merge_kernel<4, 8>;
+  hipLaunchKernelGGL(merge, dim3((unsigned)fa_ceil_div(rows, 4)), dim3(256), 0, s, *a, (int)a->split_span);
   return fa_check_launch(who);
 }
 
