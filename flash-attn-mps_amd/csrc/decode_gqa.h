@@ -51,6 +51,7 @@ using namespace fa_prefill;
 constexpr int GQA_THREADS = 256;   // 4 waves
 constexpr int GQA_HEADS = 32;      // head columns per workgroup (one MFMA tile)
 constexpr int GQA_STAGE = 32;      // keys per wave stage
+constexpr float GQA_RESCALE = 8.0f;  // log2 headroom before a column's running max moves
 #ifndef FA_GQA_NT
 #define FA_GQA_NT 1
 #endif
@@ -420,9 +421,14 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
       mx = fmaxf(mx, v);
     }
     mx = max_hh(mx);
-    const float m_new = fmaxf(m_run, mx);
+    // Lazy rescale: the running max moves only when a score passes it by
+    // more than GQA_RESCALE (log2 units; always for the first finite max),
+    // so probabilities stay <= 2^GQA_RESCALE and O is rescaled in few
+    // stages even when 32 columns each raise their max now and then.
+    const bool need = mx > m_run + GQA_RESCALE;
+    const float m_new = need ? mx : m_run;
     const float mref = m_new == -INFINITY ? 0.0f : m_new;
-    const float f = fast_exp2((m_run == -INFINITY ? mref : m_run) - mref);
+    const float f = need ? fast_exp2((m_run == -INFINITY ? mref : m_run) - mref) : 1.0f;
     m_run = m_new;
     l_run *= f;
     if (__builtin_expect(__any(f != 1.0f), 0)) {
