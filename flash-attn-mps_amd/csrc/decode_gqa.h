@@ -517,34 +517,48 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
       *(float4*)(co + ((int64_t)wave * GQA_HEADS + l32) * CO_ROW + 32 * db + 8 * g + 4 * hh) =
           float4{o[db][4 * g], o[db][4 * g + 1], o[db][4 * g + 2], o[db][4 * g + 3]};
   __syncthreads();
-  for (int idx = tid; idx < nh * ntok * D; idx += GQA_THREADS) {
-    const int hc = idx / D, d = idx - hc * D;   // column hc: head h0 + hc / ntok, token hc % ntok
-    const int th = hc / ntok, tt = hc - th * ntok;
-    if (th >= nheads || tt >= r.q_len) continue;
-    float M = cm[hc];
+  // Per column, once: the combined max, the four waves' weights times the
+  // output scale (written over cm) and the LSE (over cl's first row).  Each
+  // column belongs to one thread here, which reads all its entries before
+  // writing them.
+  const int ncol = nh * ntok;   // <= GQA_HEADS
+  if (tid < ncol) {
+    float M = cm[tid];
 #pragma unroll
-    for (int w = 1; w < 4; ++w) M = fmaxf(M, cm[w * GQA_HEADS + hc]);
+    for (int w = 1; w < 4; ++w) M = fmaxf(M, cm[w * GQA_HEADS + tid]);
     const float ref = M == -INFINITY ? 0.0f : M;
-    float L = 0.0f, O = 0.0f;
+    float fw[4], L = 0.0f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const float fw = fast_exp2(cm[w * GQA_HEADS + hc] - ref);
-      L += cl[w * GQA_HEADS + hc] * fw;
-      O += co[((int64_t)w * GQA_HEADS + hc) * CO_ROW + d] * fw;
+      fw[w] = fast_exp2(cm[w * GQA_HEADS + tid] - ref);
+      L += cl[w * GQA_HEADS + tid] * fw[w];
     }
     const float norm = L > 0.0f ? vdsc / L : 0.0f;
-    const float lse = L > 0.0f ? M * LN2 + logf(L) : -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) cm[w * GQA_HEADS + tid] = fw[w] * norm;
+    cl[tid] = L > 0.0f ? M * LN2 + logf(L) : -INFINITY;
+  }
+  __syncthreads();
+  // hc / ntok for hc < 32 and 1 <= ntok <= 16 as a multiply by
+  // ceil(2^32 / ntok) and a shift (the rounding error stays below 32 / 2^32).
+  const uint64_t ntok_inv = ((1ull << 32) + (uint64_t)ntok - 1) / (uint64_t)ntok;
+  for (int idx = tid; idx < ncol * D; idx += GQA_THREADS) {
+    const int hc = idx / D, d = idx - hc * D;   // column hc: head h0 + hc / ntok, token hc % ntok
+    const int th = (int)(((uint64_t)hc * ntok_inv) >> 32), tt = hc - th * ntok;
+    if (th >= nheads || tt >= r.q_len) continue;
+    float O = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) O += co[((int64_t)w * GQA_HEADS + hc) * CO_ROW + d] * cm[w * GQA_HEADS + hc];
     const int h = h0 + th;
     const int64_t tq = r.q_begin + tt;
     if (S == 1) {
-      store_any(a.out, tq * a.out_stride[0] + (int64_t)h * a.out_stride[1] + (int64_t)d * a.out_stride[2], a.out_dtype,
-                O * norm);
-      if (d == 0) a.lse[(int64_t)h * a.lse_stride[0] + tq * a.lse_stride[1]] = lse;
+      store_any(a.out, tq * a.out_stride[0] + (int64_t)h * a.out_stride[1] + (int64_t)d * a.out_stride[2], a.out_dtype, O);
+      if (d == 0) a.lse[(int64_t)h * a.lse_stride[0] + tq * a.lse_stride[1]] = cl[hc];
     } else {
       // Partial rows [batch][ntok][Hq][S] (one token: [batch][Hq][S]).
       const int64_t row = ((b * ntok + tt) * a.heads_q + h) * S + split;
-      a.partial_out[row * D + d] = O * norm;
-      if (d == 0) a.partial_lse[row] = lse;
+      a.partial_out[row * D + d] = O;
+      if (d == 0) a.partial_lse[row] = cl[hc];
     }
   }
 }
