@@ -172,6 +172,16 @@ FA_DEV float wave_max(float x) {
   return x;
 }
 
+FA_DEV int wave_min_i(int x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x = min(x, __shfl_xor(x, m));
+  return x;
+}
+FA_DEV int wave_max_i(int x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x = max(x, __shfl_xor(x, m));
+  return x;
+}
 FA_DEV float readlane_f(float x, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
 }

@@ -3,8 +3,8 @@
 
 namespace fa_prefill {
 
-PrefillChoice pick_f16_large(int64_t dq, int64_t dv, bool causal, int score, bool win, bool fp8) {
-  return pick_dims_large<F16T>(dq, dv, causal, score, win, fp8);
+PrefillChoice pick_f16_large(int64_t dq, int64_t dv, bool causal, int score, bool win, bool fp8, int mk) {
+  return pick_dims_large<F16T>(dq, dv, causal, score, win, fp8, mk);
 }
 
 }  // namespace fa_prefill

@@ -318,7 +318,7 @@ FA_DEV bool compact_item(const fa_attn_args& a, int slot, int xcd, int lane, int
     w.r.q_len = __builtin_amdgcn_readlane(qlen[c], l);
     w.r.k_len = __builtin_amdgcn_readlane(klen[c], l);
     w.r.k_base = __builtin_amdgcn_readlane(kbase[c], l);
-    w.r.left = 0;
+    w.r.left = a.leftpad_k ? load_invariant_i32(a.leftpad_k, w.b * a.leftpad_stride) : 0;
     w.r.causal = a.causal_by_batch ? a.causal_by_batch[w.b * a.causal_stride] != 0 : a.causal != 0;
     return true;
   }
@@ -339,9 +339,14 @@ FA_DEV bool compact_item(const fa_attn_args& a, int slot, int xcd, int lane, int
 // QT: query storage type, T or E4M3.  E4M3 queries (with E4M3 K/V) compute
 // S = K Q^T on v_mfma_f32_32x32x64_f8f6f4 with K kept as raw bytes in LDS;
 // V is staged and widened exactly to T for O += V P (P stays 16-bit).
+// MK: vLLM mask kind (a.mask_kind; 0 none): each row's visible keys are at
+// most two key ranges (see mask_ranges below); causality and the window
+// fields do not apply, as in the reference (kernels/attention.metal:29-45).
 template <typename T, int DQ, int DV, int W, int NB, int MINB, bool CAUSAL, bool CAP, bool WIN, int DQT = DQ,
-          int DVT = DV, typename KT = T, bool ALIBI = false, typename QT = T>
+          int DVT = DV, typename KT = T, bool ALIBI = false, typename QT = T, int MK = 0>
 __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_args a, const PrefillShape shp) {
+  static_assert(MK == 0 || (!CAUSAL && !WIN && !ALIBI), "mask kinds carry their own causality and windows");
+  constexpr bool GEN = WIN || MK != 0;   // per-stage hot / masked decisions (no closed-form hot loop)
   constexpr bool FP8 = KT::id == FA_E4M3;
   constexpr bool FQ = QT::id == FA_E4M3;       // E4M3 queries: FP8 MFMA for S
   static_assert(!(CAP && ALIBI), "the ALiBi bias is added before the softcap would apply");
@@ -416,6 +421,8 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   const int q0 = qb * bmh;
   if (q0 >= r.q_len) return;
   const int off = r.k_len - r.q_len;   // absolute position of query row i is i + off
+  const int wq0 = q0 + (wave_u % wph) * 32 * NB;   // this wave's first query row
+  auto wq0_of = [&](int nb) { return wq0 + 32 * nb + l32; };   // this lane's row of block nb
   // Row qa sees keys j with qa - WL <= j (WL >= 0), j <= qa (causal) or
   // j <= qa + WR (WR >= 0, not causal), j < k_len (flash_attn_mps/kernels/
   // attention.metal:29-45, window kind).  The workgroup's key range follows
@@ -427,9 +434,88 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   int kv_end = r.k_len;
   if (CAUSAL) kv_end = min(kv_end, qa_last + 1);
   else if (WR >= 0) kv_end = min(kv_end, max(qa_last + WR + 1, 0));
-  const int kv_begin = WL >= 0 ? min(max(qa_first - WL, 0), max(kv_end, 0)) : 0;
-  const int n_tiles = kv_end > 0 ? (kv_end + PF_BN - 1) / PF_BN : 0;
-  const int tile0 = kv_begin / PF_BN;   // first tile with a visible key
+  int kv_begin = WL >= 0 ? min(max(qa_first - WL, 0), max(kv_end, 0)) : 0;
+
+  // Mask kinds (flash_attn_mps/kernels/attention.metal:29-45), with qa the
+  // row's absolute position and keys below k_len:
+  //   kind 1 (vllm.mm_prefix_mask): [qa - W + 1, qa] (W = a.mask_window,
+  //     [0, qa] when W < 0) and the row's modality range [lo, hi] =
+  //     a.mask_ranges[row] when lo >= 0 (from qa - W + 1 on with
+  //     a.mask_clamp);
+  //   kind 2 (vllm.rswa_mask): [0, min(P - 1, qa)] with P = a.mask_prefix[b]
+  //     and [qa - Wl + 1, qa] with Wl = a.mask_window_len[0].
+  // mr[nb] = {a1, b1, a2, b2}: the two ranges of this lane's row of block nb
+  // (absolute keys, a > b when empty).  Kind 2 runs the key pipeline once per
+  // range when the two are apart for every row of the workgroup (the keys
+  // between them are never loaded), each run with one range.
+  constexpr int PF_FAR = 1 << 29;   // beyond any key (the host bounds k_len)
+  int mr[NB][4];
+  int mk_p = 0, mk_w = 0;           // kind 2: prefix length, window
+  bool mk_split = false;            // kind 2: two runs
+  auto clip_hi = [&](int x) { return min(x, r.k_len - 1); };
+  auto set_ranges = [&](int part) {  // kind 2: 0 both ranges, 1 the prefix only, 2 the window only
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int row = wq0_of(nb), qa = row + off;
+      int a1 = PF_FAR, b1 = -PF_FAR, a2 = PF_FAR, b2 = -PF_FAR;
+      if (row < r.q_len) {
+        if constexpr (MK == 1) {
+          const int wm = a.mask_window;
+          a1 = wm > 0 ? max(qa - wm + 1, 0) : 0;
+          b1 = clip_hi(qa);
+          const int64_t tq = (int64_t)r.q_begin + row;
+          const int lo = a.mask_ranges[tq * a.ranges_stride[0]];
+          const int hi = a.mask_ranges[tq * a.ranges_stride[0] + a.ranges_stride[1]];
+          if (lo >= 0) {
+            a2 = (a.mask_clamp && wm > 0) ? max(lo, qa - wm + 1) : lo;
+            b2 = clip_hi(hi);
+          }
+        } else if constexpr (MK == 2) {
+          if (part != 2) {
+            a1 = 0;
+            b1 = clip_hi(min(mk_p - 1, qa));
+          }
+          if (part != 1) {
+            a2 = max(max(qa - mk_w + 1, 0), part == 2 ? mk_p : 0);
+            b2 = clip_hi(qa);
+          }
+        }
+      }
+      mr[nb][0] = a1, mr[nb][1] = b1, mr[nb][2] = a2, mr[nb][3] = b2;
+    }
+  };
+  if constexpr (MK == 1) {
+    // Key range of the workgroup: its rows' windows and modality ranges.
+    int lo_min = PF_FAR, hi_max = -1;
+    for (int i = lane; i < bmh; i += 64) {
+      const int row = q0 + i;
+      if (row < r.q_len) {
+        const int64_t tq = (int64_t)r.q_begin + row;
+        const int lo = a.mask_ranges[tq * a.ranges_stride[0]];
+        const int hi = a.mask_ranges[tq * a.ranges_stride[0] + a.ranges_stride[1]];
+        if (lo >= 0 && hi >= lo) {
+          lo_min = min(lo_min, lo);
+          hi_max = max(hi_max, hi);
+        }
+      }
+    }
+    lo_min = __builtin_amdgcn_readfirstlane(wave_min_i(lo_min));
+    hi_max = __builtin_amdgcn_readfirstlane(wave_max_i(hi_max));
+    kv_end = min(r.k_len, max(qa_last + 1, hi_max + 1));
+    kv_begin = a.mask_window > 0 ? max(min(qa_first - a.mask_window + 1, lo_min), 0) : 0;
+    kv_begin = min(kv_begin, max(kv_end, 0));
+  } else if constexpr (MK == 2) {
+    mk_p = load_invariant_i32(a.mask_prefix, b * a.prefix_stride);
+    mk_w = load_invariant_i32(a.mask_window_len, 0);
+    kv_end = min(r.k_len, qa_last + 1);
+    const int wfirst = max(qa_first - mk_w + 1, 0);   // first key of the earliest row's window
+    // Apart when no key between the prefix and the windows is visible:
+    // whole 64-key tiles lie between them.
+    mk_split = mk_p > 0 && (mk_p + PF_BN - 1) / PF_BN < wfirst / PF_BN;
+    kv_begin = mk_p > 0 ? 0 : min(wfirst, max(kv_end, 0));
+  }
+  int n_tiles = kv_end > 0 ? (kv_end + PF_BN - 1) / PF_BN : 0;
+  int tile0 = kv_begin / PF_BN;   // first tile with a visible key
 
   // Descales (per request and KV head, 1 when absent): score = scale *
   // q_descale * k_descale * q.k, output * v_descale
@@ -446,7 +532,6 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
 
   // Q^T operands for the whole kernel: block nb, lane holds
   // Q[wq0 + 32 nb + l32][16 kk + 8 hh .. +8].
-  const int wq0 = q0 + (wave_u % wph) * 32 * NB;
   constexpr int KST8 = DQ / 64;                // k-steps of the E4M3 S MFMA
   u32x4 qop[FQ ? 1 : NB][FQ ? 1 : KST];
   i32x8 qop8[FQ ? NB : 1][FQ ? KST8 : 1];      // E4M3: Q[row][64 j + 32 hh .. +32]
@@ -531,11 +616,12 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     const int nvalid = min(max(r.k_len - key0, 0), 16);
     const char* g = head;
     if (nvalid > 0) {
+      const int pos = key0 + r.left;   // storage position (leftpad: a dense cache's hidden prefix)
       if (paged) {
-        const uint32_t blk = (uint32_t)load_invariant_i32(trow, (int64_t)(key0 >> lp) * bt1);
-        g = head + (uint64_t)blk * page_b + (uint32_t)(key0 & pmask) * row_b;
+        const uint32_t blk = (uint32_t)load_invariant_i32(trow, (int64_t)(pos >> lp) * bt1);
+        g = head + (uint64_t)blk * page_b + (uint32_t)(pos & pmask) * row_b;
       } else {
-        g = head + (uint64_t)(uint32_t)(r.k_base + key0) * row_b;
+        g = head + (uint64_t)(uint32_t)(r.k_base + pos) * row_b;
       }
     }
     // readfirstlane keeps the (uniform) size in an SGPR: a VGPR-held
@@ -549,11 +635,12 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   const int knrec = 15 * (int)krow_b + KEB * DQT, vnrec = 15 * (int)vrow_b + KEB * DVT;
   auto full_rsrc = [&](auto pg, const char* head, uint32_t row_b, uint32_t page_b, int key0, int nrec) {
     const char* g;
+    const int pos = key0 + r.left;
     if constexpr (decltype(pg)::value) {
-      const uint32_t blk = (uint32_t)load_invariant_i32(trow, (int64_t)(key0 >> lp) * bt1);
-      g = head + (uint64_t)blk * page_b + (uint32_t)(key0 & pmask) * row_b;
+      const uint32_t blk = (uint32_t)load_invariant_i32(trow, (int64_t)(pos >> lp) * bt1);
+      g = head + (uint64_t)blk * page_b + (uint32_t)(pos & pmask) * row_b;
     } else {
-      g = head + (uint64_t)(uint32_t)(r.k_base + key0) * row_b;
+      g = head + (uint64_t)(uint32_t)(r.k_base + pos) * row_b;
     }
     return __builtin_amdgcn_make_buffer_rsrc((void*)g, (short)0, nrec, 0x00020000);
   };
@@ -720,16 +807,44 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   const int wave_qabs_hi = min(wq0 + 32 * NB, r.q_len) - 1 + off;
   // The pipeline runs over 32-key stages: stage st is half st % 2 of tile
   // st / 2 (keys 32 st .. +32).
-  const int n_stages = kv_end > 0 ? (kv_end + 31) / 32 : 0;
-  const int st0 = 2 * tile0;
+  int n_stages = kv_end > 0 ? (kv_end + 31) / 32 : 0;
+  int st0 = 2 * tile0;
   // Keys some row of this wave sees: [wave_key_lo, wave_key_hi].
   const int wave_key_lo = WL >= 0 ? wave_qabs_lo - WL : INT_MIN;
   const int wave_key_hi = CAUSAL ? wave_qabs_hi : (WR >= 0 ? wave_qabs_hi + WR : INT_MAX);
-  auto active = [&](int st) { return wave_rows && st * 32 <= wave_key_hi && st * 32 + 31 >= wave_key_lo; };
+  // Mask kinds: keys some row of this wave sees, [wu_lo, wu_hi], and the
+  // keys of range 1 / range 2 every row of it sees, [wf1a, wf1b] / [wf2a,
+  // wf2b] (from mr; rows past the request constrain nothing).
+  int wu_lo = PF_FAR, wu_hi = -PF_FAR, wf1a = 0, wf1b = -1, wf2a = 0, wf2b = -1;
+  auto wave_bounds = [&]() {
+    int ulo = PF_FAR, uhi = -PF_FAR, f1a = -PF_FAR, f1b = PF_FAR, f2a = -PF_FAR, f2b = PF_FAR;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      if (wq0_of(nb) < r.q_len) {
+        if (mr[nb][0] <= mr[nb][1]) ulo = min(ulo, mr[nb][0]), uhi = max(uhi, mr[nb][1]);
+        if (mr[nb][2] <= mr[nb][3]) ulo = min(ulo, mr[nb][2]), uhi = max(uhi, mr[nb][3]);
+        f1a = max(f1a, mr[nb][0]), f1b = min(f1b, mr[nb][1]);
+        f2a = max(f2a, mr[nb][2]), f2b = min(f2b, mr[nb][3]);
+      }
+    }
+    // Wave-uniform after the reductions; readfirstlane keeps them in SGPRs.
+    wu_lo = __builtin_amdgcn_readfirstlane(wave_min_i(ulo));
+    wu_hi = __builtin_amdgcn_readfirstlane(wave_max_i(uhi));
+    wf1a = __builtin_amdgcn_readfirstlane(wave_max_i(f1a));
+    wf1b = __builtin_amdgcn_readfirstlane(wave_min_i(f1b));
+    wf2a = __builtin_amdgcn_readfirstlane(wave_max_i(f2a));
+    wf2b = __builtin_amdgcn_readfirstlane(wave_min_i(f2b));
+  };
+  auto active = [&](int st) {
+    if constexpr (MK != 0) return wave_rows && st * 32 + 31 >= wu_lo && st * 32 <= wu_hi;
+    else return wave_rows && st * 32 <= wave_key_hi && st * 32 + 31 >= wave_key_lo;
+  };
   auto needs_mask = [&](int st) {
     const int t0 = st * 32;
-    return (t0 + 32 > r.k_len) || (CAUSAL && t0 + 31 > wave_qabs_lo) ||
-           (WL >= 0 && t0 < wave_qabs_hi - WL) || (WR >= 0 && t0 + 31 > wave_qabs_lo + WR);
+    if constexpr (MK != 0) return !((t0 >= wf1a && t0 + 31 <= wf1b) || (t0 >= wf2a && t0 + 31 <= wf2b));
+    else
+      return (t0 + 32 > r.k_len) || (CAUSAL && t0 + 31 > wave_qabs_lo) || (WL >= 0 && t0 < wave_qabs_hi - WL) ||
+             (WR >= 0 && t0 + 31 > wave_qabs_lo + WR);
   };
 
   // S^T of one stage: s[nb][i] = score of key 32 st + 16 (i >> 3) + 8 hh + (i & 7).
@@ -787,7 +902,17 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
           s[nb][i] = cap_out * (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f));
         }
       }
-      if constexpr (MASK) {
+      if constexpr (MASK && MK != 0) {
+        // Key t0 + 16 (i >> 3) + 8 hh + (i & 7) is visible iff its offset
+        // 16 (i >> 3) + (i & 7) from t0 + 8 hh lies in one of the row's ranges.
+        const int base = st * 32 + 8 * hh;
+        const int a1 = mr[nb][0] - base, b1 = mr[nb][1] - base, a2 = mr[nb][2] - base, b2 = mr[nb][3] - base;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int o = 16 * (i >> 3) + (i & 7);
+          if (!((o >= a1 && o <= b1) || (o >= a2 && o <= b2))) s[nb][i] = -INFINITY;
+        }
+      } else if constexpr (MASK) {
         // Key t0 + 16 (i >> 3) + 8 hh + (i & 7) is visible iff its offset
         // 16 (i >> 3) + (i & 7) (an inline constant) <= lim.
         const int t0 = st * 32, qa = wq0 + 32 * nb + l32 + off;
@@ -954,7 +1079,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     tile_start(std::integral_constant<int, PF_ANY_TILE>(), st);
     const bool act = active(st), act_n = st + 1 < n_stages && active(st + 1);
     u32x4 pop[NB][2];
-    if constexpr (WIN) {
+    if constexpr (GEN) {
       if (!act && !act_n) return;
       if (act) {
         rescale_o(f);
@@ -974,6 +1099,8 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   };
   auto hot = [&](int st) { return st < n_stages && active(st) && !needs_mask(st); };
 
+  // The key pipeline over tiles tile0 .. n_tiles - 1 (stages st0 .. n_stages - 1).
+  auto run_keys = [&]() {
   if (st0 < n_stages) {
     // Prologue: tile tile0 and K(tile0 + 1) rows 0..31 in LDS; S(st0) and
     // its phase A.
@@ -1017,7 +1144,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     // wave is active (its window may start after st0).
     // The hot loop is instantiated once per K/V layout (packed, paged).
     int st = st0;
-    if constexpr (WIN) {
+    if constexpr (GEN) {
       auto run_hot = [&](auto mode) {
         for (; hot(st + 1) && hot(st + 2) && dma_full(st >> 1); st += 2) {
           step_hot(mode, st, sa, sb, f);
@@ -1059,6 +1186,38 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
         else step_any(st, sa, sb, f);
       }
     }
+  }
+  };
+  if constexpr (MK == 2) {
+    if (mk_split) {
+      // The prefix's tiles, then those of the windows; the running (m, l, O)
+      // carry over, and a barrier keeps the second run's first DMAs off tiles
+      // still being read.
+      const int kv_all = kv_end;
+      set_ranges(1);
+      wave_bounds();
+      kv_end = min(mk_p, kv_all);
+      n_tiles = (kv_end + PF_BN - 1) / PF_BN, n_stages = (kv_end + 31) / 32;
+      tile0 = 0, st0 = 0;
+      run_keys();
+      __syncthreads();
+      set_ranges(2);
+      wave_bounds();
+      kv_end = kv_all;
+      n_tiles = (kv_end + PF_BN - 1) / PF_BN, n_stages = (kv_end + 31) / 32;
+      tile0 = max(qa_first - mk_w + 1, 0) / PF_BN, st0 = 2 * tile0;
+      run_keys();
+    } else {
+      set_ranges(0);
+      wave_bounds();
+      run_keys();
+    }
+  } else {
+    if constexpr (MK == 1) {
+      set_ranges(0);
+      wave_bounds();
+    }
+    run_keys();
   }
 
   // Epilogue: O = O^T / l, LSE = m * ln2 + ln(l).
@@ -1120,12 +1279,26 @@ struct PrefillChoice {
   size_t lds;
 };
 
-// score: 0 plain, 1 softcap, 2 ALiBi (without window or softcap).
+// score: 0 plain, 1 softcap, 2 ALiBi (without window or softcap); mk: vLLM
+// mask kind (0 none; instantiated for unpadded head dims without ALiBi, not
+// for E4M3 K/V at d256, whose registers are already spilled).
 template <typename T, int DQ, int DV, bool CAUSAL, typename S, int DQT, int DVT, typename KT>
-PrefillChoice pick_tile(int score, bool win) {
+PrefillChoice pick_tile(int score, bool win, int mk) {
   PrefillChoice c;
   const bool cap = score == 1;
-  if (score == 2) {   // ALiBi: 16-bit K/V and no window only
+  if (mk != 0) {
+    if constexpr (CAUSAL || DQT != DQ || DVT != DV || (KT::id == FA_E4M3 && DQ == 256)) {
+      return PrefillChoice{nullptr, 0, 0, 0};
+    } else {
+      if (score == 2) return PrefillChoice{nullptr, 0, 0, 0};
+      if (mk == 1)
+        c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB_WIN, false, true, false, DQT, DVT, KT, false, T, 1>
+                     : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB_WIN, false, false, false, DQT, DVT, KT, false, T, 1>;
+      else
+        c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB_WIN, false, true, false, DQT, DVT, KT, false, T, 2>
+                     : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB_WIN, false, false, false, DQT, DVT, KT, false, T, 2>;
+    }
+  } else if (score == 2) {   // ALiBi: 16-bit K/V and no window only
     if constexpr (KT::id == FA_E4M3) return PrefillChoice{nullptr, 0, 0, 0};
     else {
       if (win) return PrefillChoice{nullptr, 0, 0, 0};
@@ -1146,9 +1319,10 @@ PrefillChoice pick_tile(int score, bool win) {
 // (DQ, DV) = the tile; (DQT, DVT) = the tensors' head dims padded into it;
 // KT = the K/V storage type.
 template <typename T, typename KT, int DQ, int DV, int DQT = DQ, int DVT = DV>
-PrefillChoice pick(bool causal, int score, bool win) {
-  return causal ? pick_tile<T, DQ, DV, true, PrefillTile<DQ, DV>, DQT, DVT, KT>(score, win)
-                : pick_tile<T, DQ, DV, false, PrefillTile<DQ, DV>, DQT, DVT, KT>(score, win);
+PrefillChoice pick(bool causal, int score, bool win, int mk) {
+  // Mask kinds carry their own causality: the non-causal instances take them.
+  return causal && mk == 0 ? pick_tile<T, DQ, DV, true, PrefillTile<DQ, DV>, DQT, DVT, KT>(score, win, mk)
+                           : pick_tile<T, DQ, DV, false, PrefillTile<DQ, DV>, DQT, DVT, KT>(score, win, mk);
 }
 
 // Head dims of the reference's fast path (flash_attn_mps/_attention.py:149-158:
@@ -1158,32 +1332,32 @@ PrefillChoice pick(bool causal, int score, bool win) {
 // query dtype and by head dim (16-bit K/V up to 128 / the rest), so that
 // they compile in parallel.
 template <typename T>
-PrefillChoice pick_dims_small(int64_t dq, int64_t dv, bool causal, int score, bool win) {
+PrefillChoice pick_dims_small(int64_t dq, int64_t dv, bool causal, int score, bool win, int mk) {
   if (dq != dv) return PrefillChoice{nullptr, 0, 0, 0};
   switch (dq) {
-    case 32: return pick<T, T, 64, 64, 32, 32>(causal, score, win);
-    case 64: return pick<T, T, 64, 64>(causal, score, win);
-    case 72: return pick<T, T, 128, 128, 72, 72>(causal, score, win);
-    case 80: return pick<T, T, 128, 128, 80, 80>(causal, score, win);
-    case 96: return pick<T, T, 128, 128, 96, 96>(causal, score, win);
-    case 128: return pick<T, T, 128, 128>(causal, score, win);
+    case 32: return pick<T, T, 64, 64, 32, 32>(causal, score, win, mk);
+    case 64: return pick<T, T, 64, 64>(causal, score, win, mk);
+    case 72: return pick<T, T, 128, 128, 72, 72>(causal, score, win, mk);
+    case 80: return pick<T, T, 128, 128, 80, 80>(causal, score, win, mk);
+    case 96: return pick<T, T, 128, 128, 96, 96>(causal, score, win, mk);
+    case 128: return pick<T, T, 128, 128>(causal, score, win, mk);
     default: return PrefillChoice{nullptr, 0, 0, 0};
   }
 }
 
 template <typename T>
-PrefillChoice pick_dims_large(int64_t dq, int64_t dv, bool causal, int score, bool win, bool fp8) {
+PrefillChoice pick_dims_large(int64_t dq, int64_t dv, bool causal, int score, bool win, bool fp8, int mk) {
   if (fp8) {
     if (dq != dv) return PrefillChoice{nullptr, 0, 0, 0};
     switch (dq) {
-      case 64: return pick<T, E4M3T, 64, 64>(causal, score, win);
-      case 128: return pick<T, E4M3T, 128, 128>(causal, score, win);
-      case 256: return pick<T, E4M3T, 256, 256>(causal, score, win);
+      case 64: return pick<T, E4M3T, 64, 64>(causal, score, win, mk);
+      case 128: return pick<T, E4M3T, 128, 128>(causal, score, win, mk);
+      case 256: return pick<T, E4M3T, 256, 256>(causal, score, win, mk);
       default: return PrefillChoice{nullptr, 0, 0, 0};
     }
   }
-  if (dq == 192 && dv == 128) return pick<T, T, 192, 128>(causal, score, win);
-  if (dq == 256 && dv == 256) return pick<T, T, 256, 256>(causal, score, win);
+  if (dq == 192 && dv == 128) return pick<T, T, 192, 128>(causal, score, win, mk);
+  if (dq == 256 && dv == 256) return pick<T, T, 256, 256>(causal, score, win, mk);
   return PrefillChoice{nullptr, 0, 0, 0};
 }
 
@@ -1218,10 +1392,10 @@ PrefillChoice pick_dims_fp8q(int64_t dq, int64_t dv, bool causal, int score, boo
 }
 
 // Defined in prefill_inst_{bf16,f16}_{small,large}.hip and prefill_inst_fp8q.hip.
-PrefillChoice pick_bf16_small(int64_t dq, int64_t dv, bool causal, int score, bool win);
-PrefillChoice pick_f16_small(int64_t dq, int64_t dv, bool causal, int score, bool win);
-PrefillChoice pick_bf16_large(int64_t dq, int64_t dv, bool causal, int score, bool win, bool fp8);
-PrefillChoice pick_f16_large(int64_t dq, int64_t dv, bool causal, int score, bool win, bool fp8);
+PrefillChoice pick_bf16_small(int64_t dq, int64_t dv, bool causal, int score, bool win, int mk);
+PrefillChoice pick_f16_small(int64_t dq, int64_t dv, bool causal, int score, bool win, int mk);
+PrefillChoice pick_bf16_large(int64_t dq, int64_t dv, bool causal, int score, bool win, bool fp8, int mk);
+PrefillChoice pick_f16_large(int64_t dq, int64_t dv, bool causal, int score, bool win, bool fp8, int mk);
 PrefillChoice pick_fp8q(int out_dtype, int64_t dq, int64_t dv, bool causal, int score, bool win);
 
 }  // namespace fa_prefill

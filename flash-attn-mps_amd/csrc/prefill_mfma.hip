@@ -17,15 +17,18 @@ bool window_set(const fa_attn_args& a) {
 PrefillChoice select_prefill(const fa_attn_args& a) {
   const bool causal = a.causal != 0, fp8 = a.k_dtype == FA_E4M3;
   const int score = a.alibi ? 2 : a.softcap > 0.0f ? 1 : 0;   // plain / softcap / ALiBi
+  // vLLM mask kinds carry their own causality and windows (the causal and
+  // window fields do not apply to them, kernels/attention.metal:29-45).
+  const int mk = a.mask_kind;
   // A right window bounds nothing under causality.
-  const bool win = window_set(a);
+  const bool win = mk == 0 && window_set(a);
   const int64_t dq = a.head_dim_qk, dv = a.head_dim_v;
   if (a.q_dtype == FA_E4M3) return pick_fp8q(a.out_dtype, dq, dv, causal, score, win);
   const bool bf16 = a.q_dtype == FA_BF16;
   if (!fp8 && dq <= 128)
-    return bf16 ? pick_bf16_small(dq, dv, causal, score, win) : pick_f16_small(dq, dv, causal, score, win);
-  return bf16 ? pick_bf16_large(dq, dv, causal, score, win, fp8)
-              : pick_f16_large(dq, dv, causal, score, win, fp8);
+    return bf16 ? pick_bf16_small(dq, dv, causal, score, win, mk) : pick_f16_small(dq, dv, causal, score, win, mk);
+  return bf16 ? pick_bf16_large(dq, dv, causal, score, win, fp8, mk)
+              : pick_f16_large(dq, dv, causal, score, win, fp8, mk);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -48,7 +51,21 @@ bool prefill_ok(const fa_attn_args& a) {
                (dq == 192 && dv == 128))) {
     return false;
   }
-  if (a.leftpad_k) return false;
+  // Left padding shifts a request's storage positions; a 16-key group must
+  // then still lie in one page: packed K/V, or one page per request (the
+  // dense-cache layout of flash_attn_with_kvcache).
+  if (a.leftpad_k && a.page_size && a.max_seqlen_k > a.page_size) return false;
+  if (a.mask_kind != 0) {
+    // vLLM mask kinds 1 / 2 (vllm.mm_prefix_mask / rswa_mask) on unpadded
+    // head dims, 16-bit queries, without ALiBi; key ranges use +-2^29
+    // sentinels, so keys stay below 2^28.
+    if (a.mask_kind != 1 && a.mask_kind != 2) return false;
+    if (fp8q || a.alibi || a.max_seqlen_k >= (1ll << 28)) return false;
+    if (a.mask_kind == 1 && !a.mask_ranges) return false;
+    if (a.mask_kind == 2 && (!a.mask_prefix || !a.mask_window_len)) return false;
+    if (!((dq == dv && (dq == 64 || dq == 128 || dq == 256)) || (dq == 192 && dv == 128))) return false;
+    if (fp8 && dq == 256) return false;
+  }
   // ALiBi (per-head or per-request slopes) without softcap, windows or FP8.
   // ALiBi folds into the accumulators in raw dot-product units (slope / scale),
   // so it needs a positive scale and no descale (FP8-only inputs).
@@ -56,7 +73,7 @@ bool prefill_ok(const fa_attn_args& a) {
                   a.k_descale))
     return false;
   const int kb = fp8 ? 1 : 2;   // K/V bytes per element
-  if (a.mask_kind != 0 || a.window_left < -1 || a.window_right < -1) return false;
+  if (a.window_left < -1 || a.window_right < -1) return false;
   if (a.num_splits != 1) return false;
   if (a.q_stride[2] != 1 || a.k_stride[3] != 1 || a.v_stride[3] != 1 || a.out_stride[2] != 1) return false;
   if (!aligned16(a.q) || !aligned16(a.k) || !aligned16(a.v) || ((uintptr_t)a.out & 7u)) return false;

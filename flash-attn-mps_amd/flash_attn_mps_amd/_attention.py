@@ -113,11 +113,12 @@ def build_args(p, out, lse, max_q=None):
 
 
 def _fits_prefill(p, out):
-    """Features the MFMA route takes at all (the kernel is asked about the rest):
-    16-bit queries over same-type or E4M3 K/V with output in the query's type,
-    or E4M3 queries over E4M3 K/V with fp16/bf16 output (S on the FP8 MFMA).
-    The kernel never splits a row, so deterministic calls qualify."""
-    if p.splits not in (0, 1) or p.mask is not None or p.leftpad is not None:
+    """Features the MFMA route takes at all (the kernel is asked about the rest,
+    vLLM mask kinds and left padding included): 16-bit queries over same-type
+    or E4M3 K/V with output in the query's type, or E4M3 queries over E4M3 K/V
+    with fp16/bf16 output (S on the FP8 MFMA).  The kernel never splits a row,
+    so deterministic calls qualify."""
+    if p.splits not in (0, 1):
         return False
     fp8 = torch.float8_e4m3fn
     if p.k.dtype != p.v.dtype:
