@@ -349,11 +349,13 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   constexpr bool GEN = WIN || MK != 0;   // per-stage hot / masked decisions (no closed-form hot loop)
   constexpr bool FP8 = KT::id == FA_E4M3;
   constexpr bool FQ = QT::id == FA_E4M3;       // E4M3 queries: FP8 MFMA for S
-  static_assert(!(CAP && ALIBI), "the ALiBi bias is added before the softcap would apply");
+  // ALiBi without softcap is folded into the score accumulators before the
+  // MFMAs (raw dot-product units); with softcap it follows the softcap.
+  constexpr bool ALIBI_FOLD = ALIBI && !CAP, ALIBI_LATE = ALIBI && CAP;
   constexpr int KEB = KT::bytes;               // bytes per K/V element
   static_assert(!FP8 || (DQT == DQ && DVT == DV && DQ == DV && (DQ == 64 || DQ == 128 || DQ == 256)),
                 "FP8 K/V tiles: 64/128/256-dim heads");
-  static_assert(!FQ || (FP8 && !ALIBI), "E4M3 queries: E4M3 K/V, no ALiBi");
+  static_assert(!FQ || FP8, "E4M3 queries: E4M3 K/V");
   constexpr int BM = 32 * NB * W;              // query rows per workgroup
   constexpr int KST = DQ / 16;                 // k-steps of the QK^T MFMA
   constexpr int KSTT = (DQT + 15) / 16;        // k-steps holding real dims
@@ -527,8 +529,14 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
                      descale_of(a.k_descale, a.k_descale_stride, b, kh);
   const float vdsc = descale_of(a.v_descale, a.v_descale_stride, b, kh);
   const bool q_flip = a.softmax_scale * kdsc < 0.0f;
-  const float kscale = q_flip ? -(a.softmax_scale * kdsc) : a.softmax_scale * kdsc;
+  float kscale = q_flip ? -(a.softmax_scale * kdsc) : a.softmax_scale * kdsc;
   const uint32_t q_flip16 = q_flip ? 0x80008000u : 0u, q_flip8 = q_flip ? 0x80808080u : 0u;   // sign bits
+  // The folded ALiBi bias is in raw units (slope / scale): with a zero score
+  // scale every dot product is replaced by 0 (Q zeroed) and the fold uses a
+  // unit scale, so the scores are the biases alone, as in the reference.
+  const bool q_zero = ALIBI_FOLD && !(kscale > 0.0f);
+  if (q_zero) kscale = 1.0f;
+  const uint32_t q_keep = q_zero ? 0u : 0xffffffffu;
 
   // Q^T operands for the whole kernel: block nb, lane holds
   // Q[wq0 + 32 nb + l32][16 kk + 8 hh .. +8].
@@ -551,8 +559,8 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          lo[e] ^= q_flip8;
-          hi[e] ^= q_flip8;
+          lo[e] = (lo[e] ^ q_flip8) & q_keep;
+          hi[e] = (hi[e] ^ q_flip8) & q_keep;
         }
         qop8[nb][j] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
       }
@@ -564,7 +572,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
         u32x4 v = {0u, 0u, 0u, 0u};
         if (ok && 16 * kk + 8 * hh + 8 <= DQT) v = *(const u32x4*)(qp + 16 * kk);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] ^= q_flip16;
+        for (int e = 0; e < 4; ++e) v[e] = (v[e] ^ q_flip16) & q_keep;
         qop[nb][kk] = v;
       }
     }
@@ -783,11 +791,12 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   const float c_scale = kscale * LOG2E;   // raw dot -> log2 units
   const float cap_in = CAP ? 2.0f * LOG2E * kscale / a.softcap : 0.0f;
   const float cap_out = a.softcap * LOG2E;
-  // ALiBi slope in raw dot-product units: the score's bias -slope |qa - key|
-  // becomes -sl |qa - key| before the scale (the host requires scale > 0).
-  const float sl = ALIBI ? a.alibi[b * a.alibi_stride[0] + (int64_t)h * a.alibi_stride[1]] /
-                               kscale
-                         : 0.0f;
+  // ALiBi slope: folded, in raw dot-product units (the score's bias
+  // -slope |qa - key| becomes -sl |qa - key| before the scale, kscale > 0);
+  // after the softcap, in log2 units.
+  const float slope = ALIBI ? a.alibi[b * a.alibi_stride[0] + (int64_t)h * a.alibi_stride[1]] : 0.0f;
+  const float sl = ALIBI_FOLD ? slope / kscale : 0.0f;
+  const float sl2 = ALIBI_LATE ? slope * LOG2E : 0.0f;
   // A sink logit seeds the running state (max = sink, sum = 1) of every row.
   const float sink2 = a.sinks ? a.sinks[(int64_t)h * a.sink_stride] * LOG2E : -INFINITY;
   float m_run[NB], l_run[NB];
@@ -855,7 +864,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     const char* kl = kbuf0 + ((st >> 1) & 1) * KTILE + (st & 1) * 32 * 128;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      if constexpr (ALIBI) {
+      if constexpr (ALIBI_FOLD) {
         const float d = (float)(st * 32 + 8 * hh - (wq0 + 32 * nb + l32 + off));
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -901,6 +910,12 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
           const float e = fast_exp2(cap_in * s[nb][i]);
           s[nb][i] = cap_out * (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f));
         }
+      }
+      if constexpr (ALIBI_LATE) {
+        // softcap(score) - slope |qa - key|, in log2 units.
+        const float d = (float)(st * 32 + 8 * hh - (wq0 + 32 * nb + l32 + off));
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[nb][i] -= sl2 * fabsf(d + (float)(16 * (i >> 3) + (i & 7)));
       }
       if constexpr (MASK && MK != 0) {
         // Key t0 + 16 (i >> 3) + 8 hh + (i & 7) is visible iff its offset
@@ -1279,7 +1294,7 @@ struct PrefillChoice {
   size_t lds;
 };
 
-// score: 0 plain, 1 softcap, 2 ALiBi (without window or softcap); mk: vLLM
+// score: 0 plain, 1 softcap, 2 ALiBi, 3 softcap then ALiBi; mk: vLLM
 // mask kind (0 none; instantiated for unpadded head dims without ALiBi, not
 // for E4M3 K/V at d256, whose registers are already spilled).
 template <typename T, int DQ, int DV, bool CAUSAL, typename S, int DQT, int DVT, typename KT>
@@ -1298,11 +1313,25 @@ PrefillChoice pick_tile(int score, bool win, int mk) {
         c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB_WIN, false, true, false, DQT, DVT, KT, false, T, 2>
                      : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB_WIN, false, false, false, DQT, DVT, KT, false, T, 2>;
     }
-  } else if (score == 2) {   // ALiBi: 16-bit K/V and no window only
-    if constexpr (KT::id == FA_E4M3) return PrefillChoice{nullptr, 0, 0, 0};
-    else {
-      if (win) return PrefillChoice{nullptr, 0, 0, 0};
+  } else if (score >= 2) {   // ALiBi (3: after a softcap)
+    // With windows, softcap or E4M3 K/V: unpadded 64 / 128 / 256-dim heads
+    // (E4M3 K/V: 64 / 128).
+    constexpr bool MORE = DQT == DQ && DVT == DV && DQ == DV && (DQ == 64 || DQ == 128 || DQ == 256) &&
+                          !(KT::id == FA_E4M3 && DQ == 256);
+    const bool capa = score == 3;
+    if (!capa && !win && KT::id != FA_E4M3) {
       c.kern = prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false, false, DQT, DVT, KT, true>;
+    } else {
+      if constexpr (!MORE) {
+        return PrefillChoice{nullptr, 0, 0, 0};
+      } else {
+        if (win)
+          c.kern = capa ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB_WIN, CAUSAL, true, true, DQT, DVT, KT, true>
+                        : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB_WIN, CAUSAL, false, true, DQT, DVT, KT, true>;
+        else
+          c.kern = capa ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, true, false, DQT, DVT, KT, true>
+                        : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false, false, DQT, DVT, KT, true>;
+      }
     }
   } else if (win)
     c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB_WIN, CAUSAL, true, true, DQT, DVT, KT>
@@ -1367,7 +1396,7 @@ PrefillChoice pick_dims_large(int64_t dq, int64_t dv, bool causal, int score, bo
 template <typename T, int D, bool CAUSAL>
 PrefillChoice pick_tile_fp8q(int score, bool win) {
   using S = PrefillTile<D, D>;
-  if (score == 2) return PrefillChoice{nullptr, 0, 0, 0};   // ALiBi: not with descaled FP8 inputs
+  if (score >= 2) return PrefillChoice{nullptr, 0, 0, 0};   // ALiBi with E4M3 queries: the generic kernel
   const bool cap = score == 1;
   PrefillChoice c;
   if (win)

@@ -16,7 +16,8 @@ bool window_set(const fa_attn_args& a) {
 
 PrefillChoice select_prefill(const fa_attn_args& a) {
   const bool causal = a.causal != 0, fp8 = a.k_dtype == FA_E4M3;
-  const int score = a.alibi ? 2 : a.softcap > 0.0f ? 1 : 0;   // plain / softcap / ALiBi
+  // plain / softcap / ALiBi / softcap then ALiBi
+  const int score = a.alibi ? (a.softcap > 0.0f ? 3 : 2) : a.softcap > 0.0f ? 1 : 0;
   // vLLM mask kinds carry their own causality and windows (the causal and
   // window fields do not apply to them, kernels/attention.metal:29-45).
   const int mk = a.mask_kind;
@@ -66,12 +67,15 @@ bool prefill_ok(const fa_attn_args& a) {
     if (!((dq == dv && (dq == 64 || dq == 128 || dq == 256)) || (dq == 192 && dv == 128))) return false;
     if (fp8 && dq == 256) return false;
   }
-  // ALiBi (per-head or per-request slopes) without softcap, windows or FP8.
-  // ALiBi folds into the accumulators in raw dot-product units (slope / scale),
-  // so it needs a positive scale and no descale (FP8-only inputs).
-  if (a.alibi && (a.softcap > 0.0f || window_set(a) || fp8 || !(a.softmax_scale > 0.0f) || a.q_descale ||
-                  a.k_descale))
-    return false;
+  // ALiBi (per-head or per-request slopes): any 16-bit head dim alone; with
+  // softcap, windows, per-request causality or E4M3 K/V, unpadded 64 / 128 /
+  // 256-dim heads (E4M3 K/V 64 / 128); not with E4M3 queries.
+  if (a.alibi) {
+    if (fp8q) return false;
+    if ((a.softcap > 0.0f || window_set(a) || fp8) &&
+        !(dq == dv && (dq == 64 || dq == 128 || (dq == 256 && !fp8))))
+      return false;
+  }
   const int kb = fp8 ? 1 : 2;   // K/V bytes per element
   if (a.window_left < -1 || a.window_right < -1) return false;
   if (a.num_splits != 1) return false;

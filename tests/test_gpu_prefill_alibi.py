@@ -5,10 +5,11 @@ score (flash_attn_mps/_attention.py applies it after softcap; the oracle in
 oracle/attention.py:109-112 restates that).  Covered: causal and non-causal,
 per-head [Hq] and per-request [B, Hq] slopes, GQA with and without head
 packing, packed and paged K/V, q_len != k_len, sinks, BLOOM-sized slopes on
-long keys, and that the MFMA kernel is the route taken.  ALiBi combined with
-softcap, a window or FP8 K/V stays on the generic kernel; those cases check
-the route and the result.  Tolerances: max-abs <= 2e-3 fp16, <= 1e-2 bf16,
-LSE <= 1e-4.
+long keys, ALiBi after a softcap, with windows, per-request causality and
+E4M3 K/V (64/128/256-dim heads; E4M3 64/128), negative and zero score
+scales, and that the MFMA kernel is the route taken (padded head dims keep
+the combinations on the generic kernel).  Tolerances: max-abs <= 2e-3 fp16,
+<= 1e-2 bf16, LSE <= 1e-4.
 """
 import pytest
 import torch
@@ -119,21 +120,68 @@ def test_alibi_paged_with_sinks(device, page):
     assert_parity(out, lse, ref, ref_lse, torch.bfloat16)
 
 
-@pytest.mark.parametrize("extra", ["softcap", "window", "fp8"])
-def test_alibi_combinations_use_generic_kernel(device, extra):
-    q_lens = [70, 300]
-    q, k, v, cuq, cuk = _case(device, torch.float16, 128, 4, 2, q_lens, q_lens, seed=11)
-    slopes = torch.tensor([0.05, 0.1, 0.2, 0.4], device=device)
-    kw = dict(cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=300, max_seqlen_k=300, causal=True,
-              alibi_slopes=slopes)
+COMBOS = ["softcap", "window", "softcap+window", "per-request causal", "fp8", "fp8+softcap+window"]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("d,extra", [(d, e) for d in (64, 128, 256) for e in COMBOS
+                                     if not (d == 256 and e.startswith("fp8"))])
+def test_alibi_combinations_on_the_mfma_prefill(device, dtype, d, extra):
+    """ALiBi after a softcap (softcap(score) - slope |diff|), with left / right
+    windows, per-request causality and E4M3 K/V with descales
+    (kernels/attention.metal:47-51, 84-87; the reference applies the bias in
+    every kernel).  E4M3 K/V take it at 64- and 128-dim heads."""
+    q_lens, k_lens = [70, 300, 1], [200, 300, 40]
+    q, k, v, cuq, cuk = _case(device, dtype, d, 8, 2, q_lens, k_lens, seed=d + len(extra))
+    v = v * 0.5
+    slopes = _bloom_slopes(8).to(device)
+    kw = dict(cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=max(q_lens), max_seqlen_k=max(k_lens),
+              causal=True, alibi_slopes=slopes)
     ref_kw = dict(causal=True, alibi=slopes)
-    if extra == "softcap":
+    if "softcap" in extra:
         kw["softcap"] = ref_kw["softcap"] = 5.0
-    elif extra == "window":
-        kw["window_size"] = ref_kw["window"] = (64, 0)
-    else:
-        k, v = k.to(torch.float8_e4m3fn), v.to(torch.float8_e4m3fn)
-    assert not _route(q, k, v, **kw)
+    if "window" in extra:
+        kw["causal"] = ref_kw["causal"] = False
+        kw["window_size"] = ref_kw["window"] = (48, 16)
+    if extra == "per-request causal":
+        flags = torch.tensor([True, False, True], device=device)
+        kw["causal"], ref_kw["causal"] = flags, flags
+    if extra.startswith("fp8"):
+        k, v = (k * 4).to(torch.float8_e4m3fn), (v * 4).to(torch.float8_e4m3fn)
+        desc = torch.full((3, 2), 0.25, device=device)
+        kw["k_descale"] = kw["v_descale"] = ref_kw["k_descale"] = ref_kw["v_descale"] = desc
+    assert _route(q, k, v, **kw)
     out, lse = attention(q, k, v, **kw)
     ref, ref_lse = oracle_attention(q, k, v, cuq, cuk, **ref_kw)
+    assert_parity(out, lse, ref, ref_lse, dtype)
+
+
+@pytest.mark.parametrize("scale", [-0.09, 0.0])
+@pytest.mark.parametrize("cap", [0.0, 5.0])
+def test_alibi_with_negative_or_zero_score_scale(device, scale, cap):
+    """A negative scale flips Q's signs; a zero scale leaves the scores equal
+    to the biases alone (the folded bias then uses a unit scale)."""
+    q_lens = [64, 200]
+    q, k, v, cuq, cuk = _case(device, torch.bfloat16, 128, 4, 2, q_lens, q_lens, seed=13)
+    v = v * 0.5
+    slopes = torch.tensor([0.05, 0.1, 0.2, 0.4], device=device)
+    kw = dict(cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=200, max_seqlen_k=200, causal=True,
+              alibi_slopes=slopes, softmax_scale=scale, softcap=cap)
+    assert _route(q, k, v, **kw)
+    out, lse = attention(q, k, v, **kw)
+    ref, ref_lse = oracle_attention(q, k, v, cuq, cuk, causal=True, alibi=slopes, scale=scale, softcap=cap)
+    assert_parity(out, lse, ref, ref_lse, torch.bfloat16)
+
+
+def test_alibi_combinations_on_padded_dims_use_generic_kernel(device):
+    """Padded head dims (72 runs in the 128-dim tile) keep ALiBi with a
+    softcap or window on the generic kernel; the result still matches."""
+    q_lens = [70, 300]
+    q, k, v, cuq, cuk = _case(device, torch.float16, 72, 4, 2, q_lens, q_lens, seed=11)
+    slopes = torch.tensor([0.05, 0.1, 0.2, 0.4], device=device)
+    kw = dict(cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=300, max_seqlen_k=300, causal=True,
+              alibi_slopes=slopes, softcap=5.0)
+    assert not _route(q, k, v, **kw)
+    out, lse = attention(q, k, v, **kw)
+    ref, ref_lse = oracle_attention(q, k, v, cuq, cuk, causal=True, alibi=slopes, softcap=5.0)
     assert_parity(out, lse, ref, ref_lse, torch.float16)
