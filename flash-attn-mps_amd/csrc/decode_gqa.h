@@ -106,10 +106,10 @@ FA_DEV void wait_dma_groups(int n) {
 }
 
 // KT: K/V storage type, T or E4M3.  E4M3 slots hold the raw K rows (16 rows
-// x D bytes, rows at sigma(r), 16-byte chunks XOR-swizzled), the raw V rows
-// (staging) and the V rows widened exactly to T (the 16-bit slot's V part):
-// K operands widen in registers after an 8-byte LDS read, V is widened in
-// LDS once per group, and the descales scale the scores and the output.
+// x D bytes, rows at sigma(r), 16-byte chunks XOR-swizzled) and the raw V
+// rows (16 x D bytes, chunks XOR-swizzled): K operands widen in registers
+// after an 8-byte LDS read, V^T comes through ds_read_b64_tr_b8 and widens in
+// registers the same way, and the descales scale the scores and the output.
 template <typename T, int D, bool CAP, typename KT = T>
 __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_attn_args a, const int span) {
   static_assert(D == 64 || D == 128, "head dims 64 and 128");
@@ -268,9 +268,12 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   // Pages of this wave's groups, 64 at a time: lane l of `pages` holds the
   // block-table entry of group 64 chunk + l (0 for groups with no key of the
   // split), read once per chunk with one vector load; each group then takes
-  // its entry with v_readlane instead of a scalar load and its wait.  Every
-  // load of the wave has landed when a chunk is read (before the first DMA,
-  // or after a stage's DMAs were waited for), so the wait is free.
+  // its entry with v_readlane instead of a scalar load and its wait.  The
+  // load is waited for with vmcnt(0): free for the first chunk (before any
+  // DMA); a wave with more than 64 groups (over 4096 keys per workgroup, e.g.
+  // one split per request on long contexts) reloads mid-loop, where that
+  // wait also drains the DMAs of the stages it already has in flight, once
+  // per 32 of its stages.
   int chunk = -1;
   uint32_t pages = 0;
   auto page_of_group = [&](int j) {

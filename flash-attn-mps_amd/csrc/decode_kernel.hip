@@ -153,6 +153,8 @@ bool chunk_aligned(const void* p, const int64_t* st, int nstrides, int esz, int 
 }
 
 DecodeKernel select_decode(const fa_attn_args& a, int* gt_out) {
+  // The head-group arithmetic below divides by heads_k.
+  if (a.heads_k < 1 || a.heads_q < 1 || a.heads_q % a.heads_k) return nullptr;
   if (a.max_seqlen_q > 1) return nullptr;   // one query row per request
   if (a.k_dtype != a.v_dtype) return nullptr;
   if (a.mask_kind != 0) return nullptr;
@@ -334,13 +336,13 @@ extern "C" int fa_decode_fwd_noalloc(const fa_attn_args* in, void* stream) {
   fa_attn_args a = *in;
   constexpr int64_t cap = FA_DECODE_SCRATCH_BYTES / (int64_t)sizeof(float);
   if (a.num_splits == 0) {
+    FA_REQUIRE(a.batch >= 1 && a.heads_k >= 1 && a.heads_q % a.heads_k == 0,
+               "fa_decode_fwd_noalloc: bad batch/head counts");
     int gt = 1;
     if (!pick_decode_gqa(a).kern && !select_decode(a, &gt)) {
       fa_set_error("fa_decode_fwd_noalloc: unsupported dtype/head-dim/stride combination");
       return FA_ERR_UNSUPPORTED;
     }
-    FA_REQUIRE(a.batch >= 1 && a.heads_k >= 1 && a.heads_q % a.heads_k == 0,
-               "fa_decode_fwd_noalloc: bad batch/head counts");
     plan_splits(a, gt, cap, &a.num_splits, &a.split_span);
   }
   int rc = fa_validate_attn(&a, "fa_decode_fwd_noalloc");

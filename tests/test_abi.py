@@ -63,8 +63,25 @@ def test_noalloc_decode_rejects_bad_arguments_before_any_hip_call():
     a.partial_out = 4096                    # partials are library-owned
     assert lib.fa_decode_fwd_noalloc(ctypes.byref(a), None) == 1
     assert b"library-owned" in lib.fa_last_error()
-    a.partial_out, a.num_splits = None, 0   # library plan: unsupported layout
+    a.partial_out, a.num_splits = None, 0   # library plan: bad head counts, then an unsupported layout
+    assert lib.fa_decode_fwd_noalloc(ctypes.byref(a), None) == 1
+    assert b"head counts" in lib.fa_last_error()
+    a.batch = a.heads_q = a.heads_k = 1
     assert lib.fa_decode_fwd_noalloc(ctypes.byref(a), None) == 2
+
+
+def test_zero_kv_heads_are_refused_not_divided_by():
+    """A supported-looking decode layout with heads_k = 0: the support query
+    answers 0 and the no-allocation entry point returns FA_ERR_INVALID (the
+    head-group arithmetic divides by heads_k)."""
+    lib = _lib.load()
+    a = _lib.AttnArgs()
+    a.q_dtype = a.k_dtype = a.v_dtype = a.out_dtype = _lib.BF16
+    a.head_dim_qk = a.head_dim_v = 128
+    a.q_stride[2] = a.out_stride[2] = a.k_stride[3] = a.v_stride[3] = 1
+    a.batch, a.heads_q, a.heads_k, a.max_seqlen_q = 1, 8, 0, 1
+    assert not _lib.supported("fa_decode_supported", a)
+    assert lib.fa_decode_fwd_noalloc(ctypes.byref(a), None) == 1
 
 
 def test_supported_queries_reject_unsupported_combinations():

@@ -51,6 +51,20 @@ def test_config2_every_row(device):
     print(f"config 2: max |out - oracle| {errors[0]:.3e}, max |lse - oracle| {errors[1]:.3e}")
 
 
+def test_config2_lengths_with_unit_normal_values(device):
+    """Config 2's lengths and Q/K with V ~ N(0, 1) (config 2 draws 0.5 N(0, 1);
+    doubling is exact in bf16): the MFMA kernel rounds the softmax weights to
+    bf16 before P.V, which bounds a row's error by about 2^-8 max|v|; every
+    row still meets the 1e-2 bar."""
+    c = bench.config2_inputs(device)
+    q, k, v, cu, lengths = c["q"], c["k"], c["v"] * 2, c["cu"], c["lengths"]
+    out, lse = flash_attn_varlen_func(q, k, v, cu, cu, max(lengths), max(lengths), causal=True,
+                                      return_softmax_lse=True)
+    ref, ref_lse = oracle_attention(q, k, v, cu, cu, causal=True, dtype=torch.float32, chunk=2048)
+    errors = assert_parity(out, lse, ref, ref_lse, torch.bfloat16, what="config 2, V ~ N(0, 1)")
+    print(f"config 2 with N(0,1) V: max |out - oracle| {errors[0]:.3e}, max |lse - oracle| {errors[1]:.3e}")
+
+
 def test_config3_every_request(device):
     """All 64 single-query requests over 512-32768 keys in permuted 16-token pages."""
     c = bench.config3_inputs(device)

@@ -5,8 +5,8 @@ queries, E4M3 K/V (packed or paged), per-(request, KV head) descales,
 score = scale * q_descale * k_descale * q.k and output * v_descale
 (flash_attn_mps/kernels/attention.metal:47-51, 170-180).  The kernel widens
 the E4M3 codes to the query dtype exactly, so the bars are those of the
-16-bit path: max-abs <= 1e-2 bf16 / 2e-3 fp16, LSE <= 1e-4 (rows that see at
-least 32 keys; all rows within the reference's own tolerance).
+16-bit path: max-abs <= 1e-2 bf16 / 2e-3 fp16, LSE <= 1e-4, on every row
+(-inf LSE where a row sees no key).
 """
 import pytest
 import torch
@@ -33,18 +33,6 @@ def _quantize(x, scale_per_token_head):
     """x / scale rounded to E4M3 (the cache holds codes, the descale restores)."""
     return (x / scale_per_token_head).to(E4M3)
 
-
-def _rows_with_keys(q_lens, k_lens, minimum=32, window=-1):
-    rows, start = [], 0
-    for n, m in zip(q_lens, k_lens):
-        for i in range(n):
-            seen = m - n + i + 1
-            if window >= 0:
-                seen = min(seen, window + 1)
-            if seen >= minimum:
-                rows.append(start + i)
-        start += n
-    return torch.tensor(rows, dtype=torch.long)
 
 
 def _packed(device, dtype, d, hq, hkv, q_lens, k_lens, seed, qscale=0.5):
@@ -82,8 +70,6 @@ def test_fp8_prefill_packed(device, dtype, d, causal):
     out, lse = attention(q, k, v, **kw)
     ref, ref_lse = oracle_attention(q, k, v, cuq, cuk, causal=causal, k_descale=ks, v_descale=vs)
     assert_parity(out, lse, ref, ref_lse, dtype)
-    rows = _rows_with_keys(q_lens, k_lens) if causal else None
-    assert_parity(out, lse, ref, ref_lse, dtype, rows=rows)
 
 
 def test_fp8_prefill_q_descale_and_broadcast_strides(device):
@@ -98,7 +84,7 @@ def test_fp8_prefill_q_descale_and_broadcast_strides(device):
     out, lse = attention(q, k, v, cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=256, max_seqlen_k=1000,
                          causal=True, q_descale=qs, k_descale=ks, v_descale=vs)
     ref, ref_lse = oracle_attention(q, k, v, cuq, cuk, causal=True, q_descale=qs, k_descale=ks, v_descale=vs)
-    assert_parity(out, lse, ref, ref_lse, torch.bfloat16, rows=_rows_with_keys(q_lens, k_lens))
+    assert_parity(out, lse, ref, ref_lse, torch.bfloat16)
     assert_parity(out, lse, ref, ref_lse, torch.bfloat16)
 
 
@@ -112,7 +98,7 @@ def test_fp8_prefill_without_descales(device):
     cu = offsets(q_lens, device)
     out, lse = attention(q, k, v, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=200, max_seqlen_k=200, causal=True)
     ref, ref_lse = oracle_attention(q, k, v, cu, cu, causal=True)
-    assert_parity(out, lse, ref, ref_lse, torch.float16, rows=_rows_with_keys(q_lens, q_lens))
+    assert_parity(out, lse, ref, ref_lse, torch.float16)
 
 
 @pytest.mark.parametrize("page", [16, 256])
@@ -149,7 +135,7 @@ def test_fp8_prefill_paged_poisoned_tail(device, page, d):
     ref, ref_lse = oracle_attention(q, kq, vq, cuq, used_k=used, block_table=table, causal=True,
                                        k_descale=ks, v_descale=vs)
     assert_parity(out, lse, ref, ref_lse, torch.bfloat16)
-    assert_parity(out, lse, ref, ref_lse, torch.bfloat16, rows=_rows_with_keys(q_lens, k_lens))
+    assert_parity(out, lse, ref, ref_lse, torch.bfloat16)
 
 
 @pytest.mark.parametrize("window", [(-1, -1), (127, 0), (40, -1)])
@@ -166,8 +152,7 @@ def test_fp8_prefill_softcap_window_sinks(device, window, cap):
     ref, ref_lse = oracle_attention(q, k, v, cuq, cuk, causal=True, window=window, softcap=cap,
                                        sinks=sinks.cpu(), k_descale=ks, v_descale=vs)
     assert_parity(out, lse, ref, ref_lse, torch.bfloat16)
-    assert_parity(out, lse, ref, ref_lse, torch.bfloat16,
-                      rows=_rows_with_keys(q_lens, k_lens, window=window[0]))
+    assert_parity(out, lse, ref, ref_lse, torch.bfloat16)
 
 
 def test_fp8_vllm_mixed_batch_into_caller_out(device):
@@ -192,9 +177,7 @@ def test_fp8_vllm_mixed_batch_into_caller_out(device):
                                 causal=True, k_descale=desc, v_descale=desc, out=out)
     ref, _ = oracle_attention(q, kc, vc, cuq, used_k=used, block_table=table, causal=True,
                                  k_descale=desc, v_descale=desc)
-    rows = _rows_with_keys(q_lens, k_lens)
-    err = (out.float().cpu()[rows] - ref.float()[rows]).abs().max().item()
-    assert err <= 1e-2, err
+    assert_parity(out, None, ref, None, torch.bfloat16)
 
 
 def test_fp8_prefill_unsupported_dims_fall_back(device):

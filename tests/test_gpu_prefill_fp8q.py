@@ -7,9 +7,8 @@ from v_mfma_f32_32x32x64_f8f6f4: E4M3 x E4M3 products are exact in fp32 and
 the dot is accumulated in fp32, so S carries the same error as the 16-bit
 path; q_descale * k_descale joins the softmax scale and v_descale scales the
 output (flash_attn_mps/kernels/attention.metal:47-51, 170-180).  V is widened
-exactly to the output's 16-bit type for P.V.  Bars: max-abs <= 1e-2 bf16 /
-2e-3 fp16, LSE <= 1e-4 (rows that see at least 32 keys; all rows within the
-output bar).
+exactly to the output's 16-bit type for P.V.  Bars, on every row: max-abs
+<= 1e-2 bf16 / 2e-3 fp16, LSE <= 1e-4 (-inf where a row sees no key).
 """
 import pytest
 import torch
@@ -24,18 +23,6 @@ E4M3 = torch.float8_e4m3fn
 # Every finite E4M3FN code: all bytes but 0x7F and 0xFF (the NaNs).
 FINITE_CODES = torch.tensor([c for c in range(256) if c & 0x7F != 0x7F], dtype=torch.uint8)
 
-
-def _rows_with_keys(q_lens, k_lens, minimum=32, window=-1):
-    rows, start = [], 0
-    for n, m in zip(q_lens, k_lens):
-        for i in range(n):
-            seen = m - n + i + 1
-            if window >= 0:
-                seen = min(seen, window + 1)
-            if seen >= minimum:
-                rows.append(start + i)
-        start += n
-    return torch.tensor(rows, dtype=torch.long)
 
 
 def _route_is_mfma(q, k, v, out_dtype, **kw):
@@ -91,9 +78,7 @@ def test_fp8q_prefill_packed(device, out_dtype, d, causal):
     out = torch.empty(q.shape[0], 8, d, dtype=out_dtype, device=device)
     out, lse = attention(q, k, v, out=out, **kw)
     ref, ref_lse = oracle_attention(q, k, v, cuq, cuk, causal=causal, q_descale=qs, k_descale=ks, v_descale=vs)
-    assert_parity(out, None, ref, None, out_dtype)
-    rows = _rows_with_keys(q_lens, k_lens) if causal else None
-    assert_parity(out, lse, ref, ref_lse, out_dtype, rows=rows)
+    assert_parity(out, lse, ref, ref_lse, out_dtype)
 
 
 def test_fp8q_default_output_is_fp16(device):
@@ -103,7 +88,7 @@ def test_fp8q_default_output_is_fp16(device):
                          causal=True, q_descale=qs, k_descale=ks, v_descale=vs)
     assert out.dtype == torch.float16
     ref, ref_lse = oracle_attention(q, k, v, cuq, cuk, causal=True, q_descale=qs, k_descale=ks, v_descale=vs)
-    assert_parity(out, lse, ref, ref_lse, torch.float16, rows=_rows_with_keys([200], [200]))
+    assert_parity(out, lse, ref, ref_lse, torch.float16)
 
 
 @pytest.mark.parametrize("d", [64, 128, 256])
@@ -134,9 +119,7 @@ def test_fp8q_all_finite_codes(device, d):
             out, lse = attention(q, k, v, out=out, **kw)
             ref, ref_lse = oracle_attention(q, k, v, cu, cu, causal=causal, q_descale=desc, k_descale=desc,
                                             v_descale=vdesc)
-            assert_parity(out, None, ref, None, out_dtype, what=f"d{d} {out_dtype} causal={causal}")
-            rows = _rows_with_keys([n], [n]) if causal else None
-            assert_parity(out, lse, ref, ref_lse, out_dtype, rows=rows, what=f"d{d} {out_dtype} causal={causal}")
+            assert_parity(out, lse, ref, ref_lse, out_dtype, what=f"d{d} {out_dtype} causal={causal}")
 
 
 @pytest.mark.parametrize("page", [16, 256])
@@ -175,7 +158,7 @@ def test_fp8q_prefill_paged_poisoned_tail(device, page, d):
     ref, ref_lse = oracle_attention(q, kq, vq, cuq, used_k=used, block_table=table, causal=True,
                                     q_descale=qs, k_descale=ks, v_descale=vs)
     assert_parity(out, None, ref, None, torch.bfloat16)
-    assert_parity(out, lse, ref, ref_lse, torch.bfloat16, rows=_rows_with_keys(q_lens, k_lens))
+    assert_parity(out, lse, ref, ref_lse, torch.bfloat16)
 
 
 @pytest.mark.parametrize("window", [(-1, -1), (127, 0), (40, -1)])
@@ -195,7 +178,7 @@ def test_fp8q_prefill_softcap_window_sinks(device, window, cap):
     ref, ref_lse = oracle_attention(q, k, v, cuq, cuk, causal=True, window=window, softcap=cap,
                                     sinks=sinks.cpu(), q_descale=qs, k_descale=ks, v_descale=vs)
     assert_parity(out, None, ref, None, torch.bfloat16)
-    assert_parity(out, lse, ref, ref_lse, torch.bfloat16, rows=_rows_with_keys(q_lens, k_lens, window=window[0]))
+    assert_parity(out, lse, ref, ref_lse, torch.bfloat16)
 
 
 def test_fp8q_mixed_batch_with_single_query_requests(device):
@@ -222,7 +205,7 @@ def test_fp8q_mixed_batch_with_single_query_requests(device):
     ref, ref_lse = oracle_attention(q, kc, vc, cuq, used_k=used, block_table=table, causal=True,
                                     q_descale=qdesc, k_descale=desc, v_descale=desc)
     assert_parity(out, None, ref, None, torch.bfloat16)
-    assert_parity(out, lse, ref, ref_lse, torch.bfloat16, rows=_rows_with_keys(q_lens, k_lens))
+    assert_parity(out, lse, ref, ref_lse, torch.bfloat16)
 
 
 def test_fp8q_unsupported_dims_take_the_generic_kernel(device):
@@ -254,4 +237,4 @@ def test_fp8q_negative_scale_and_descales(device):
                                     k_descale=ks, v_descale=vs)
     assert torch.isfinite(out).all()
     assert_parity(out, None, ref, None, torch.bfloat16)
-    assert_parity(out, lse, ref, ref_lse, torch.bfloat16, rows=_rows_with_keys(q_lens, k_lens))
+    assert_parity(out, lse, ref, ref_lse, torch.bfloat16)

@@ -5,10 +5,9 @@ GQA 1-4 query heads per KV head, head dims 64/128/256 or DIFFKV 192/128,
 bf16/fp16, packed or paged (16/64-token pages) K/V, causal or not, left/right
 windows, softcap, sinks, a positive or negative softmax scale and, for 16-bit
 128-dim heads, E4M3 K/V with descales, then runs it through the public
-router (MFMA prefill, mixed batch or generic kernel) at the parity bar: fp16
-2e-3, bf16 1e-2, LSE 1e-4 on rows that see at least 32 keys (rows that see
-fewer are held to the output bar only: one or two bf16-rounded weights carry
-the whole row).  V is drawn as 0.5 N(0, 1), as in config 2.
+router (MFMA prefill, mixed batch or generic kernel) at the parity bar on
+every row: fp16 2e-3, bf16 1e-2, LSE 1e-4 (-inf where a row sees no key).
+V is drawn as 0.5 N(0, 1), as in config 2.
 """
 import random
 
@@ -37,18 +36,6 @@ def _draw(seed):
         c["causal"] = False
     return c
 
-
-def _rows_with_keys(c, minimum=32):
-    rows, start = [], 0
-    for n, m in zip(c["q_lens"], c["k_lens"]):
-        for i in range(n):
-            seen = m - n + i + 1 if c["causal"] else m
-            if c["window"][0] >= 0:
-                seen = min(seen, c["window"][0] + 1)
-            if seen >= minimum:
-                rows.append(start + i)
-        start += n
-    return torch.tensor(rows, dtype=torch.long)
 
 
 @pytest.mark.parametrize("seed", range(40))
@@ -96,5 +83,4 @@ def test_random_prefill_case(device, seed):
     ref, ref_lse = oracle_attention(q, k, v, cu_q, causal=c["causal"], window=c["window"], softcap=c["cap"],
                                     sinks=sinks, scale=scale, k_descale=kd, v_descale=vd, chunk=512, **okw)
     what = str({key: val for key, val in c.items() if key != "dtype"})
-    assert_parity(out, None, ref, None, what=what)
-    assert_parity(out, lse, ref, ref_lse, rows=_rows_with_keys(c), what=what)
+    assert_parity(out, lse, ref, ref_lse, what=what)
