@@ -558,10 +558,15 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
       store_any(a.out, tq * a.out_stride[0] + (int64_t)h * a.out_stride[1] + (int64_t)d * a.out_stride[2], a.out_dtype, O);
       if (d == 0) a.lse[(int64_t)h * a.lse_stride[0] + tq * a.lse_stride[1]] = cl[hc];
     } else {
-      // Partial rows [batch][ntok][Hq][S] (one token: [batch][Hq][S]).
-      const int64_t row = ((b * ntok + tt) * a.heads_q + h) * S + split;
-      a.partial_out[row * D + d] = O;
-      if (d == 0) a.partial_lse[row] = cl[hc];
+      // Partial outputs [batch][S][ntok][Hq][D], LSEs [batch][ntok][Hq][S].
+      // A workgroup's outputs are ntok runs of 4 D nheads bytes, and the
+      // workgroups running together (neighbouring heads and splits of one
+      // request) fill neighbouring runs; streaming stores keep the partials
+      // from displacing K/V in the caches.  Interleaved 4 D-byte rows (the
+      // splits of one row together) cost config 3's speculative step ~6%.
+      const int64_t orow = ((b * S + split) * ntok + tt) * a.heads_q + h;
+      __builtin_nontemporal_store(O, &a.partial_out[orow * D + d]);
+      if (d == 0) a.partial_lse[((b * ntok + tt) * a.heads_q + h) * S + split] = cl[hc];
     }
   }
 }

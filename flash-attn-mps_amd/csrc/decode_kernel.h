@@ -571,9 +571,10 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
                 O * norm);
       if (d == 0) a.lse[(int64_t)h * a.lse_stride[0] + tq * a.lse_stride[1]] = lse;
     } else {
-      const int64_t row = (b * a.heads_q + h) * S + split;
-      a.partial_out[row * DVT + d] = O * norm;
-      if (d == 0) a.partial_lse[row] = lse;
+      // Partial outputs [batch][S][Hq][Dv], LSEs [batch][Hq][S], as the
+      // matrix-core decode writes them (streaming stores, split-major rows).
+      __builtin_nontemporal_store(O * norm, &a.partial_out[((b * S + split) * a.heads_q + h) * DVT + d]);
+      if (d == 0) a.partial_lse[(b * a.heads_q + h) * S + split] = lse;
     }
   }
 }

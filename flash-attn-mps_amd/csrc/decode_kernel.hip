@@ -46,8 +46,11 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const fa_attn_args a,
   const int DV = (int)a.head_dim_v;
   const int n = r.k_len - decode_vis_begin(a, r.k_len, r.q_len);
   const int nv = n > 0 ? min(S, (n + span - 1) / span) : 1;
+  // Partial outputs [batch][S][ntok][Hq][Dv]: this row's splits are pitch
+  // floats apart; LSEs [batch][ntok][Hq][S] contiguous.
+  const int64_t rows_b = (int64_t)ntok * a.heads_q, pitch = rows_b * DV;
   const float* plse = a.partial_lse + row * S;
-  const float* po = a.partial_out + row * S * DV;
+  const float* po = a.partial_out + (b * S * rows_b + (row - b * rows_b)) * DV;
   // A zero-weight split (empty, its partial never written) is read like the
   // others but dropped by a select, so its contents never reach the sum.
   float x0[GROUP][DIMS];
@@ -55,7 +58,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const fa_attn_args a,
   for (int u = 0; u < GROUP; ++u)
 #pragma unroll
     for (int k = 0; k < DIMS; ++k)
-      x0[u][k] = u < nv && lane + 64 * k < DV ? po[(int64_t)u * DV + lane + 64 * k] : 0.0f;
+      x0[u][k] = u < nv && lane + 64 * k < DV ? po[(int64_t)u * pitch + lane + 64 * k] : 0.0f;
   const float lse0 = lane < nv ? plse[lane] : -INFINITY;
   float peak = lse0;
   for (int s = lane + 64; s < nv; s += 64) peak = fmaxf(peak, plse[s]);
@@ -84,7 +87,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const fa_attn_args a,
 #pragma unroll
       for (int u = 0; u < GROUP; ++u) {
         ws[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j + u));
-        const float* src = po + (int64_t)(s0 + j + u) * DV;
+        const float* src = po + (int64_t)(s0 + j + u) * pitch;
 #pragma unroll
         for (int k = 0; k < DIMS; ++k) x[u][k] = lane + 64 * k < DV ? src[lane + 64 * k] : 0.0f;
       }
@@ -96,7 +99,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const fa_attn_args a,
     for (; j < cnt; ++j) {
       const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
       if (ws > 0.0f) {   // zero-weight splits are never read
-        const float* src = po + (int64_t)(s0 + j) * DV;
+        const float* src = po + (int64_t)(s0 + j) * pitch;
 #pragma unroll
         for (int k = 0; k < DIMS; ++k)
           if (lane + 64 * k < DV) acc[k] = fmaf(ws, src[lane + 64 * k], acc[k]);
@@ -210,7 +213,8 @@ extern "C" int fa_decode_supported(const fa_attn_args* a) {
 
 namespace {
 
-// Partial rows: [batch][max_seqlen_q][Hq] (x [splits][Dv] and x [splits]).
+// Partial rows: [batch][max_seqlen_q][Hq] (outputs [batch][splits][rows][Dv],
+// LSEs [batch][rows][splits]).
 int64_t partial_rows(const fa_attn_args& a) {
   return a.batch * (a.max_seqlen_q > 1 ? a.max_seqlen_q : 1) * a.heads_q;
 }

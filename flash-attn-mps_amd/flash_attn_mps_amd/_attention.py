@@ -171,7 +171,7 @@ def _mixed_batch(p, a, fixed_order=False):
     splits, span = split_plan(p.batch, groups, p.max_k, 1 if fixed_order else 0)
     dec.num_splits, dec.split_span = splits, span
     if splits > 1:
-        _partials(p, dec, (p.batch, p.heads, splits, p.dim_v), (p.batch, p.heads, splits))
+        _partials(p, dec, (p.batch, splits, p.heads, p.dim_v), (p.batch, p.heads, splits))
     main = torch.cuda.current_stream(p.device)
     side = _side_stream(p.device)
     side.wait_stream(main)

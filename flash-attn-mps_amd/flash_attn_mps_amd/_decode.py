@@ -119,8 +119,8 @@ def decode_rows(p, out):
 
 def _run_split_kv(p, a, rows, splits=None):
     """fa_decode_fwd with the split plan (or `splits` splits) and partials
-    [batch][rows][Hq][S]; False when the decode kernels do not take the
-    arguments."""
+    (outputs [batch][S][rows][Hq][Dv], LSEs [batch][rows][Hq][S]); False when
+    the decode kernels do not take the arguments."""
     if not _lib.supported("fa_decode_supported", a):
         return False
     groups = workgroups_per_token(p.heads, p.kv_heads, p.dim_qk, p.dim_v, uses_gqa_kernel(p, rows), rows)
@@ -129,6 +129,6 @@ def _run_split_kv(p, a, rows, splits=None):
     splits, span = split_plan(p.batch, groups, visible, splits or p.splits)
     a.num_splits, a.split_span = splits, span
     if splits > 1:
-        _partials(p, a, (p.batch, rows, p.heads, splits, p.dim_v), (p.batch, rows, p.heads, splits))
+        _partials(p, a, (p.batch, splits, rows, p.heads, p.dim_v), (p.batch, rows, p.heads, splits))
     _lib.call("fa_decode_fwd", a, p.device)
     return True

@@ -163,7 +163,7 @@ typedef struct fa_attn_args {
                                         window_left + R) (window_left < 0: max_seqlen_k),
                                         R = max(1, max_seqlen_q) */
   float* partial_out;                /* num_splits > 1: caller-owned fp32 workspace,
-                                        fa_decode_fwd [batch, R, Hq, S, Dv] contiguous,
+                                        fa_decode_fwd [batch, S, R, Hq, Dv] contiguous,
                                         fa_attn_fwd [S, total_q, Hq, Dv] contiguous */
   float* partial_lse;                /* fa_decode_fwd [batch, R, Hq, S], fa_attn_fwd [S, Hq, total_q] */
 
@@ -216,7 +216,7 @@ int fa_rotary(const fa_rotary_args* args, void* stream);
  * windows bottom-right aligned), on the matrix-core kernel only --
  * fa_decode_supported says whether it takes the arguments.  Writes out/lse
  * directly when num_splits == 1, otherwise fills partial_out
- * [batch, R, Hq, S, Dv] / partial_lse [batch, R, Hq, S] (R = 1 for one row)
+ * [batch, S, R, Hq, Dv] / partial_lse [batch, R, Hq, S] (R = 1 for one row)
  * and merges. */
 int fa_decode_supported(const fa_attn_args* args);
 int fa_decode_fwd(const fa_attn_args* args, void* stream);

@@ -82,7 +82,7 @@ def _decode_fwd(t):
     a.num_splits, a.split_span = splits, span
     batch, heads, dim = t["q"].shape
     if splits > 1:
-        po = torch.empty(batch, heads, splits, dim, dtype=torch.float32, device=out.device)
+        po = torch.empty(batch, splits, heads, dim, dtype=torch.float32, device=out.device)
         pl = torch.empty(batch, heads, splits, dtype=torch.float32, device=out.device)
         keep += [po, pl]
         a.partial_out, a.partial_lse = po.data_ptr(), pl.data_ptr()
