@@ -250,3 +250,52 @@ def test_fp32_output_keeps_fp32_accuracy(device, heads, kv_heads):
     got, lse = decode_attention(q, kc, vc, max_seqlen_k=cols * page, out=out, **kw)
     ref, ref_lse = oracle_attention(q, kc, vc, cu_q, used_k=used, block_table=table)
     assert_parity(got, lse, ref, ref_lse)
+
+
+def _work_order_lengths(batch, seed):
+    """Contexts of 0 keys, exact multiples of the spans the split plan picks
+    (no short last split), one key either side of them, and random lengths,
+    shuffled over the batch."""
+    g = torch.Generator().manual_seed(seed)
+    fixed = [0, 1, 127, 128, 129, 256, 384, 512, 513, 1023, 1024, 1025]
+    lengths = [fixed[b] if b < len(fixed) else int(torch.randint(0, 700, (1,), generator=g)) for b in range(batch)]
+    return [lengths[i] for i in torch.randperm(batch, generator=g).tolist()], g
+
+
+@pytest.mark.parametrize("batch", [63, 64, 65, 130, 256, 257, 300])
+@pytest.mark.parametrize("splits", [0, 1, 4])
+def test_work_order_across_request_counts(device, batch, splits):
+    """The kernel hands its (split, request) slots out longest first for up
+    to 256 requests (64 per pass of a wave) and in grid order past that; with
+    full splits, short last splits of every length class, empty requests and
+    unused slots in one launch, each request's result must land in its own
+    rows (a sentinel-filled output shows any slot stored twice or never)."""
+    heads, kv_heads, d, page = 8, 2, 64, 16
+    lengths, g = _work_order_lengths(batch, 790 + batch + splits)
+    kc, vc, table, cols = _pool(lengths, page, kv_heads, d, torch.bfloat16, device, 791 + batch, [0] * batch)
+    q = torch.randn(batch, heads, d, generator=g).to(torch.bfloat16).to(device)
+    cu_q, used = torch.arange(batch + 1, device=device, dtype=torch.int32), _i32(lengths, device)
+    buffer = torch.full((batch, heads + 4, d), 7.0, device=device, dtype=torch.bfloat16)
+    kw = dict(cu_seqlens_q=cu_q, seqused_k=used, block_table=table)
+    assert uses_gqa_kernel(problem(q, kc, vc, max_seqlen_q=1, max_seqlen_k=cols * page, **kw))
+    got, lse = decode_attention(q, kc, vc, max_seqlen_k=cols * page, num_splits=splits, out=buffer[:, :heads], **kw)
+    ref, ref_lse = oracle_attention(q, kc, vc, cu_q, used_k=used, block_table=table)
+    assert_parity(got, lse, ref, ref_lse)
+    assert (buffer[:, heads:] == 7.0).all(), "a head slot past the call was stored"
+
+
+@pytest.mark.parametrize("batch", [70, 256, 260])
+def test_rows_work_order_with_empty_requests(device, batch):
+    """Multi-row calls over many requests, some with no query row (no slot
+    at all) and some with fewer keys than rows."""
+    heads, kv_heads, d, page = 16, 4, 128, 16
+    lengths, g = _work_order_lengths(batch, 795 + batch)
+    q_lens = torch.randint(0, 5, (batch,), generator=g).tolist()
+    q_lens[0] = 4
+    kc, vc, table, cols = _pool(lengths, page, kv_heads, d, torch.bfloat16, device, 796 + batch, [0] * batch)
+    q = torch.randn(sum(q_lens), heads, d, generator=g).to(torch.bfloat16).to(device)
+    used = _i32(lengths, device)
+    kw = dict(seqused_k=used, block_table=table, causal=True)
+    (got, lse), cu_q = _rows_call(q, kc, vc, q_lens, max_seqlen_k=cols * page, **kw)
+    ref, ref_lse = oracle_attention(q, kc, vc, cu_q, used_k=used, block_table=table, causal=True)
+    assert_parity(got, lse, ref, ref_lse)
