@@ -105,116 +105,6 @@ FA_DEV void wait_dma_groups(int n) {
   }
 }
 
-// Work order of the split workgroups.  The grid holds S x batch slots per
-// head tile; slot w = blockIdx.y + S blockIdx.z takes, longest first: every
-// split of a full span of keys, request by request, then each request's
-// last, shorter split by decreasing length class (span / 16 keys per class;
-// a request with no visible key has one empty split, class 0), and past the
-// work the slots exit at once.  In plain (split, request) order a request's
-// unused split slots sit among the work (each one a workgroup launch), and
-// the short last splits fall anywhere, so the launch can end on a few full
-// splits started late: measured on config 3 (64 requests, 512-32768 keys)
-// the plain order ran ~4% longer.  A request outside 1..ntok query rows gets
-// no slot, as the merge expects, and no request gets a split past S - 1.
-// Every wave computes the same item from the request metadata (up to
-// GQA_ORDER_CHUNKS x 64 requests, one per lane and chunk, in registers);
-// the chosen request's RequestInfo comes from the lane that loaded it.
-constexpr int GQA_ORDER_CHUNKS = 4;
-constexpr int GQA_CLASSES = 16;
-
-struct GqaItem {
-  RequestInfo r;
-  int64_t b;
-  int split;
-  bool ok;
-};
-
-FA_DEV RequestInfo request_from_lane(const RequestInfo& r, int l) {
-  RequestInfo o;
-  o.q_begin = __builtin_amdgcn_readlane(r.q_begin, l);
-  o.q_len = __builtin_amdgcn_readlane(r.q_len, l);
-  o.k_len = __builtin_amdgcn_readlane(r.k_len, l);
-  o.k_base = __builtin_amdgcn_readlane(r.k_base, l);
-  o.left = __builtin_amdgcn_readlane(r.left, l);
-  o.causal = __builtin_amdgcn_readlane((int)r.causal, l) != 0;
-  return o;
-}
-
-FA_DEV GqaItem gqa_item(const fa_attn_args& a, int ntok, int span, int S, int w) {
-  const int lane = threadIdx.x & 63;
-  const int B = (int)a.batch, nc = (B + 63) / 64;
-  GqaItem it;
-  it.ok = false;
-  it.b = 0;
-  it.split = 0;
-  RequestInfo rq[GQA_ORDER_CHUNKS];
-  int full[GQA_ORDER_CHUNKS], cls[GQA_ORDER_CHUNKS];
-#pragma unroll
-  for (int c = 0; c < GQA_ORDER_CHUNKS; ++c) {
-    full[c] = 0;
-    cls[c] = -1;
-    rq[c] = RequestInfo{0, 0, 0, 0, 0, false};
-    const int q = 64 * c + lane;
-    if (c < nc && q < B) {
-      rq[c] = load_request(a, q);
-      if (rq[c].q_len >= 1 && rq[c].q_len <= ntok) {
-        const int n = max(rq[c].k_len - fa_decode::decode_vis_begin(a, rq[c].k_len, rq[c].q_len), 0);
-        full[c] = min(n / span, S);
-        const int rem = n - full[c] * span;
-        if ((rem > 0 || n == 0) && full[c] < S) cls[c] = (int)((int64_t)rem * GQA_CLASSES / span);
-      }
-    }
-  }
-  // Full splits: the request whose running count passes w.
-  int base = 0;
-#pragma unroll
-  for (int c = 0; c < GQA_ORDER_CHUNKS; ++c) {
-    int incl = full[c];
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int t = __shfl_up(incl, o);
-      if (lane >= o) incl += t;
-    }
-    const uint64_t hit = __ballot(w < base + incl);
-    if (hit) {
-      const int l = __builtin_ctzll(hit);
-      it.r = request_from_lane(rq[c], l);
-      it.b = 64 * c + l;
-      it.split = w - base - (__builtin_amdgcn_readlane(incl, l) - __builtin_amdgcn_readlane(full[c], l));
-      it.ok = true;
-      return it;
-    }
-    base += __builtin_amdgcn_readlane(incl, 63);
-  }
-  // Last splits: longest class first, requests in order within a class.
-  int rest = w - base;
-  int k = GQA_CLASSES - 1;
-  for (; k >= 0; --k) {
-    int n = 0;
-#pragma unroll
-    for (int c = 0; c < GQA_ORDER_CHUNKS; ++c) n += __popcll(__ballot(cls[c] == k));
-    if (rest < n) break;
-    rest -= n;
-  }
-  if (k < 0) return it;
-#pragma unroll
-  for (int c = 0; c < GQA_ORDER_CHUNKS; ++c) {
-    const uint64_t m = __ballot(cls[c] == k);
-    const int n = __popcll(m);
-    if (rest < n) {
-      const uint64_t below = lane ? m & (~0ull >> (64 - lane)) : 0ull;
-      const int l = __builtin_ctzll(__ballot(cls[c] == k && __popcll(below) == rest));
-      it.r = request_from_lane(rq[c], l);
-      it.b = 64 * c + l;
-      it.split = __builtin_amdgcn_readlane(full[c], l);
-      it.ok = true;
-      return it;
-    }
-    rest -= n;
-  }
-  return it;
-}
-
 // KT: K/V storage type, T or E4M3.  E4M3 slots hold the raw K rows (16 rows
 // x D bytes, rows at sigma(r), 16-byte chunks XOR-swizzled) and the raw V
 // rows (16 x D bytes, chunks XOR-swizzled): K operands widen in registers
@@ -249,16 +139,8 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   const int nheads = min(nh, group - t0);
   const int h0 = kh * group + t0;
   const int S = a.num_splits;
-  GqaItem item;
-  if (a.batch <= 64 * GQA_ORDER_CHUNKS) {
-    item = gqa_item(a, ntok, span, S, (int)(blockIdx.y + gridDim.y * blockIdx.z));
-    if (!item.ok) return;
-  } else {
-    item.split = blockIdx.y;
-    item.b = blockIdx.z;
-    item.r = load_request(a, item.b);
-    if (item.r.q_len < 1 || item.r.q_len > ntok) return;
-  }
+  const fa_decode::SplitItem item = fa_decode::split_item(a, ntok, span);
+  if (!item.ok) return;
   const int split = item.split;
   const int64_t b = item.b;
   const RequestInfo r = item.r;

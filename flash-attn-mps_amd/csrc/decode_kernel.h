@@ -201,6 +201,127 @@ FA_DEV int decode_vis_begin(const fa_attn_args& a, int k_len, int q_len = 1) {
   return a.window_left >= 0 ? max(0, k_len - q_len - a.window_left) : 0;
 }
 
+// Work order of the split workgroups (both decode kernels).  The grid
+// holds num_splits x batch slots per head tile; slot w = blockIdx.y +
+// num_splits blockIdx.z takes, longest first: every split of a full span of
+// keys, request by request, then each request's last, shorter split by
+// decreasing length class (span / 16 keys per class; a request with no
+// visible key has one empty split, class 0), and past the work the slots
+// exit at once.  In plain (split, request) order a request's unused split
+// slots sit among the work (each one a workgroup launch), and the short last
+// splits fall anywhere, so the launch can end on a few full splits started
+// late: measured on config 3 (64 requests, 512-32768 keys) the plain order
+// ran ~4% longer.  Requests outside 1..rows query rows get no slot, as the
+// merge expects, and no request gets a split past num_splits - 1.  Every
+// wave computes the same item from the request metadata (up to
+// SPLIT_ORDER_CHUNKS x 64 requests, one per lane and chunk, in registers);
+// the chosen request's RequestInfo comes from the lane that loaded it.
+// Larger batches keep the grid order (split y, request z).
+constexpr int SPLIT_ORDER_CHUNKS = 4;
+constexpr int SPLIT_CLASSES = 16;
+
+struct SplitItem {
+  RequestInfo r;
+  int64_t b;
+  int split;
+  bool ok;
+};
+
+FA_DEV RequestInfo request_from_lane(const RequestInfo& r, int l) {
+  RequestInfo o;
+  o.q_begin = __builtin_amdgcn_readlane(r.q_begin, l);
+  o.q_len = __builtin_amdgcn_readlane(r.q_len, l);
+  o.k_len = __builtin_amdgcn_readlane(r.k_len, l);
+  o.k_base = __builtin_amdgcn_readlane(r.k_base, l);
+  o.left = __builtin_amdgcn_readlane(r.left, l);
+  o.causal = __builtin_amdgcn_readlane((int)r.causal, l) != 0;
+  return o;
+}
+
+FA_DEV SplitItem split_item(const fa_attn_args& a, int rows, int span) {
+  const int S = a.num_splits;
+  SplitItem it;
+  it.ok = false;
+  it.b = 0;
+  it.split = 0;
+  if (a.batch > 64 * SPLIT_ORDER_CHUNKS) {
+    it.split = blockIdx.y;
+    it.b = blockIdx.z;
+    it.r = load_request(a, it.b);
+    it.ok = it.r.q_len >= 1 && it.r.q_len <= rows;
+    return it;
+  }
+  const int w = (int)(blockIdx.y + gridDim.y * blockIdx.z);
+  const int lane = threadIdx.x & 63;
+  const int B = (int)a.batch, nc = (B + 63) / 64;
+  RequestInfo rq[SPLIT_ORDER_CHUNKS];
+  int full[SPLIT_ORDER_CHUNKS], cls[SPLIT_ORDER_CHUNKS];
+#pragma unroll
+  for (int c = 0; c < SPLIT_ORDER_CHUNKS; ++c) {
+    full[c] = 0;
+    cls[c] = -1;
+    rq[c] = RequestInfo{0, 0, 0, 0, 0, false};
+    const int q = 64 * c + lane;
+    if (c < nc && q < B) {
+      rq[c] = load_request(a, q);
+      if (rq[c].q_len >= 1 && rq[c].q_len <= rows) {
+        const int n = max(rq[c].k_len - decode_vis_begin(a, rq[c].k_len, rq[c].q_len), 0);
+        full[c] = min(n / span, S);
+        const int rem = n - full[c] * span;
+        if ((rem > 0 || n == 0) && full[c] < S) cls[c] = (int)((int64_t)rem * SPLIT_CLASSES / span);
+      }
+    }
+  }
+  // Full splits: the request whose running count passes w.
+  int base = 0;
+#pragma unroll
+  for (int c = 0; c < SPLIT_ORDER_CHUNKS; ++c) {
+    int incl = full[c];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_up(incl, o);
+      if (lane >= o) incl += t;
+    }
+    const uint64_t hit = __ballot(w < base + incl);
+    if (hit) {
+      const int l = __builtin_ctzll(hit);
+      it.r = request_from_lane(rq[c], l);
+      it.b = 64 * c + l;
+      it.split = w - base - (__builtin_amdgcn_readlane(incl, l) - __builtin_amdgcn_readlane(full[c], l));
+      it.ok = true;
+      return it;
+    }
+    base += __builtin_amdgcn_readlane(incl, 63);
+  }
+  // Last splits: longest class first, requests in order within a class.
+  int rest = w - base;
+  int k = SPLIT_CLASSES - 1;
+  for (; k >= 0; --k) {
+    int n = 0;
+#pragma unroll
+    for (int c = 0; c < SPLIT_ORDER_CHUNKS; ++c) n += __popcll(__ballot(cls[c] == k));
+    if (rest < n) break;
+    rest -= n;
+  }
+  if (k < 0) return it;
+#pragma unroll
+  for (int c = 0; c < SPLIT_ORDER_CHUNKS; ++c) {
+    const uint64_t m = __ballot(cls[c] == k);
+    const int n = __popcll(m);
+    if (rest < n) {
+      const uint64_t below = lane ? m & (~0ull >> (64 - lane)) : 0ull;
+      const int l = __builtin_ctzll(__ballot(cls[c] == k && __popcll(below) == rest));
+      it.r = request_from_lane(rq[c], l);
+      it.b = 64 * c + l;
+      it.split = __builtin_amdgcn_readlane(full[c], l);
+      it.ok = true;
+      return it;
+    }
+    rest -= n;
+  }
+  return it;
+}
+
 // D / DV: the tile's head dims; DT / DVT <= them: the tensors' own.  Lanes
 // past the real dims read the row's last real chunk (always in bounds), with
 // a zero query there, so they add nothing to Q.K; their V columns are never
@@ -222,9 +343,8 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
   __shared__ float sm_acc[4][GT][DV];
 
   // Head groups are the fastest grid dimension: the workgroups of one
-  // (request, split) run together and read whole token rows of the same pages.
-  const int split = blockIdx.y;
-  const int64_t b = blockIdx.z;
+  // (request, split) run together and read whole token rows of the same pages;
+  // split_item() gives each (split, request) slot its work.
   // The wave index as a scalar: everything the steps derive from it (their
   // positions, whether a step lies wholly inside the split) is then
   // wave-uniform, so the full / partial load paths are scalar branches
@@ -233,8 +353,11 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
   // before computing the current one).
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, rg = lane >> 4, l16 = lane & 15;
-  const RequestInfo r = load_request(a, b);
-  if (r.q_len != 1) return;
+  const SplitItem item = split_item(a, 1, span);
+  if (!item.ok) return;
+  const int split = item.split;
+  const int64_t b = item.b;
+  const RequestInfo r = item.r;
   // Workgroup x holds query heads t GT .. t GT + GT - 1 of KV head kh's group
   // (t = x % tiles, tiles = ceil(group / GT)); a last tile past the group
   // recomputes its last real head in the spare slots and stores nothing there.
