@@ -137,17 +137,25 @@ def _partials(p, a, shape_out, shape_lse):
     a.partial_out, a.partial_lse = po.data_ptr(), pl.data_ptr()
 
 
-_SIDE_STREAMS = {}
+_SIDE = {}
+
+# Below this many K/V bytes (an upper bound of what the decode pass of a
+# mixed batch reads: every request at the longest visible length) the decode
+# pass follows the prefill on the caller's stream: it takes a few µs of GPU
+# time, less than the host time of the cross-stream fork and join (an event
+# record and a stream wait each way, ~30 µs per call measured on short calls).
+_SIDE_STREAM_MIN_BYTES = 64 << 20
 
 
 def _side_stream(device):
     """A second stream per device (default priority) for the decode rows of a
-    mixed batch."""
+    mixed batch, with the two events that fork and join it (reused: a stream
+    wait takes the event's most recent record)."""
     index = torch.device(device).index
-    stream = _SIDE_STREAMS.get(index)
-    if stream is None:
-        stream = _SIDE_STREAMS[index] = torch.cuda.Stream(device)
-    return stream
+    side = _SIDE.get(index)
+    if side is None:
+        side = _SIDE[index] = (torch.cuda.Stream(device), torch.cuda.Event(), torch.cuda.Event())
+    return side
 
 
 def _mixed_batch(p, a, fixed_order=False):
@@ -158,6 +166,8 @@ def _mixed_batch(p, a, fixed_order=False):
     first on the caller's stream and the decode on a side stream that starts
     after the caller's earlier work; the caller's stream then waits for it.
     The memory-bound decode fills the CUs the compute-bound prefill leaves.
+    Small calls (under _SIDE_STREAM_MIN_BYTES of K/V) run both on the
+    caller's stream, one after the other.
     Returns False (nothing launched) when the decode kernel cannot take the
     single-query rows.  With `fixed_order` the decode runs one split per
     request, so each single-query row is reduced in an order of its own
@@ -172,14 +182,21 @@ def _mixed_batch(p, a, fixed_order=False):
     dec.num_splits, dec.split_span = splits, span
     if splits > 1:
         _partials(p, dec, (p.batch, splits, p.heads, p.dim_v), (p.batch, p.heads, splits))
-    main = torch.cuda.current_stream(p.device)
-    side = _side_stream(p.device)
-    side.wait_stream(main)
     a.flags |= _lib.FLAG_SKIP_SINGLE_QUERY
+    kv_bytes = p.batch * p.visible_max * p.kv_heads * (p.dim_qk + p.dim_v) * p.k.element_size()
+    if kv_bytes < _SIDE_STREAM_MIN_BYTES:
+        _lib.call("fa_prefill_fwd", a, p.device)
+        _lib.call("fa_decode_fwd", dec, p.device)
+        return True
+    main = torch.cuda.current_stream(p.device)
+    side, fork, join = _side_stream(p.device)
+    fork.record(main)
+    side.wait_event(fork)
     _lib.call("fa_prefill_fwd", a, p.device)
     with torch.cuda.stream(side):
         _lib.call("fa_decode_fwd", dec, p.device)
-    main.wait_stream(side)
+    join.record(side)
+    main.wait_event(join)
     return True
 
 

@@ -90,11 +90,15 @@ class Want:
         return " or ".join("[" + ", ".join("*" if e is None else str(e) for e in s) + "]" for s in options)
 
 
-def check_rules(rules):
-    """rules: iterable of (holds, error class, message); the first that does not hold raises."""
-    for holds, error, message in rules:
-        if not holds():
-            raise error(message)
+def _check(t, name, shape, dtypes, device, dtype_error=ValueError):
+    """Want(name, shape, dtypes).check(t, device) for one exact shape, with
+    the Want (and its message) built only when the tensor breaks it."""
+    if t is None:
+        return
+    ts = t.shape
+    if (t.device != device or len(ts) != len(shape) or any(e is not None and e != n for e, n in zip(shape, ts))
+            or (dtypes and t.dtype not in dtypes)):
+        Want(name, shape, dtypes, dtype_error).check(t, device)
 
 
 @dataclass
@@ -179,67 +183,61 @@ class Problem:
 
     # ---- contract
     def validate(self):
-        reject_training(tensors=(self.q, self.k, self.v, self.alibi, self.sinks, self.q_descale,
-                                 self.k_descale, self.v_descale, self.out))
-        for name in ("q", "k", "v"):
-            t = getattr(self, name)
-            if not on_gpu(t):
-                raise ValueError(f"{name} is on {t.device}; this library runs on a ROCm GPU ('cuda' device)")
+        """Raise on the first broken contract (the checks run on every call,
+        so each one is a plain test; messages are formatted only on failure)."""
         q, k, v = self.q, self.k, self.v
-        check_rules([
-            (lambda: q.ndim == 3, ValueError, f"q must be packed [tokens, heads, dim]; got {q.ndim} dims"),
-            (lambda: k.ndim in (3, 4) and v.ndim == k.ndim, ValueError,
-             "k and v must both be packed [tokens, heads, dim] or both paged [pages, page_size, heads, dim]"),
-            (lambda: k.shape[:-1] == v.shape[:-1], ValueError,
-             f"k {tuple(k.shape)} and v {tuple(v.shape)} differ in more than their head dimension"),
-            (lambda: q.shape[-1] == k.shape[-1], ValueError,
-             f"query head dim {q.shape[-1]} differs from key head dim {k.shape[-1]}"),
-            (lambda: k.shape[-2] > 0 and q.shape[1] % k.shape[-2] == 0, ValueError,
-             f"{q.shape[1]} query heads are not a multiple of {k.shape[-2]} key/value heads"),
-            (lambda: 1 <= q.shape[-1] <= MAX_HEAD_DIM and 1 <= v.shape[-1] <= MAX_HEAD_DIM, ValueError,
-             f"head dims ({q.shape[-1]}, {v.shape[-1]}) must lie in 1..{MAX_HEAD_DIM}"),
-            (lambda: self.cu_q.ndim == 1 and self.cu_q.numel() >= 1, ValueError,
-             "cu_seqlens_q must be a vector of batch + 1 offsets"),
-            (lambda: (self.cu_k is None) != (self.used_k is None), ValueError,
-             "give key lengths exactly once: cu_seqlens_k or seqused_k"),
-            (lambda: (self.table is None) == (k.ndim == 3), ValueError,
-             "paged 4-D K/V goes with a block_table, packed 3-D K/V without one"),
-        ])
+        reject_training(tensors=(q, k, v, self.alibi, self.sinks, self.q_descale, self.k_descale, self.v_descale,
+                                 self.out))
+        for name, t in (("q", q), ("k", k), ("v", v)):
+            if t.device.type != "cuda":
+                raise ValueError(f"{name} is on {t.device}; this library runs on a ROCm GPU ('cuda' device)")
+        if q.ndim != 3:
+            raise ValueError(f"q must be packed [tokens, heads, dim]; got {q.ndim} dims")
+        if k.ndim not in (3, 4) or v.ndim != k.ndim:
+            raise ValueError("k and v must both be packed [tokens, heads, dim] or both paged "
+                             "[pages, page_size, heads, dim]")
+        if k.shape[:-1] != v.shape[:-1]:
+            raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} differ in more than their head dimension")
+        if q.shape[-1] != k.shape[-1]:
+            raise ValueError(f"query head dim {q.shape[-1]} differs from key head dim {k.shape[-1]}")
+        if not (k.shape[-2] > 0 and q.shape[1] % k.shape[-2] == 0):
+            raise ValueError(f"{q.shape[1]} query heads are not a multiple of {k.shape[-2]} key/value heads")
+        if not (1 <= q.shape[-1] <= MAX_HEAD_DIM and 1 <= v.shape[-1] <= MAX_HEAD_DIM):
+            raise ValueError(f"head dims ({q.shape[-1]}, {v.shape[-1]}) must lie in 1..{MAX_HEAD_DIM}")
+        if not (self.cu_q.ndim == 1 and self.cu_q.numel() >= 1):
+            raise ValueError("cu_seqlens_q must be a vector of batch + 1 offsets")
+        if (self.cu_k is None) == (self.used_k is None):
+            raise ValueError("give key lengths exactly once: cu_seqlens_k or seqused_k")
+        if (self.table is None) != (k.ndim == 3):
+            raise ValueError("paged 4-D K/V goes with a block_table, packed 3-D K/V without one")
+        device = q.device
         b, hq, hk = self.batch, self.heads, self.kv_heads
-        i32 = (torch.int32,)
-        f32 = (torch.float32,)
-        wants = [
-            (self.cu_q, Want("cu_seqlens_q", (b + 1,), i32)),
-            (self.cu_k, Want("cu_seqlens_k", (b + 1,), i32)),
-            (self.used_k, Want("seqused_k", (b,), i32)),
-            (self.table, Want("block_table", (b, None), i32)),
-            (self.leftpad, Want("leftpad_k", (b,), i32)),
-            (self.out, Want("out", (self.tokens, hq, self.dim_v))),
-        ]
-        for t, want in wants:
-            want.check(t, self.device)
+        i32, f32 = (torch.int32,), (torch.float32,)
+        _check(self.cu_q, "cu_seqlens_q", (b + 1,), i32, device)
+        _check(self.cu_k, "cu_seqlens_k", (b + 1,), i32, device)
+        _check(self.used_k, "seqused_k", (b,), i32, device)
+        _check(self.table, "block_table", (b, None), i32, device)
+        _check(self.leftpad, "leftpad_k", (b,), i32, device)
+        _check(self.out, "out", (self.tokens, hq, self.dim_v), (), device)
         window = tuple(self.window)
-        check_rules([
-            (lambda: len(window) == 2 and min(window) >= -1, ValueError,
-             f"window_size {window} must be two bounds, each -1 (unbounded) or >= 0"),
-            (lambda: self.softcap >= 0, ValueError, f"softcap {self.softcap} must be >= 0 (0 disables it)"),
-            (lambda: self.splits >= 0, ValueError, f"num_splits {self.splits} must be >= 0"),
-            (lambda: self.max_q >= 0 and self.max_k >= 0, ValueError,
-             f"max_seqlen_q/max_seqlen_k ({self.max_q}, {self.max_k}) must be >= 0"),
-            (lambda: self.mask is None or isinstance(self.mask, MaskSpec), TypeError,
-             "mask_mod must come from mm_prefix_mask() or rswa_mask()"),
-        ])
-        feature_wants = [
-            (self.q_descale, Want("q_descale", (b, hk), f32)),
-            (self.k_descale, Want("k_descale", (b, hk), f32)),
-            (self.v_descale, Want("v_descale", (b, hk), f32)),
-            (self.alibi, Want("alibi_slopes", {(hq,), (b, hq)}, f32)),
-            (self.sinks, Want("s_aux", (hq,))),
-        ]
+        if not (len(window) == 2 and min(window) >= -1):
+            raise ValueError(f"window_size {window} must be two bounds, each -1 (unbounded) or >= 0")
+        if not self.softcap >= 0:
+            raise ValueError(f"softcap {self.softcap} must be >= 0 (0 disables it)")
+        if not self.splits >= 0:
+            raise ValueError(f"num_splits {self.splits} must be >= 0")
+        if not (self.max_q >= 0 and self.max_k >= 0):
+            raise ValueError(f"max_seqlen_q/max_seqlen_k ({self.max_q}, {self.max_k}) must be >= 0")
+        if not (self.mask is None or isinstance(self.mask, MaskSpec)):
+            raise TypeError("mask_mod must come from mm_prefix_mask() or rswa_mask()")
         if torch.is_tensor(self.causal):
-            feature_wants.insert(0, (self.causal, Want("dynamic causal flags", (b,), (torch.bool,))))
-        for t, want in feature_wants:
-            want.check(t, self.device)
+            _check(self.causal, "dynamic causal flags", (b,), (torch.bool,), device)
+        _check(self.q_descale, "q_descale", (b, hk), f32, device)
+        _check(self.k_descale, "k_descale", (b, hk), f32, device)
+        _check(self.v_descale, "v_descale", (b, hk), f32, device)
+        if self.alibi is not None:
+            Want("alibi_slopes", {(hq,), (b, hq)}, f32).check(self.alibi, device)
+        _check(self.sinks, "s_aux", (hq,), (), device)
         if self.mask is not None:
             if self.mask.kind not in (1, 2) or self.mask_aux is None or len(self.mask_aux) != 2:
                 raise ValueError("a vLLM mask needs its two auxiliary tensors")
@@ -250,11 +248,10 @@ class Problem:
             for t, want in zip(self.mask_aux, aux_wants):
                 if t is None:
                     raise ValueError(f"{want.name} is missing")
-                want.check(t, self.device)
+                want.check(t, device)
         elif self.mask_aux is not None:
             raise ValueError("aux_tensors were given without a mask_mod to use them")
-        for name in ("q", "k", "v"):
-            t = getattr(self, name)
+        for name, t in (("q", q), ("k", k), ("v", v)):
             if t.dtype not in ELEMENT_TYPES:
                 raise TypeError(f"{name} is {t.dtype}; attention reads float16, bfloat16, float32 or float8_e4m3fn")
         if self.out is not None and self.out.dtype not in OUTPUT_TYPES:
