@@ -240,7 +240,7 @@ FA_DEV int64_t request_by_rank(const fa_attn_args& a, int64_t rank, int lane) {
 
 struct PrefillShape {
   int n_qblocks;
-  int log2_page;   // paged K/V: page size = 1 << log2_page
+  int log2_page;   // paged K/V: page of position p = p >> log2_page, slot p & (2^log2_page - 1)
   int compact;     // 1: workgroups map onto the compact work list
   int hp;          // query heads per workgroup (1 or 2, dividing the GQA group): W / hp waves per head
 };

@@ -91,7 +91,12 @@ bool prefill_ok(const fa_attn_args& a) {
   if (a.k_stride[1] < dq || a.v_stride[1] < dv) return false;
   if (16 * a.k_stride[1] * kb >= 0x7fffffffll || 16 * a.v_stride[1] * kb >= 0x7fffffffll) return false;
   if (a.page_size) {
-    if (a.page_size < 16 || (a.page_size & (a.page_size - 1))) return false;
+    // Power-of-two pages (the kernel splits a position into page and slot
+    // with a shift and a mask), or one page holding every key: a dense cache
+    // [B, capacity, Hkv, D] seen through a one-column table, whose positions
+    // stay below max_seqlen_k <= capacity < 2^log2_page, so the page index
+    // is always 0 whatever the capacity.
+    if (a.page_size < 16 || ((a.page_size & (a.page_size - 1)) && a.max_seqlen_k > a.page_size)) return false;
     // Page strides are 32-bit byte counts in the group descriptors.
     if (kb * a.k_stride[0] >= (1ll << 32) || kb * a.v_stride[0] >= (1ll << 32)) return false;
   }

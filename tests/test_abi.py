@@ -91,3 +91,30 @@ def test_supported_queries_reject_unsupported_combinations():
     a.heads_q = a.heads_k = 1
     assert not _lib.supported("fa_decode_supported", a)
     assert not _lib.supported("fa_prefill_supported", a)
+
+
+def _paged_prefill_args(page_size, max_k):
+    """A bf16 d128 paged-prefill layout (pointers only need 16-byte alignment here)."""
+    a = _lib.AttnArgs()
+    a.q_dtype = a.k_dtype = a.v_dtype = a.out_dtype = _lib.BF16
+    a.head_dim_qk = a.head_dim_v = 128
+    a.batch, a.heads_q, a.heads_k, a.total_q = 2, 8, 2, 128
+    a.max_seqlen_q, a.max_seqlen_k = 64, max_k
+    a.q = a.k = a.v = a.out = 1 << 20
+    for name, strides in (("q_stride", (8 * 128, 128, 1)), ("out_stride", (8 * 128, 128, 1)),
+                          ("k_stride", (page_size * 2 * 128, 2 * 128, 128, 1)),
+                          ("v_stride", (page_size * 2 * 128, 2 * 128, 128, 1))):
+        for i, s in enumerate(strides):
+            getattr(a, name)[i] = s
+    a.page_size, a.num_splits = page_size, 1
+    a.window_left = a.window_right = -1
+    return a
+
+
+@pytest.mark.parametrize("page_size,max_k,ok", [(16, 4096, True), (256, 100000, True), (48, 96, False),
+                                                (4160, 4160, True), (600, 512, True), (600, 601, False)])
+def test_prefill_pages_are_powers_of_two_or_one_page_per_request(page_size, max_k, ok):
+    """The MFMA prefill splits a position into page and slot with a shift:
+    pages must be powers of two unless every key lies in the first page (a
+    dense cache of any capacity seen through a one-column table)."""
+    assert _lib.supported("fa_prefill_supported", _paged_prefill_args(page_size, max_k)) == ok

@@ -161,15 +161,17 @@ def test_masks_with_fp8_cache_and_softcap(device, mask_name):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("d", [64, 128, 256])
 @pytest.mark.parametrize("causal", [True, False])
-def test_cache_leftpad_on_the_mfma_prefill(device, dtype, d, causal):
-    """flash_attn_with_kvcache over a dense cache of capacity 512 with
-    cache_leftpad: key j of request b sits at slot leftpad[b] + j."""
-    batch, sq, cap, hq, hkv = 3, 40, 512, 8, 2
+@pytest.mark.parametrize("cap", [512, 600, 1000])
+def test_cache_leftpad_on_the_mfma_prefill(device, dtype, d, causal, cap):
+    """flash_attn_with_kvcache over a dense cache with cache_leftpad: key j
+    of request b sits at slot leftpad[b] + j.  Capacities that are not powers
+    of two run as one page per request (every position in page 0)."""
+    batch, sq, hq, hkv = 3, 40, 8, 2
     g = torch.Generator().manual_seed(d)
     q = (torch.randn(batch, sq, hq, d, generator=g) * 0.5).to(dtype).to(device)
     kc = (torch.randn(batch, cap, hkv, d, generator=g) * 0.5).to(dtype).to(device)
     vc = (torch.randn(batch, cap, hkv, d, generator=g) * VALUE_SCALE).to(dtype).to(device)
-    seqlens = torch.tensor([500, 300, 77], dtype=torch.int32, device=device)
+    seqlens = torch.tensor([min(500, cap), 300, 77], dtype=torch.int32, device=device)
     leftpad = torch.tensor([13, 0, 30], dtype=torch.int32, device=device)
     out, lse = flash_attn_with_kvcache(q, kc, vc, cache_seqlens=seqlens, cache_leftpad=leftpad, causal=causal,
                                        return_softmax_lse=True)
