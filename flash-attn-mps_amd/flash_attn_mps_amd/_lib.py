@@ -123,7 +123,7 @@ ENTRY_POINTS = {
     "fa_merge_partials": (MergePartialsArgs, ctypes.c_int),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 FLAG_SKIP_SINGLE_QUERY = 1
 DECODE_SCRATCH_BYTES = 32 << 20   # FA_DECODE_SCRATCH_BYTES
 _lib = None

@@ -41,7 +41,9 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 2
+/* 3: fa_decode_fwd's split partials became split-major ([batch, S, R, Hq,
+ * Dv]; the struct layouts are those of version 2). */
+#define FA_ABI_VERSION 3
 
 /* Element types of attention/cache tensors. */
 enum fa_dtype { FA_F16 = 0, FA_BF16 = 1, FA_F32 = 2, FA_E4M3 = 3 };
