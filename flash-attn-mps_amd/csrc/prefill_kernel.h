@@ -543,37 +543,48 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   constexpr int KST8 = DQ / 64;                // k-steps of the E4M3 S MFMA
   u32x4 qop[FQ ? 1 : NB][FQ ? 1 : KST];
   i32x8 qop8[FQ ? NB : 1][FQ ? KST8 : 1];      // E4M3: Q[row][64 j + 32 hh .. +32]
+  // Rows past the request load its last row (their results are never
+  // stored), so every load is unconditional and nothing touches the loaded
+  // registers before the first tile's wait: the Q loads' latency overlaps
+  // the first K/V DMAs.  (Exec-masked loads with zero defaults made the
+  // compiler wait for the first of them before issuing the rest.)  The sign
+  // flip and the ALiBi zeroing are rare; a uniform branch applies them.
+  const bool q_fix = q_flip || q_zero;
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    const int row = wq0 + 32 * nb + l32;
-    const bool ok = row < r.q_len;
+    const int row = min(wq0 + 32 * nb + l32, r.q_len - 1);
     if constexpr (FQ) {
       const uint8_t* qp = (const uint8_t*)a.q + ((int64_t)r.q_begin + row) * a.q_stride[0] +
                           (int64_t)h * a.q_stride[1] + 32 * hh;
 #pragma unroll
       for (int j = 0; j < KST8; ++j) {
-        u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
-        if (ok) {
-          lo = *(const u32x4*)(qp + 64 * j);
-          hi = *(const u32x4*)(qp + 64 * j + 16);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          lo[e] = (lo[e] ^ q_flip8) & q_keep;
-          hi[e] = (hi[e] ^ q_flip8) & q_keep;
-        }
+        const u32x4 lo = *(const u32x4*)(qp + 64 * j), hi = *(const u32x4*)(qp + 64 * j + 16);
         qop8[nb][j] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      }
+      if (q_fix) {
+#pragma unroll
+        for (int j = 0; j < KST8; ++j)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) qop8[nb][j][e] = (int)(((uint32_t)qop8[nb][j][e] ^ q_flip8) & q_keep);
       }
     } else {
       const uint16_t* qp = (const uint16_t*)a.q + ((int64_t)r.q_begin + row) * a.q_stride[0] +
                            (int64_t)h * a.q_stride[1] + 8 * hh;
 #pragma unroll
       for (int kk = 0; kk < KST; ++kk) {
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (ok && 16 * kk + 8 * hh + 8 <= DQT) v = *(const u32x4*)(qp + 16 * kk);
+        if constexpr (DQT == DQ) {
+          qop[nb][kk] = *(const u32x4*)(qp + 16 * kk);
+        } else {
+          u32x4 v = {0u, 0u, 0u, 0u};
+          if (16 * kk + 8 * hh + 8 <= DQT) v = *(const u32x4*)(qp + 16 * kk);
+          qop[nb][kk] = v;
+        }
+      }
+      if (q_fix) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (v[e] ^ q_flip16) & q_keep;
-        qop[nb][kk] = v;
+        for (int kk = 0; kk < KST; ++kk)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) qop[nb][kk][e] = (qop[nb][kk][e] ^ q_flip16) & q_keep;
       }
     }
   }
@@ -587,13 +598,20 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
       const u32x4 z = {0u, 0u, 0u, 0u};
       *(u32x4*)(stk + 16 * i) = z;
     }
+    __syncthreads();
   } else {
-    for (int i = tid; i < 2 * VTILE / 16; i += 64 * W) {
-      const u32x4 z = {0u, 0u, 0u, 0u};
-      *(u32x4*)(vbuf0 + 16 * i) = z;
+    // Only a buffer whose first tile ends past the request's last key needs
+    // it (later tiles find the finite rows of earlier ones); without mask
+    // kinds the first tiles are tile0 and tile0 + 1.
+    const bool need = MK != 0 || (tile0 + 1) * PF_BN > r.k_len || (tile0 + 1 < n_tiles && (tile0 + 2) * PF_BN > r.k_len);
+    if (need) {
+      for (int i = tid; i < 2 * VTILE / 16; i += 64 * W) {
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        *(u32x4*)(vbuf0 + 16 * i) = z;
+      }
+      __syncthreads();
     }
   }
-  __syncthreads();
 
   // ---- DMA addressing.  A tile is 8 row blocks (8 rows each) per column
   // group; one instruction moves one row block of one column group.  Lane p
