@@ -33,11 +33,12 @@ PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 PEAK_FP8_TFLOPS = 5000.0
 PEAK_FP8_BF16_MIXED_TFLOPS = 2.0 / (1.0 / 5000.0 + 1.0 / 2500.0)
-# Warmup calls of the secondary decode / store / mixed lines (at least the
-# command's --warmup): after the process's first heavy GPU work the decode
-# kernel's calls 5-10 run up to 20% slower than its steady state (kernel
-# trace: 797-808 us, then 871-953, then 775), so with 5 warmups their timed
-# calls sat in that dip.  Each entry states the warmup it used.
+# Warmup calls of every secondary line (at least the command's --warmup):
+# after an idle period the GPU's clock dips and ramps back over the first
+# tens of calls (a per-call trace of config 3: ~1 ms for the first call, the
+# shader clock down to ~1.7 GHz for calls 2-8, back to 2.4 GHz by call ~24),
+# and MFMA-bound launches settle only after ~100 of them.  Each entry states
+# the warmup it used.
 SECONDARY_WARMUP = 50
 
 
@@ -517,9 +518,13 @@ def main():
                          ("prefill_fp8", lambda *x: prefill_fp8(*x, c=c2_inputs, defer=True))):
             if only and name not in only and not (name == "store4" and "4" in only):
                 continue
-            # The E4M3 line precedes config 2 on the GPU and keeps the
-            # command's warmup, so config 2 starts from the same state.
-            warmup = args.warmup if name == "prefill_fp8" else max(args.warmup, SECONDARY_WARMUP)
+            # Every secondary line takes at least SECONDARY_WARMUP untimed
+            # calls.  For the E4M3 prefill these are MFMA-bound launches that
+            # bring the clock to its loaded state (it settles over ~100
+            # launches, ~55 ms), so its timed calls and config 2 after it are
+            # measured there rather than in the ramp; config 2 itself takes
+            # exactly --warmup untimed steps.
+            warmup = max(args.warmup, SECONDARY_WARMUP)
             r = fn(device, args.steps, warmup)
             if name == "prefill_fp8":
                 pending = r
@@ -538,7 +543,7 @@ def main():
 
     c2 = config2(device, args.steps, args.warmup, c=c2_inputs)
     if pending is not None:
-        secondary["prefill_fp8"] = secondary_entry("prefill_fp8", pending(), args.warmup)
+        secondary["prefill_fp8"] = secondary_entry("prefill_fp8", pending(), max(args.warmup, SECONDARY_WARMUP))
     line = {
         "metric": "bf16 prefill TFLOP/s & paged-decode KV GB/s, % of MI355X roofline, 1 GPU",
         "value": round(c2["tflops"], 2),
