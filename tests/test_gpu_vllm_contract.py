@@ -8,6 +8,7 @@ untouched sentinels, and bit-exact batch invariance.
 import pytest
 import torch
 
+from flash_attn_mps_amd import _lib
 from flash_attn_mps_amd.vllm import flash_attn_varlen_func, merge_attn_states, mm_prefix_mask, rswa_mask
 from harness import assert_parity, offsets, oracle_attention, seeded
 
@@ -73,6 +74,40 @@ def test_mask_descriptors_over_a_poisoned_paged_cache(device, mask_name):
     got, lse = flash_attn_varlen_func(q, k, v, 96, lengths["cu_seqlens_q"], 257, seqused_k=used,
                                       block_table=table, mask_mod=mask, aux_tensors=aux,
                                       return_softmax_lse=True, fa_version=4)
+    ref, ref_lse = oracle_attention(q, k, v, lengths["cu_seqlens_q"], used_k=used, block_table=table,
+                                    mask=mask, aux=aux)
+    assert_parity(got, lse, ref, ref_lse)
+
+
+@pytest.mark.parametrize("mask_name", ["prefix", "prefix+window", "prefix clamped to window", "rolling window"])
+def test_mask_descriptors_run_on_the_mfma_prefill(device, mask_name, monkeypatch):
+    """The same mask calls at dq = dv = 64 (the dims the MFMA prefill takes
+    mask kinds at) go to fa_prefill_fwd, not to the generic kernel, and meet
+    the parity bar."""
+    q, k_packed, v_packed, lengths = _requests(device, (96,), (257,), 64, 64, seed=320)
+    table = torch.tensor([[5, 1, 7, 3, 0]], device=device, dtype=torch.int32)
+    k = torch.full((8, 64, 2, 64), float("nan"), device=device, dtype=q.dtype)
+    v = torch.full((8, 64, 2, 64), float("nan"), device=device, dtype=q.dtype)
+    pos = torch.arange(257, device=device)
+    pages = table[0, pos // 64].long()
+    k[pages, pos % 64], v[pages, pos % 64] = k_packed, v_packed
+    used = torch.tensor([257], device=device, dtype=torch.int32)
+    ranges = torch.full((96, 2), -1, device=device, dtype=torch.int32)
+    ranges[31:61] = torch.tensor([192, 221], device=device, dtype=torch.int32)
+    if mask_name == "rolling window":
+        mask = rswa_mask()
+        aux = [torch.tensor([64], device=device, dtype=torch.int32),
+               torch.tensor([16], device=device, dtype=torch.int32)]
+    else:
+        mask = mm_prefix_mask(None if mask_name == "prefix" else 16, mask_name == "prefix clamped to window")
+        aux = [ranges, lengths["cu_seqlens_q"]]
+    calls = []
+    real_call = _lib.call
+    monkeypatch.setattr(_lib, "call", lambda name, *a, **kw: (calls.append(name), real_call(name, *a, **kw))[1])
+    got, lse = flash_attn_varlen_func(q, k, v, 96, lengths["cu_seqlens_q"], 257, seqused_k=used,
+                                      block_table=table, mask_mod=mask, aux_tensors=aux,
+                                      return_softmax_lse=True, fa_version=4)
+    assert "fa_prefill_fwd" in calls and "fa_attn_fwd" not in calls, calls
     ref, ref_lse = oracle_attention(q, k, v, lengths["cu_seqlens_q"], used_k=used, block_table=table,
                                     mask=mask, aux=aux)
     assert_parity(got, lse, ref, ref_lse)
