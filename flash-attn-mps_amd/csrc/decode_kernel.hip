@@ -271,7 +271,7 @@ int64_t partial_floats(const fa_attn_args& a, int64_t splits) {
 
 // The split plan of the Python host layer (flash_attn_mps_amd/_decode.py
 // split_plan with num_splits == 0): spans of 4096 keys halving down to 128
-// until the grid holds 2048 workgroups.  Then the split count is reduced
+// until the grid holds 1024 workgroups.  Then the split count is reduced
 // until the partials fit in `cap_floats` (one split needs no partials).
 void plan_splits(const fa_attn_args& a, int gt, int64_t cap_floats, int32_t* splits_out, int32_t* span_out) {
   const int64_t vis = decode_visible_max(a);
@@ -282,7 +282,7 @@ void plan_splits(const fa_attn_args& a, int gt, int64_t cap_floats, int32_t* spl
   }
   const int64_t groups = decode_head_groups(a, gt);
   int64_t span = 4096;
-  while (span > 128 && a.batch * groups * fa_ceil_div(vis, span) < 2048) span /= 2;
+  while (span > 128 && a.batch * groups * fa_ceil_div(vis, span) < 1024) span /= 2;
   int64_t splits = fa_ceil_div(vis, span);
   while (splits > 1 && partial_floats(a, splits) > cap_floats) {
     span = fa_ceil_div(fa_ceil_div(vis, fa_ceil_div(splits, 2)), 32) * 32;

@@ -6,10 +6,12 @@ The split plan uses only host-known sizes: the most keys a query can see
 (max_seqlen_k clipped by a left window, _decode.py:63; with R rows the first
 row's window, R - 1 keys wider) and the number of (request, query-head group)
 work units.  A split covers `span` keys; the span
-starts at 4096 and halves (down to 128) until the grid holds at least 2048
-workgroups, so small batches still fill the 256 compute units.  (With the
-kernels' longest-first work order, 4096-key spans beat 2048: config 3
-0.749-0.765 -> 0.730 ms, its 4-row step 0.79-0.80 -> 0.755, config 5 -1%.)  An explicit
+starts at 4096 and halves (down to 128) until the grid holds at least 1024
+workgroups (two rounds of the 512 that the decode kernels keep resident),
+so small batches still fill the 256 compute units.  (With the kernels'
+longest-first work order, 4096-key spans beat 2048: config 3 0.749-0.765
+-> 0.730 ms, its 4-row step 0.79-0.80 -> 0.755, config 5 -1%; and 1024
+workgroups beat 2048: config 4's single split 0.324-0.328 -> 0.318 ms.)  An explicit
 num_splits is honoured.  fa_decode_fwd_noalloc plans the same way in C.
 """
 import torch
@@ -17,7 +19,7 @@ import torch
 from . import _lib
 from ._attention import _partials, build_args
 
-_MIN_WORKGROUPS = 2048
+_MIN_WORKGROUPS = 1024
 _START_SPAN = 4096
 _MIN_SPAN = 128
 _SPAN_ALIGN = 32
