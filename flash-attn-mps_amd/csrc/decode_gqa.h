@@ -37,7 +37,8 @@
 //   head dims 64 and 128 (Dqk = Dv), outputs of the query's type, packed or
 //   paged K/V (page size a multiple of 16), sinks, softcap, windows, 1-16
 //   query rows per request; the host keeps other combinations on the VALU
-//   kernel.
+//   kernel.  Neighbouring 64-dim KV heads can run in pairs as one 128-dim
+//   virtual head (PACK below), so that the DMA reads 128-dim row runs.
 #ifndef FA_DECODE_GQA_H
 #define FA_DECODE_GQA_H
 
@@ -110,9 +111,19 @@ FA_DEV void wait_dma_groups(int n) {
 // rows (16 x D bytes, chunks XOR-swizzled): K operands widen in registers
 // after an 8-byte LDS read, V^T comes through ds_read_b64_tr_b8 and widens in
 // registers the same way, and the descales scale the scores and the output.
-template <typename T, int D, bool CAP, typename KT = T>
+// PACK = 2: two neighbouring KV heads of D / 2 = 64 dims, stored next to each
+// other in every key row, run as one virtual head of D = 128 dims, so each
+// DMA instruction reads rows of 2 x 64 dims (128 bytes of E4M3, 256 of
+// 16-bit) instead of 64-dim rows.  The virtual head's query heads are the
+// two heads' groups; a column's query holds its own head's half of the
+// virtual dims and zeros in the other, so S^T = K Q^T gives each column the
+// scores of its own KV head, and of O^T += V^T P^T each column keeps its own
+// half.  Descales are per column (its KV head).
+template <typename T, int D, bool CAP, typename KT = T, int PACK = 1>
 __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_attn_args a, const int span) {
   static_assert(D == 64 || D == 128, "head dims 64 and 128");
+  static_assert(PACK == 1 || (PACK == 2 && D == 128), "two 64-dim heads per virtual 128-dim head");
+  constexpr int DH = D / PACK;            // the heads' own dims
   constexpr bool FP8 = KT::id == FA_E4M3;
   constexpr int EB = KT::bytes;           // bytes per K/V element
   constexpr int KSTEPS = D / 16;          // k-steps of S^T = K Q^T
@@ -131,9 +142,12 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   // 32 / ntok query heads per workgroup; column c is head h0 + c / ntok,
   // token c % ntok (one token: column c = head h0 + c).  A request's tokens
   // are its last q_len key positions.
-  // Grid: x = KV head * head tiles + tile, y = split, z = request.
+  // Grid: x = (virtual) KV head * head tiles + tile, y = split, z = request.
+  // Virtual KV head kh holds KV heads PACK kh .. PACK kh + PACK - 1 and their
+  // PACK * gr query heads, numbered contiguously.
   const int ntok = a.max_seqlen_q > 1 ? (int)a.max_seqlen_q : 1, nh = GQA_HEADS / ntok;
-  const int group = (int)(a.heads_q / a.heads_k);
+  const int gr = (int)(a.heads_q / a.heads_k);   // query heads per KV head
+  const int group = PACK * gr;
   const int tiles = (group + nh - 1) / nh;
   const int kh = blockIdx.x / tiles, t0 = (blockIdx.x % tiles) * nh;
   const int nheads = min(nh, group - t0);
@@ -151,6 +165,10 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   // This lane's column.
   const int chead = l32 / ntok, ctok = l32 - chead * ntok;
   const bool col_ok = chead < nheads && ctok < r.q_len;
+  // KV head of query head h0 + c (c < nheads), as its part of the virtual
+  // head; columns past the group take the last part (they hold no query).
+  auto part_of = [&](int c) { return PACK > 1 ? min((h0 + c) / gr - PACK * kh, PACK - 1) : 0; };
+  const int cpart = part_of(chead);
 
   // Zeroed V buffers: rows the DMA does not write (past the request) then
   // hold finite values, which a zero probability keeps out of O.  The
@@ -162,18 +180,22 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   wait_lds();
 
   // Q^T operands: k-step kk, lane (l32, hh) holds its column's query
-  // (token ctok, head h0 + chead), dims 16 kk + 8 hh .. +8 (zeros for
-  // columns past the group or the request's tokens).
+  // (token ctok, head h0 + chead), dims 16 kk + 8 hh .. +8 of the virtual
+  // head, i.e. of part kk / KPH (zeros for the other part, and for columns
+  // past the group or the request's tokens).
+  constexpr int KPH = KSTEPS / PACK;   // k-steps per part
   u32x4 qop[KSTEPS];
   {
     const uint16_t* qp = (const uint16_t*)a.q + (int64_t)(r.q_begin + (col_ok ? ctok : 0)) * a.q_stride[0] +
                          (int64_t)(h0 + (col_ok ? chead : 0)) * a.q_stride[1] + 8 * hh;
 #pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) qop[kk] = col_ok ? *(const u32x4*)(qp + 16 * kk) : u32x4{0u, 0u, 0u, 0u};
+    for (int kk = 0; kk < KSTEPS; ++kk)
+      qop[kk] = col_ok && kk / KPH == cpart ? *(const u32x4*)(qp + 16 * (kk % KPH)) : u32x4{0u, 0u, 0u, 0u};
   }
 
-  const float kdsc = descale_of(a.q_descale, a.q_descale_stride, b, kh) * descale_of(a.k_descale, a.k_descale_stride, b, kh);
-  const float vdsc = descale_of(a.v_descale, a.v_descale_stride, b, kh);
+  // Descales of this column's KV head (one per workgroup unless packed).
+  const int ckh = PACK * kh + cpart;
+  const float kdsc = descale_of(a.q_descale, a.q_descale_stride, b, ckh) * descale_of(a.k_descale, a.k_descale_stride, b, ckh);
   const float c_scale = a.softmax_scale * kdsc * LOG2E;   // raw dot -> log2 units
   const float cap_in = CAP ? 2.0f * LOG2E * a.softmax_scale * kdsc / a.softcap : 0.0f;
   const float cap_out = a.softcap * LOG2E;
@@ -214,8 +236,8 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   const int pos_end = r.k_base + r.left + r.k_len;                                   // the request's end
   const uint32_t krow_b = (uint32_t)(EB * a.k_stride[1]), vrow_b = (uint32_t)(EB * a.v_stride[1]);
   const uint32_t kpage_b = (uint32_t)(EB * a.k_stride[0]), vpage_b = (uint32_t)(EB * a.v_stride[0]);
-  const char* const khead = (const char*)a.k + EB * (int64_t)kh * a.k_stride[2];
-  const char* const vhead = (const char*)a.v + EB * (int64_t)kh * a.v_stride[2];
+  const char* const khead = (const char*)a.k + EB * (int64_t)(PACK * kh) * a.k_stride[2];
+  const char* const vhead = (const char*)a.v + EB * (int64_t)(PACK * kh) * a.v_stride[2];
   const int32_t* const trow = P ? a.block_table + b * a.bt_stride[0] : nullptr;
   int kdoff[2];
 #pragma unroll
@@ -537,6 +559,7 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
       fw[w] = fast_exp2(cm[w * GQA_HEADS + tid] - ref);
       L += cl[w * GQA_HEADS + tid] * fw[w];
     }
+    const float vdsc = descale_of(a.v_descale, a.v_descale_stride, b, PACK * kh + part_of(tid / ntok));
     const float norm = L > 0.0f ? vdsc / L : 0.0f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) cm[w * GQA_HEADS + tid] = fw[w] * norm;
@@ -546,13 +569,14 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   // hc / ntok for hc < 32 and 1 <= ntok <= 16 as a multiply by
   // ceil(2^32 / ntok) and a shift (the rounding error stays below 32 / 2^32).
   const uint64_t ntok_inv = ((1ull << 32) + (uint64_t)ntok - 1) / (uint64_t)ntok;
-  for (int idx = tid; idx < ncol * D; idx += GQA_THREADS) {
-    const int hc = idx / D, d = idx - hc * D;   // column hc: head h0 + hc / ntok, token hc % ntok
+  for (int idx = tid; idx < ncol * DH; idx += GQA_THREADS) {
+    const int hc = idx / DH, d = idx - hc * DH;   // column hc: head h0 + hc / ntok, token hc % ntok
     const int th = (int)(((uint64_t)hc * ntok_inv) >> 32), tt = hc - th * ntok;
     if (th >= nheads || tt >= r.q_len) continue;
+    const int dv = d + DH * part_of(th);   // the column's own half of the virtual dims
     float O = 0.0f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) O += co[((int64_t)w * GQA_HEADS + hc) * CO_ROW + d] * cm[w * GQA_HEADS + hc];
+    for (int w = 0; w < 4; ++w) O += co[((int64_t)w * GQA_HEADS + hc) * CO_ROW + dv] * cm[w * GQA_HEADS + hc];
     const int h = h0 + th;
     const int64_t tq = r.q_begin + tt;
     if (S == 1) {
@@ -566,7 +590,7 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
       // from displacing K/V in the caches.  Interleaved 4 D-byte rows (the
       // splits of one row together) cost config 3's speculative step ~6%.
       const int64_t orow = ((b * S + split) * ntok + tt) * a.heads_q + h;
-      __builtin_nontemporal_store(O, &a.partial_out[orow * D + d]);
+      __builtin_nontemporal_store(O, &a.partial_out[orow * DH + d]);
       if (d == 0) a.partial_lse[((b * ntok + tt) * a.heads_q + h) * S + split] = cl[hc];
     }
   }

@@ -1,6 +1,7 @@
 // Variants of the matrix-core GQA decode kernel (decode_gqa.h) and their
 // selection: 16-bit queries over K/V of the same type or E4M3, Dqk = Dv in
-// {64, 128}, with and without softcap.
+// {64, 128}, with and without softcap; 64-dim heads stored next to each
+// other run two KV heads per workgroup (PACK = 2).
 #include "decode_gqa.h"
 
 namespace fa_decode {
@@ -23,29 +24,52 @@ bool chunks_aligned(const fa_attn_args& a, int kvb) {
   return true;
 }
 
-template <typename T, typename KT, int D>
+template <typename T, typename KT, int D, int PACK>
 GqaChoice choose(bool cap) {
   GqaChoice c;
-  c.kern = cap ? fa_decode_gqa::decode_gqa_kernel<T, D, true, KT> : fa_decode_gqa::decode_gqa_kernel<T, D, false, KT>;
+  c.kern = cap ? fa_decode_gqa::decode_gqa_kernel<T, D, true, KT, PACK>
+               : fa_decode_gqa::decode_gqa_kernel<T, D, false, KT, PACK>;
   c.lds = fa_decode_gqa::gqa_lds_bytes<D, KT::id == FA_E4M3>();
+  c.pack = PACK;
   return c;
 }
 
+// Two 64-dim KV heads per workgroup when every key row holds them next to
+// each other (head stride 64 elements, rows of at least 128), both heads'
+// query columns fit one 32-column tile (a second tile would read both heads'
+// rows again: 48/2 heads at 16 bits 4.82 -> 2.64 TB/s), and the cache is
+// E4M3 or has 8 KV heads or more.  Measured on 64 requests of U[512, 32768]
+// keys, one query row each: E4M3 32/8 2.95 -> 4.92 TB/s, 12/4 2.76 -> 4.01,
+// 6/2 2.40 -> 3.32 (64-byte rows are the worst case of the paged gather);
+// 16-bit 32/8 5.33 -> 5.65, 64/8 5.47 -> 5.81, but 12/4 5.58 -> 5.33 and 14/2
+// 5.01 -> 4.74 (with few KV heads a key row is 256-512 bytes that the heads'
+// workgroups already read side by side, and pairing halves the workgroups).
+// Paired heads also take groups of 1 and 2, which otherwise run on the VALU
+// kernel: E4M3 16/16 3.06 -> 5.64, 16/8 2.91 -> 4.92; 16-bit 16/16 5.94 ->
+// 6.29, 16/8 the same.
+bool packable(const fa_attn_args& a) {
+  const int64_t ntok = a.max_seqlen_q > 1 ? a.max_seqlen_q : 1;
+  return a.head_dim_qk == 64 && a.heads_k % 2 == 0 && a.k_stride[2] == 64 && a.v_stride[2] == 64 &&
+         a.k_stride[1] >= 128 && a.v_stride[1] >= 128 && 2 * (a.heads_q / a.heads_k) * ntok <= fa_decode_gqa::GQA_HEADS &&
+         (a.k_dtype == FA_E4M3 || a.heads_k >= 8);
+}
+
 template <typename T, typename KT>
-GqaChoice choose_dim(int64_t d, bool cap) {
-  return d == 64 ? choose<T, KT, 64>(cap) : choose<T, KT, 128>(cap);
+GqaChoice choose_dim(const fa_attn_args& a, bool cap) {
+  if (a.head_dim_qk == 64) return packable(a) ? choose<T, KT, 128, 2>(cap) : choose<T, KT, 64, 1>(cap);
+  return choose<T, KT, 128, 1>(cap);
 }
 
 }  // namespace
 
 GqaChoice pick_decode_gqa(const fa_attn_args& a) {
-  const GqaChoice none{nullptr, 0};
+  const GqaChoice none{nullptr, 0, 1};
   if (a.heads_k <= 0 || a.heads_q % a.heads_k) return none;
   // One query row per request: groups of DECODE_GQA_MIN_GROUP or more (the
   // VALU kernel is faster below); 2..DECODE_GQA_MAX_ROWS rows: any group
   // (nothing else runs a few rows per request as decode).
   if (a.max_seqlen_q > DECODE_GQA_MAX_ROWS) return none;
-  if (a.max_seqlen_q <= 1 && a.heads_q / a.heads_k < DECODE_GQA_MIN_GROUP) return none;
+  if (a.max_seqlen_q <= 1 && a.heads_q / a.heads_k < DECODE_GQA_MIN_GROUP && !packable(a)) return none;
   if (a.q_dtype != FA_BF16 && a.q_dtype != FA_F16) return none;
   // P.V runs on probabilities rounded to the query's type: fp32 outputs
   // (held to fp32 accuracy) take the VALU kernel, which keeps P in fp32.
@@ -60,9 +84,8 @@ GqaChoice pick_decode_gqa(const fa_attn_args& a) {
   for (int i = 0; i < 2; ++i)
     if (a.k_stride[i] * kvb >= (1ll << 31) / 16 || a.v_stride[i] * kvb >= (1ll << 31) / 16) return none;
   const bool cap = a.softcap > 0.0f, fp8 = a.k_dtype == FA_E4M3;
-  if (a.q_dtype == FA_BF16)
-    return fp8 ? choose_dim<BF16T, E4M3T>(a.head_dim_qk, cap) : choose_dim<BF16T, BF16T>(a.head_dim_qk, cap);
-  return fp8 ? choose_dim<F16T, E4M3T>(a.head_dim_qk, cap) : choose_dim<F16T, F16T>(a.head_dim_qk, cap);
+  if (a.q_dtype == FA_BF16) return fp8 ? choose_dim<BF16T, E4M3T>(a, cap) : choose_dim<BF16T, BF16T>(a, cap);
+  return fp8 ? choose_dim<F16T, E4M3T>(a, cap) : choose_dim<F16T, F16T>(a, cap);
 }
 
 }  // namespace fa_decode

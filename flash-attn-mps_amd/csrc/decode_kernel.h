@@ -758,9 +758,10 @@ DecodeKernel pick_decode_fp8_bf16(int64_t d, int64_t dv, int gt, bool cap, bool 
 DecodeKernel pick_decode_fp8_f16(int64_t d, int64_t dv, int gt, bool cap, bool alibi);
 
 // The matrix-core decode for GQA groups of DECODE_GQA_MIN_GROUP or more query
-// heads per KV head (decode_gqa.h, decode_gqa.hip): its kernel and LDS bytes,
-// or a null kernel when the arguments need the VALU kernel.  Its workgroups
-// take 32 query heads of one KV head each.  From 3 heads per KV head it
+// heads per KV head, and for any group when 64-dim KV heads run in pairs
+// (decode_gqa.h, decode_gqa.hip): its kernel and LDS bytes, or a null kernel
+// when the arguments need the VALU kernel.  Its workgroups take 32 query
+// heads of one KV head (or of a pair) each.  From 3 heads per KV head it
 // outruns the VALU kernel (32/8 at d128: 5.70 vs 5.55-5.67 TB/s, 24/8 E4M3
 // 4.26-4.35 vs 4.08); at 2 the VALU kernel is as fast or faster.
 constexpr int DECODE_GQA_MIN_GROUP = 3;
@@ -770,6 +771,7 @@ constexpr int DECODE_GQA_MAX_ROWS = 16;
 struct GqaChoice {
   DecodeKernel kern;
   size_t lds;
+  int pack;   // KV heads per workgroup (2: two 64-dim heads as one 128-dim virtual head)
 };
 GqaChoice pick_decode_gqa(const fa_attn_args& a);
 

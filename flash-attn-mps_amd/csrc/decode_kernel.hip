@@ -194,12 +194,13 @@ DecodeKernel select_decode(const fa_attn_args& a, int* gt_out) {
 
 // Workgroups per (request, split): KV heads x head tiles of the kernel that
 // runs (32 / max_seqlen_q query heads for the matrix-core GQA kernel, GT for
-// the VALU one).
+// the VALU one); the matrix-core kernel may take KV heads in pairs.
 int64_t decode_head_groups(const fa_attn_args& a, int gt) {
   const int64_t group = a.heads_q / a.heads_k;
   const int64_t ntok = a.max_seqlen_q > 1 ? a.max_seqlen_q : 1;
-  const int64_t tile = pick_decode_gqa(a).kern ? 32 / ntok : gt;
-  return a.heads_k * fa_ceil_div(group, tile);
+  const GqaChoice gqa = pick_decode_gqa(a);
+  if (gqa.kern) return a.heads_k / gqa.pack * fa_ceil_div(gqa.pack * group, 32 / ntok);
+  return a.heads_k * fa_ceil_div(group, gt);
 }
 
 }  // namespace

@@ -176,8 +176,8 @@ def _mixed_batch(p, a, fixed_order=False):
     dec.max_seqlen_q = 1   # the decode kernel takes the one-row requests only
     if not _lib.supported("fa_decode_supported", dec):
         return False
-    from ._decode import split_plan, uses_gqa_kernel, workgroups_per_token
-    groups = workgroups_per_token(p.heads, p.kv_heads, p.dim_qk, p.dim_v, uses_gqa_kernel(p, 1))
+    from ._decode import decode_workgroups, split_plan
+    groups = decode_workgroups(p, 1)
     splits, span = split_plan(p.batch, groups, p.max_k, 1 if fixed_order else 0)
     dec.num_splits, dec.split_span = splits, span
     if splits > 1:

@@ -58,9 +58,10 @@ def group_tile(heads, kv_heads, dim_qk, dim_v):
 
 
 # The matrix-core decode (decode_gqa.h): one query row per request from
-# DECODE_GQA_MIN_GROUP query heads per KV head, or 2..DECODE_GQA_MAX_ROWS rows
-# per request with any group (decode_kernel.h); its workgroups take 32 columns,
-# i.e. 32 // rows query heads.
+# DECODE_GQA_MIN_GROUP query heads per KV head (any group when 64-dim KV heads
+# run in pairs, gqa_pack), or 2..DECODE_GQA_MAX_ROWS rows per request with any
+# group (decode_kernel.h); its workgroups take 32 columns, i.e. 32 // rows
+# query heads.
 _GQA_MIN_GROUP = 3
 _GQA_MAX_ROWS = 16
 
@@ -72,7 +73,7 @@ def uses_gqa_kernel(p, rows=None):
     changes the split plan's workgroup estimate)."""
     page = p.k.shape[1] if p.paged else 0
     rows = p.max_q if rows is None else rows
-    rows_ok = (p.heads // p.kv_heads >= _GQA_MIN_GROUP) if rows <= 1 else rows <= _GQA_MAX_ROWS
+    rows_ok = (p.heads // p.kv_heads >= _GQA_MIN_GROUP or gqa_pack(p, 1) == 2) if rows <= 1 else rows <= _GQA_MAX_ROWS
     out_dtype = p.out.dtype if p.out is not None else p.output_dtype
     return (rows_ok and p.q.dtype in (torch.float16, torch.bfloat16) and out_dtype == p.q.dtype
             and p.k.dtype == p.v.dtype and p.k.dtype in (p.q.dtype, torch.float8_e4m3fn)
@@ -80,10 +81,33 @@ def uses_gqa_kernel(p, rows=None):
             and page % 16 == 0)
 
 
-def workgroups_per_token(heads, kv_heads, dim_qk, dim_v, gqa=False, rows=1):
-    """Decode workgroups per (request, split): KV heads x ceil(group / tile)."""
-    tile = 32 // max(rows, 1) if gqa else group_tile(heads, kv_heads, dim_qk, dim_v)
-    return kv_heads * -(-(heads // kv_heads) // tile)
+def gqa_pack(p, rows=1):
+    """KV heads per matrix-core decode workgroup at `rows` query rows per
+    request (mirrors packable() in decode_gqa.hip): 2 when 64-dim heads sit
+    next to each other in every key row (head stride 64 elements, rows of 128
+    or more), the KV heads pair up, both heads' query columns fit one
+    32-column tile, and the cache is E4M3 or has 8 or more KV heads; else 1."""
+    k, v = p.k, p.v
+    fits = 2 * (p.heads // p.kv_heads) * max(rows, 1) <= 32
+    return 2 if (p.dim_qk == 64 and p.kv_heads % 2 == 0 and k.stride(-2) == 64 and v.stride(-2) == 64
+                 and k.stride(-3) >= 128 and v.stride(-3) >= 128 and fits
+                 and (k.dtype == torch.float8_e4m3fn or p.kv_heads >= 8)) else 1
+
+
+def workgroups_per_token(heads, kv_heads, dim_qk, dim_v, gqa=False, rows=1, pack=1):
+    """Decode workgroups per (request, split): KV heads x ceil(group / tile);
+    the matrix-core kernel takes `pack` KV heads (and their query heads) per
+    workgroup."""
+    if gqa:
+        return kv_heads // pack * -(-(pack * (heads // kv_heads)) // (32 // max(rows, 1)))
+    return kv_heads * -(-(heads // kv_heads) // group_tile(heads, kv_heads, dim_qk, dim_v))
+
+
+def decode_workgroups(p, rows=1):
+    """Decode workgroups per (request, split) of Problem `p` at `rows` query
+    rows per request (mirrors decode_head_groups in decode_kernel.hip)."""
+    gqa = uses_gqa_kernel(p, rows)
+    return workgroups_per_token(p.heads, p.kv_heads, p.dim_qk, p.dim_v, gqa, rows, gqa_pack(p, rows) if gqa else 1)
 
 
 def decode(p, out, splits=None):
@@ -127,7 +151,7 @@ def _run_split_kv(p, a, rows, splits=None):
     the decode kernels do not take the arguments."""
     if not _lib.supported("fa_decode_supported", a):
         return False
-    groups = workgroups_per_token(p.heads, p.kv_heads, p.dim_qk, p.dim_v, uses_gqa_kernel(p, rows), rows)
+    groups = decode_workgroups(p, rows)
     left = p.window[0]
     visible = min(p.max_k, left + rows) if left >= 0 else p.max_k   # the first row's window
     splits, span = split_plan(p.batch, groups, visible, splits or p.splits)

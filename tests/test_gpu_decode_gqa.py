@@ -13,13 +13,18 @@ fp16 2e-3, bf16 1e-2, LSE 1e-4 max-abs.
 
 The same kernel takes 2-16 query rows per request (speculative decode) with
 any group: 32 (head, row) columns per workgroup, each column with its own
-causal/window key range.
+causal/window key range.  64-dim heads stored next to each other run in
+pairs when both heads' columns fit one tile (two KV heads as one 128-dim
+virtual head, each column keeping its own head's half; E4M3 caches, or 8+
+KV heads), also for groups of 1 and 2: paired groups of 1-16 heads, per-head
+descales, and heads that do not pair (strided, an odd head count, groups
+past 16 heads, 16-bit caches with few KV heads) are covered.
 """
 import pytest
 import torch
 
 from flash_attn_mps_amd import _lib
-from flash_attn_mps_amd._decode import decode_rows, uses_gqa_kernel
+from flash_attn_mps_amd._decode import decode_rows, gqa_pack, uses_gqa_kernel
 from harness import assert_parity, decode_attention, kernel_args, oracle_attention, problem
 
 pytestmark = pytest.mark.gpu
@@ -45,7 +50,8 @@ def _pool(stored, page, kv_heads, dim, dtype, device, seed, valid_from):
     return kc.to(dtype).to(device), vc.to(dtype).to(device), table.to(device), cols
 
 
-@pytest.mark.parametrize("heads,kv_heads", [(3, 1), (8, 2), (5, 1), (8, 1), (14, 2), (32, 1), (48, 1), (64, 2)])
+@pytest.mark.parametrize("heads,kv_heads", [(3, 1), (8, 2), (5, 1), (8, 1), (14, 2), (32, 1), (48, 1), (64, 2),
+                                             (6, 2), (48, 2), (30, 6), (32, 8), (40, 8), (16, 16), (16, 8)])
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("splits", [0, 1, 3])
@@ -60,7 +66,9 @@ def test_groups_dims_and_splits(device, heads, kv_heads, d, dtype, splits):
     buffer = torch.full((len(lengths), heads + 8, d), 7.0, device=device, dtype=dtype)
     kw = dict(cu_seqlens_q=cu_q, seqused_k=used, block_table=table, s_aux=sinks)
     p = problem(q, kc, vc, max_seqlen_q=1, max_seqlen_k=cols * page, **kw)
-    assert uses_gqa_kernel(p)
+    # Groups of 1 and 2 take this kernel only with paired 64-dim heads.
+    assert uses_gqa_kernel(p) == (heads // kv_heads >= 3 or gqa_pack(p) == 2)
+    assert gqa_pack(p) == (2 if d == 64 and (heads, kv_heads) in ((32, 8), (40, 8), (16, 16), (16, 8)) else 1)
     got, lse = decode_attention(q, kc, vc, max_seqlen_k=cols * page, num_splits=splits, out=buffer[:, :heads], **kw)
     ref, ref_lse = oracle_attention(q, kc, vc, cu_q, used_k=used, block_table=table, sinks=sinks)
     assert_parity(got, lse, ref, ref_lse)
@@ -114,7 +122,7 @@ def test_packed_keys_explicit_scale_and_descales(device, d):
     assert_parity(got, lse, ref, ref_lse)
 
 
-@pytest.mark.parametrize("heads,kv_heads", [(8, 1), (16, 2), (64, 2)])
+@pytest.mark.parametrize("heads,kv_heads", [(8, 1), (16, 2), (64, 2), (48, 2), (24, 8), (16, 16), (8, 4)])
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("q_dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("splits", [0, 3])
@@ -141,7 +149,8 @@ def test_e4m3_caches_with_descales(device, heads, kv_heads, d, q_dtype, splits):
     kw = dict(cu_seqlens_q=cu_q.to(device), seqused_k=used.to(device), block_table=table.to(device),
               s_aux=sinks.to(device), softcap=30.0, k_descale=kd.to(device), v_descale=vd.to(device))
     p = problem(q.to(device), kc.to(device), vc.to(device), max_seqlen_q=1, max_seqlen_k=cols * page, **kw)
-    assert uses_gqa_kernel(p)
+    assert uses_gqa_kernel(p) == (heads // kv_heads >= 3 or gqa_pack(p) == 2)
+    assert gqa_pack(p) == (2 if d == 64 and (heads, kv_heads) in ((16, 2), (24, 8), (16, 16), (8, 4)) else 1)
     got, lse = decode_attention(q.to(device), kc.to(device), vc.to(device), max_seqlen_k=cols * page,
                                 num_splits=splits, **kw)
     ref, ref_lse = oracle_attention(q, kc, vc, cu_q, used_k=used, block_table=table, sinks=sinks, softcap=30.0,
@@ -190,13 +199,14 @@ def test_rows_per_request(device, q_lens, heads, kv_heads, causal, splits):
 @pytest.mark.parametrize("window", [(0, 0), (45, 0), (20, 3), (1000, -1)])
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("splits", [0, 2])
-def test_rows_windows_softcap_leftpad(device, window, d, splits):
+@pytest.mark.parametrize("heads,kv_heads", [(16, 4), (32, 8)])
+def test_rows_windows_softcap_leftpad(device, window, d, splits, heads, kv_heads):
     """Multi-row decode with left/right windows (each row's own window),
-    softcap 30, descales of a 16-bit cache and NaN left padding."""
+    softcap 30, descales of a 16-bit cache and NaN left padding (32 / 8
+    heads of 64 dims at 4 rows: paired KV heads filling one tile)."""
     q_lens, left = [3, 4, 1, 4, 2], [0, 5, 17, 3, 16]
     lengths = [3, 40, 777, 1500, 33]
     stored = [n + p for n, p in zip(lengths, left)]
-    heads, kv_heads = 16, 4
     kc, vc, table, cols = _pool(stored, 48, kv_heads, d, torch.float16, device, 750 + d + splits, left)
     g = torch.Generator().manual_seed(751 + d)
     q = torch.randn(sum(q_lens), heads, d, generator=g).to(torch.float16).to(device)
@@ -213,9 +223,12 @@ def test_rows_windows_softcap_leftpad(device, window, d, splits):
 
 @pytest.mark.parametrize("q_lens", [[2, 2, 1], [5, 8, 3]])
 @pytest.mark.parametrize("q_dtype", [torch.bfloat16, torch.float16])
-def test_rows_e4m3_cache(device, q_lens, q_dtype):
-    """Multi-row decode over an E4M3 paged cache with descales and sinks."""
-    heads, kv_heads, d, page = 32, 8, 128, 16
+@pytest.mark.parametrize("heads,d", [(32, 128), (32, 64), (24, 64)])
+def test_rows_e4m3_cache(device, q_lens, q_dtype, heads, d):
+    """Multi-row decode over an E4M3 paged cache with descales and sinks
+    (64-dim heads in pairs: 24 / 8 heads at 4 rows put 6 heads of two KV
+    heads in one tile)."""
+    kv_heads, page = 8, 16
     lengths = [300, 2049, 77]
     g = torch.Generator().manual_seed(760 + sum(q_lens))
     cols = max(-(-n // page) for n in lengths) + 1
@@ -231,6 +244,42 @@ def test_rows_e4m3_cache(device, q_lens, q_dtype):
               k_descale=kd.to(device), v_descale=vd.to(device))
     (got, lse), cu_q = _rows_call(q.to(device), kc.to(device), vc.to(device), q_lens, max_seqlen_k=cols * page, **kw)
     ref, ref_lse = oracle_attention(q, kc, vc, cu_q, used_k=used, block_table=table, sinks=sinks, causal=True,
+                                    k_descale=kd, v_descale=vd)
+    assert_parity(got, lse, ref, ref_lse)
+
+
+@pytest.mark.parametrize("layout", ["pairs", "strided", "odd"])
+@pytest.mark.parametrize("kind", [torch.bfloat16, torch.float8_e4m3fn])
+def test_head_pairs_and_unpaired_layouts(device, layout, kind):
+    """64-dim heads: neighbouring KV heads run in pairs; heads of a cache
+    sliced from wider rows (head stride 128) and an odd KV head count run one
+    KV head per workgroup.  Per-(request, KV head) descales differ between the
+    two heads of a pair, so a column scaled with its neighbour's descale
+    fails the bar."""
+    lengths, page, d = [1, 31, 33, 0, 300, 2049, 77], 16, 64
+    kv_heads = 3 if layout == "odd" else 8
+    heads = 6 * kv_heads
+    g = torch.Generator().manual_seed(770 + len(layout))
+    cols = max(-(-n // page) for n in lengths) + 1
+    pool = len(lengths) * cols
+    table = torch.randperm(pool, generator=g).int().reshape(len(lengths), cols)
+    width = 2 * d if layout == "strided" else d
+    kc = torch.randn(pool, page, kv_heads, width, generator=g).to(kind)
+    vc = (torch.randn(pool, page, kv_heads, width, generator=g) * 0.5).to(kind)
+    q = torch.randn(len(lengths), heads, d, generator=g).to(torch.bfloat16)
+    kd = torch.rand(len(lengths), kv_heads, generator=g) * 0.5 + 0.5
+    vd = torch.rand(len(lengths), kv_heads, generator=g) * 0.5 + 0.5
+    if kind == torch.float8_e4m3fn:
+        kd, vd = kd * 0.1, vd * 0.5
+    cu_q, used = torch.arange(len(lengths) + 1, dtype=torch.int32), torch.tensor(lengths, dtype=torch.int32)
+    kg, vg = kc.to(device)[..., :d], vc.to(device)[..., :d]
+    kw = dict(cu_seqlens_q=cu_q.to(device), seqused_k=used.to(device), block_table=table.to(device),
+              k_descale=kd.to(device), v_descale=vd.to(device))
+    p = problem(q.to(device), kg, vg, max_seqlen_q=1, max_seqlen_k=cols * page, **kw)
+    assert uses_gqa_kernel(p)
+    assert gqa_pack(p) == (2 if layout == "pairs" else 1)
+    got, lse = decode_attention(q.to(device), kg, vg, max_seqlen_k=cols * page, **kw)
+    ref, ref_lse = oracle_attention(q, kc[..., :d], vc[..., :d], cu_q, used_k=used, block_table=table,
                                     k_descale=kd, v_descale=vd)
     assert_parity(got, lse, ref, ref_lse)
 

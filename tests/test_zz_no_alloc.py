@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from flash_attn_mps_amd import _lib
-from flash_attn_mps_amd._decode import split_plan, uses_gqa_kernel, workgroups_per_token
+from flash_attn_mps_amd._decode import decode_workgroups, split_plan, workgroups_per_token
 from harness import kernel_args, problem
 
 pytestmark = pytest.mark.gpu
@@ -67,7 +67,7 @@ def _python_plan(t):
     batch, heads, dim = t["q"].shape
     p = problem(t["q"], t["k"], t["v"], cu_seqlens_q=t["cu_q"], seqused_k=t["used"], max_seqlen_q=1,
                 max_seqlen_k=t["max_ctx"], block_table=t["table"])
-    groups = workgroups_per_token(heads, t["k"].shape[2], dim, dim, uses_gqa_kernel(p))
+    groups = decode_workgroups(p)
     wl = t["window"][0]
     visible = min(t["max_ctx"], wl + 1) if wl >= 0 else t["max_ctx"]
     return split_plan(batch, groups, visible, 0)
