@@ -78,12 +78,13 @@ def test_groups_dims_and_splits(device, heads, kv_heads, d, dtype, splits):
 @pytest.mark.parametrize("window", [(-1, -1), (0, 0), (45, 0), (1000, -1)])
 @pytest.mark.parametrize("splits", [0, 2])
 @pytest.mark.parametrize("page", [16, 48])
-def test_softcap_windows_and_left_padding(device, window, splits, page):
+@pytest.mark.parametrize("heads,kv_heads,d", [(32, 2, 128), (32, 8, 64)])
+def test_softcap_windows_and_left_padding(device, window, splits, page, heads, kv_heads, d):
     """Left padding of 0-17 slots holding NaN before each request's keys; a
-    left window then starts a split in the middle of a 16-key group."""
+    left window then starts a split in the middle of a 16-key group (32 / 8
+    heads of 64 dims: paired KV heads)."""
     lengths, left = [1, 40, 777, 0, 1500, 33], [0, 5, 17, 3, 0, 16]
     stored = [n + p for n, p in zip(lengths, left)]
-    heads, kv_heads, d = 32, 2, 128
     kc, vc, table, cols = _pool(stored, page, kv_heads, d, torch.bfloat16, device, 710 + page + splits, left)
     g = torch.Generator().manual_seed(711)
     q = torch.randn(len(lengths), heads, d, generator=g).to(torch.bfloat16).to(device)
