@@ -3,8 +3,8 @@
 
 namespace fa_decode {
 
-DecodeKernel pick_decode_f16(int64_t d, int64_t dv, int gt, bool cap, bool alibi) {
-  return pick_dims<F16T, F16T, F16T>(d, dv, gt, cap, alibi);
+DecodeKernel pick_decode_f16(int64_t d, int64_t dv, int gt, bool cap, bool alibi, int pk) {
+  return pick_dims<F16T, F16T, F16T>(d, dv, gt, cap, alibi, pk);
 }
 
 }  // namespace fa_decode

@@ -326,14 +326,27 @@ FA_DEV SplitItem split_item(const fa_attn_args& a, int rows, int span) {
 // past the real dims read the row's last real chunk (always in bounds), with
 // a zero query there, so they add nothing to Q.K; their V columns are never
 // stored.
+// PK = 2: two neighbouring KV heads whose rows sit next to each other in
+// every key row run in one workgroup as one row of 2 D elements, so each
+// 16-lane row reads 512-byte (or longer) runs instead of 256-byte ones.  A
+// lane's share of a head row is whole 16-byte pieces (piece j at byte
+// 256 j + 16 l), so in the paired row the first head's pieces come first and
+// the second head's follow, each in its own head's layout: query head g of
+// the workgroup (heads of the first KV head, then of the second) takes the
+// K and V words of its half only, and the arithmetic per byte is that of
+// one head.  GT counts the query heads of both halves.
 template <typename CT, typename KT, typename VT, int D, int DV, int GT, bool CAP, int DT = D, int DVT = DV,
-          bool ALIBI = false>
+          bool ALIBI = false, int PK = 1>
 __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const fa_attn_args a, const int span) {
   constexpr int EK = D / 16, EV = DV / 16;
   constexpr int LK = DT / EK, LV = DVT / EV;   // lanes of a 16-lane row holding real dims
   static_assert(DT % EK == 0 && DVT % EV == 0 && DT <= D && DVT <= DV, "true head dims fill whole lane chunks");
-  constexpr int KB = EK * KT::bytes, VB = EV * VT::bytes;
-  constexpr int NT = DecodeRows<KB, VB>::value;
+  constexpr int KB = EK * KT::bytes, VB = EV * VT::bytes;   // one head's bytes per lane
+  static_assert(PK == 1 || (PK == 2 && DT == D && DVT == DV && KB % 16 == 0 && VB % 16 == 0 && GT % 2 == 0),
+                "paired heads: unpadded rows of whole 16-byte lane pieces");
+  constexpr int KBP = PK * KB, VBP = PK * VB;   // bytes per lane of the (paired) row
+  constexpr int GH = GT / PK;                   // query heads per KV head of the workgroup
+  constexpr int NT = DecodeRows<KBP, VBP>::value;
   constexpr int STEP = 4 * NT;          // positions of one wave step
   constexpr int WSTRIDE = 4 * STEP;     // positions between a wave's consecutive steps
   static_assert(EK % 4 == 0 && EV % 4 == 0 && KB % 4 == 0 && VB % 4 == 0, "decode tile shape");
@@ -341,6 +354,8 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
   static_assert(LV == 16 || piece_count(VB) == 1, "padded V rows use a single piece per lane");
   __shared__ float sm_m[4][GT], sm_l[4][GT];
   __shared__ float sm_acc[4][GT][DV];
+  // Half of the paired row that query head g of the workgroup reads.
+  auto half_of = [](int g) { return PK > 1 ? g / GH : 0; };
 
   // Head groups are the fastest grid dimension: the workgroups of one
   // (request, split) run together and read whole token rows of the same pages;
@@ -361,7 +376,10 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
   // Workgroup x holds query heads t GT .. t GT + GT - 1 of KV head kh's group
   // (t = x % tiles, tiles = ceil(group / GT)); a last tile past the group
   // recomputes its last real head in the spare slots and stores nothing there.
-  const int group = (int)(a.heads_q / a.heads_k), tiles = (group + GT - 1) / GT;
+  // Paired (PK = 2): kh numbers KV head pairs, whose PK groups are one
+  // group of contiguous query heads, held whole by the workgroup (GT = PK x
+  // the heads per KV head).
+  const int group = PK * (int)(a.heads_q / a.heads_k), tiles = (group + GT - 1) / GT;
   const int kh = blockIdx.x / tiles, t0 = (blockIdx.x % tiles) * GT;
   const int h0 = kh * group + t0, nreal = min(GT, group - t0);
   const int vis_begin = decode_vis_begin(a, r.k_len);
@@ -371,10 +389,16 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
   const int64_t tq = r.q_begin;
   const int S = a.num_splits;
 
-  const float sscale = a.softmax_scale * descale_of(a.q_descale, a.q_descale_stride, b, kh) *
-                       descale_of(a.k_descale, a.k_descale_stride, b, kh) * (CAP ? 1.0f : LOG2E);
+  // Descales per KV head (of each half when paired).
+  float sscale[PK], vscale[PK];
+#pragma unroll
+  for (int u = 0; u < PK; ++u) {
+    const int kv = PK * kh + u;
+    sscale[u] = a.softmax_scale * descale_of(a.q_descale, a.q_descale_stride, b, kv) *
+                descale_of(a.k_descale, a.k_descale_stride, b, kv) * (CAP ? 1.0f : LOG2E);
+    vscale[u] = descale_of(a.v_descale, a.v_descale_stride, b, kv);
+  }
   const float cap_in = CAP ? 2.0f * LOG2E / a.softcap : 0.0f, cap_out = a.softcap * LOG2E;
-  const float vscale = descale_of(a.v_descale, a.v_descale_stride, b, kh);
   // ALiBi: -slope |q_pos - key| in log2 units after the softcap
   // (flash_attn_mps/kernels/attention.metal:47-51); the query sits at key
   // position k_len - 1, storage row qrow, so the bias is slope (row - qrow).
@@ -450,15 +474,15 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
   // base + blk * page_stride + r * row_stride + kh * head_stride + l16 * E * bytes.
   const uint32_t kpage_b = (uint32_t)(a.k_stride[0] * KT::bytes), vpage_b = (uint32_t)(a.v_stride[0] * VT::bytes);
   const uint32_t krow_b = (uint32_t)(a.k_stride[1] * KT::bytes), vrow_b = (uint32_t)(a.v_stride[1] * VT::bytes);
-  const char* kbase = (const char*)a.k + (int64_t)kh * a.k_stride[2] * KT::bytes;
-  uint32_t koff[piece_count(KB)];
+  const char* kbase = (const char*)a.k + (int64_t)(PK * kh) * a.k_stride[2] * KT::bytes;
+  uint32_t koff[piece_count(KBP)];
 #pragma unroll
-  for (int j = 0; j < piece_count(KB); ++j) koff[j] = 16 * piece_start(KB, j) + piece_bytes(KB, j) * lq;
-  const char* vbase = (const char*)a.v + (int64_t)kh * a.v_stride[2] * VT::bytes;
+  for (int j = 0; j < piece_count(KBP); ++j) koff[j] = 16 * piece_start(KBP, j) + piece_bytes(KBP, j) * lq;
+  const char* vbase = (const char*)a.v + (int64_t)(PK * kh) * a.v_stride[2] * VT::bytes;
   const int lv = min(l16, LV - 1);
-  uint32_t voff[piece_count(VB)];
+  uint32_t voff[piece_count(VBP)];
 #pragma unroll
-  for (int j = 0; j < piece_count(VB); ++j) voff[j] = 16 * piece_start(VB, j) + piece_bytes(VB, j) * lv;
+  for (int j = 0; j < piece_count(VBP); ++j) voff[j] = 16 * piece_start(VBP, j) + piece_bytes(VBP, j) * lv;
 
   // Address of the split's first key: the read target of rows with no valid position.
   const char* ksafe = kbase;
@@ -498,7 +522,7 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
   // split (rows with none read the split's first key).  The choice is a
   // scalar branch that only sets offsets, so the loads of consecutive steps
   // never alias registers the compiler must wait on.
-  auto issue = [&](int t, uint32_t (&kw)[NT][KB / 4], uint32_t (&vw)[NT][VB / 4]) {
+  auto issue = [&](int t, uint32_t (&kw)[NT][KBP / 4], uint32_t (&vw)[NT][VBP / 4]) {
     const int sbt = sb0 + WSTRIDE * t;
     const bool full = sbt >= plo && sbt + STEP <= phi;
     const char* krow = kbase + kin;
@@ -535,9 +559,9 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
       }
     }
 #pragma unroll
-    for (int i = 0; i < NT; ++i) load_pieces_nt<KB>(krow + ko[i], koff, kw[i]);
+    for (int i = 0; i < NT; ++i) load_pieces_nt<KBP>(krow + ko[i], koff, kw[i]);
 #pragma unroll
-    for (int i = 0; i < NT; ++i) load_pieces_nt<VB>(vrow + vo[i], voff, vw[i]);
+    for (int i = 0; i < NT; ++i) load_pieces_nt<VBP>(vrow + vo[i], voff, vw[i]);
     if (P) {
       inr += wrap;
       kin += (uint64_t)wrap * krow_b;
@@ -553,20 +577,20 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
     }
   };
 
-  auto compute = [&](int t, const uint32_t (&kw)[NT][KB / 4], const uint32_t (&vw)[NT][VB / 4]) {
+  auto compute = [&](int t, const uint32_t (&kw)[NT][KBP / 4], const uint32_t (&vw)[NT][VBP / 4]) {
     const int sbt = sb0 + WSTRIDE * t;
     const bool full = sbt >= plo && sbt + STEP <= phi;
     const int rp = rp0 + WSTRIDE * t;
     float s[GT][NT];
 #pragma unroll
     for (int i = 0; i < NT; ++i) {
-      uint32_t kp[EK / 2];
-      k_pairs<CT, KT, EK>(kw[i], kp);
+      uint32_t kp[PK * EK / 2];
+      k_pairs<CT, KT, PK * EK>(kw[i], kp);
 #pragma unroll
       for (int g = 0; g < GT; ++g) {
         float dot = 0.0f;
 #pragma unroll
-        for (int j = 0; j < EK / 2; ++j) dot = dot2<CT>(qp[g][j], kp[j], dot);
+        for (int j = 0; j < EK / 2; ++j) dot = dot2<CT>(qp[g][j], kp[half_of(g) * (EK / 2) + j], dot);
         s[g][i] = dot;
       }
     }
@@ -574,7 +598,7 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
     for (int g = 0; g < GT; ++g)
 #pragma unroll
       for (int i = 0; i < NT; ++i) {
-        float v = row16_sum(s[g][i]) * sscale;
+        float v = row16_sum(s[g][i]) * sscale[half_of(g)];
         if constexpr (CAP) v = cap_out * (1.0f - 2.0f * __builtin_amdgcn_rcpf(fast_exp2(v * cap_in) + 1.0f));
         if constexpr (ALIBI) v = fmaf(slope2[g], (float)(rp + i - qrow), v);
         s[g][i] = v;
@@ -611,17 +635,17 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
     }
 #pragma unroll
     for (int i = 0; i < NT; ++i) {
-      float vf[EV];
-      words_to_f32<VT, EV>(vw[i], vf);
+      float vf[PK * EV];
+      words_to_f32<VT, PK * EV>(vw[i], vf);
 #pragma unroll
       for (int g = 0; g < GT; ++g)
 #pragma unroll
-        for (int e = 0; e < EV; ++e) acc[g][e] = fmaf(s[g][i], vf[e], acc[g][e]);
+        for (int e = 0; e < EV; ++e) acc[g][e] = fmaf(s[g][i], vf[half_of(g) * EV + e], acc[g][e]);
     }
   };
 
   if (nsteps > 0) {
-    uint32_t kwa[NT][KB / 4], vwa[NT][VB / 4], kwb[NT][KB / 4], vwb[NT][VB / 4];
+    uint32_t kwa[NT][KBP / 4], vwa[NT][VBP / 4], kwb[NT][KBP / 4], vwb[NT][VBP / 4];
     // Steps t + 1 and t + 2 are issued unconditionally (past the last step
     // they read the split's first key: one K and one V row per wave,
     // cached) and only the compute of step t + 1 is conditional, so the loop
@@ -686,7 +710,7 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
       L += sm_l[w][g] * f;
       O += sm_acc[w][g][d] * f;
     }
-    const float norm = L > 0.0f ? vscale / L : 0.0f;
+    const float norm = L > 0.0f ? vscale[half_of(g)] / L : 0.0f;
     const float lse = L > 0.0f ? M * LN2 + logf(L) : -INFINITY;
     const int h = h0 + g;
     if (S == 1) {
@@ -743,8 +767,30 @@ inline int64_t decode_tile_dim(int64_t d) {
   }
 }
 
+// Paired KV heads (PK = 2): 2 x the group's heads per workgroup; 4 only at
+// d128 and for E4M3 d256 (16-bit d256 rows hold twice the registers).
+template <typename CT, typename KT, typename VT, bool CAP>
+DecodeKernel pick_pair(int64_t d, int gt) {
+  if (d == 128) {
+    if constexpr (KT::bytes == 2) {
+      if (gt == 2) return decode_kernel<CT, KT, VT, 128, 128, 2, CAP, 128, 128, false, 2>;
+      if (gt == 4) return decode_kernel<CT, KT, VT, 128, 128, 4, CAP, 128, 128, false, 2>;
+    }
+  } else if (d == 256) {
+    if (gt == 2) return decode_kernel<CT, KT, VT, 256, 256, 2, CAP, 256, 256, false, 2>;
+    if constexpr (KT::bytes == 1) {
+      if (gt == 4) return decode_kernel<CT, KT, VT, 256, 256, 4, CAP, 256, 256, false, 2>;
+    }
+  }
+  return nullptr;
+}
+
 template <typename CT, typename KT, typename VT>
-DecodeKernel pick_dims(int64_t d, int64_t dv, int gt, bool cap, bool alibi) {
+DecodeKernel pick_dims(int64_t d, int64_t dv, int gt, bool cap, bool alibi, int pk) {
+  if (pk == 2) {
+    if (alibi || d != dv) return nullptr;
+    return cap ? pick_pair<CT, KT, VT, true>(d, gt) : pick_pair<CT, KT, VT, false>(d, gt);
+  }
   // ALiBi variants exist without softcap only (softcap + ALiBi: generic kernel).
   if (alibi) return cap ? nullptr : pick_dims_cap<CT, KT, VT, false, true>(d, dv, gt);
   return cap ? pick_dims_cap<CT, KT, VT, true, false>(d, dv, gt) : pick_dims_cap<CT, KT, VT, false, false>(d, dv, gt);
@@ -752,10 +798,10 @@ DecodeKernel pick_dims(int64_t d, int64_t dv, int gt, bool cap, bool alibi) {
 
 // Variants by (query, K/V) types, instantiated in decode_inst_*.hip so they
 // compile in parallel.
-DecodeKernel pick_decode_bf16(int64_t d, int64_t dv, int gt, bool cap, bool alibi);
-DecodeKernel pick_decode_f16(int64_t d, int64_t dv, int gt, bool cap, bool alibi);
-DecodeKernel pick_decode_fp8_bf16(int64_t d, int64_t dv, int gt, bool cap, bool alibi);
-DecodeKernel pick_decode_fp8_f16(int64_t d, int64_t dv, int gt, bool cap, bool alibi);
+DecodeKernel pick_decode_bf16(int64_t d, int64_t dv, int gt, bool cap, bool alibi, int pk);
+DecodeKernel pick_decode_f16(int64_t d, int64_t dv, int gt, bool cap, bool alibi, int pk);
+DecodeKernel pick_decode_fp8_bf16(int64_t d, int64_t dv, int gt, bool cap, bool alibi, int pk);
+DecodeKernel pick_decode_fp8_f16(int64_t d, int64_t dv, int gt, bool cap, bool alibi, int pk);
 
 // The matrix-core decode for GQA groups of DECODE_GQA_MIN_GROUP or more query
 // heads per KV head, and for any group when 64-dim KV heads run in pairs

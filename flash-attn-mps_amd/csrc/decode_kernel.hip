@@ -147,6 +147,28 @@ int decode_group_tile(const fa_attn_args& a) {
   return gt;
 }
 
+// KV heads per VALU-decode workgroup: 2 (decode_kernel PK = 2) when two
+// neighbouring heads' rows sit next to each other in every key row (head
+// stride = the head dim, rows of two heads or more), a lane's share of a
+// head row is whole 16-byte pieces (16-bit d128 / d256, E4M3 d256), no
+// ALiBi, the pair's 2 x group query heads fit one tile (groups of 1-2; 1
+// for 16-bit d256), and there are 8 KV heads or more (16 for 16-bit d256).
+// Each 16-lane row then reads 512-byte runs or longer.  Measured (64
+// requests of U[512, 32768] keys, one query row): 16-bit d128 16/16 6.26 ->
+// 6.66 TB/s, 32/32 6.43 -> 6.88, 16/8 6.03 -> 6.25, 8/8 6.11 -> 6.41, d256
+// 16/16 6.28 -> 6.68; config 4 (E4M3 d256, 16/8) 329 -> 325 us.  With fewer
+// KV heads pairing halves an already small grid: 16-bit d128 8/4 5.88 ->
+// 5.60, E4M3 d256 4/2 5.03 -> 4.52, 16-bit d256 8/8 6.32 -> 6.21.
+int valu_pair(const fa_attn_args& a) {
+  const int64_t d = a.head_dim_qk, group = a.heads_q / a.heads_k;
+  if (a.alibi || a.head_dim_v != d || (d != 128 && d != 256) || (d * elem_size(a.k_dtype)) % 256) return 1;
+  if (a.heads_k % 2 || a.k_stride[2] != d || a.v_stride[2] != d || a.k_stride[1] < 2 * d || a.v_stride[1] < 2 * d)
+    return 1;
+  const bool wide16 = d == 256 && a.k_dtype != FA_E4M3;
+  if (a.heads_k < (wide16 ? 16 : 8)) return 1;
+  return group <= (wide16 ? 1 : 2) ? 2 : 1;
+}
+
 bool chunk_aligned(const void* p, const int64_t* st, int nstrides, int esz, int bytes_per_lane) {
   const int c = bytes_per_lane % 16 == 0 ? 16 : bytes_per_lane % 8 == 0 ? 8 : 4;
   if (((uintptr_t)p) % c) return false;
@@ -179,28 +201,30 @@ DecodeKernel select_decode(const fa_attn_args& a, int* gt_out) {
   // FP8 K widens exactly to either.
   if (a.q_dtype != FA_BF16 && a.q_dtype != FA_F16) return nullptr;
   if (a.q_stride[2] == 1 && !chunk_aligned(a.q, a.q_stride, 2, 2, (int)(tq / 16) * 2)) return nullptr;
-  const int gt = decode_group_tile(a);
+  const int pk = valu_pair(a);
+  const int gt = pk == 2 ? 2 * (int)(a.heads_q / a.heads_k) : decode_group_tile(a);
   *gt_out = gt;
   const bool qbf = a.q_dtype == FA_BF16, cap = a.softcap > 0.0f, alibi = a.alibi != nullptr;
   const int64_t dq = a.head_dim_qk, dv = a.head_dim_v;
   switch (a.k_dtype) {
-    case FA_BF16: return qbf ? pick_decode_bf16(dq, dv, gt, cap, alibi) : nullptr;
-    case FA_F16: return qbf ? nullptr : pick_decode_f16(dq, dv, gt, cap, alibi);
+    case FA_BF16: return qbf ? pick_decode_bf16(dq, dv, gt, cap, alibi, pk) : nullptr;
+    case FA_F16: return qbf ? nullptr : pick_decode_f16(dq, dv, gt, cap, alibi, pk);
     case FA_E4M3:
-      return qbf ? pick_decode_fp8_bf16(dq, dv, gt, cap, alibi) : pick_decode_fp8_f16(dq, dv, gt, cap, alibi);
+      return qbf ? pick_decode_fp8_bf16(dq, dv, gt, cap, alibi, pk) : pick_decode_fp8_f16(dq, dv, gt, cap, alibi, pk);
     default: return nullptr;
   }
 }
 
 // Workgroups per (request, split): KV heads x head tiles of the kernel that
 // runs (32 / max_seqlen_q query heads for the matrix-core GQA kernel, GT for
-// the VALU one); the matrix-core kernel may take KV heads in pairs.
+// the VALU one); either kernel may take KV heads in pairs.
 int64_t decode_head_groups(const fa_attn_args& a, int gt) {
   const int64_t group = a.heads_q / a.heads_k;
   const int64_t ntok = a.max_seqlen_q > 1 ? a.max_seqlen_q : 1;
   const GqaChoice gqa = pick_decode_gqa(a);
   if (gqa.kern) return a.heads_k / gqa.pack * fa_ceil_div(gqa.pack * group, 32 / ntok);
-  return a.heads_k * fa_ceil_div(group, gt);
+  const int pk = valu_pair(a);
+  return a.heads_k / pk * fa_ceil_div(pk * group, gt);
 }
 
 }  // namespace

@@ -94,20 +94,43 @@ def gqa_pack(p, rows=1):
                  and (k.dtype == torch.float8_e4m3fn or p.kv_heads >= 8)) else 1
 
 
+def valu_pair(p):
+    """KV heads per VALU-decode workgroup (mirrors valu_pair() in
+    decode_kernel.hip): 2 when neighbouring heads' rows sit next to each other
+    in every key row, a lane's share of a head row is whole 16-byte pieces
+    (16-bit d128 / d256, E4M3 d256), there is no ALiBi, the group has 1-2
+    query heads per KV head (1 for 16-bit d256), and there are 8 or more KV
+    heads (16 for 16-bit d256); else 1."""
+    k, v, d = p.k, p.v, p.dim_qk
+    if p.alibi is not None or p.dim_v != d or d not in (128, 256) or (d * k.element_size()) % 256:
+        return 1
+    if (p.kv_heads % 2 or k.stride(-2) != d or v.stride(-2) != d or k.stride(-3) < 2 * d
+            or v.stride(-3) < 2 * d):
+        return 1
+    wide16 = d == 256 and k.dtype != torch.float8_e4m3fn
+    if p.kv_heads < (16 if wide16 else 8):
+        return 1
+    return 2 if p.heads // p.kv_heads <= (1 if wide16 else 2) else 1
+
+
 def workgroups_per_token(heads, kv_heads, dim_qk, dim_v, gqa=False, rows=1, pack=1):
     """Decode workgroups per (request, split): KV heads x ceil(group / tile);
-    the matrix-core kernel takes `pack` KV heads (and their query heads) per
-    workgroup."""
+    either kernel takes `pack` KV heads (and their query heads) per
+    workgroup (the VALU kernel then holds the pair's heads in one tile)."""
+    group = heads // kv_heads
     if gqa:
-        return kv_heads // pack * -(-(pack * (heads // kv_heads)) // (32 // max(rows, 1)))
-    return kv_heads * -(-(heads // kv_heads) // group_tile(heads, kv_heads, dim_qk, dim_v))
+        return kv_heads // pack * -(-(pack * group) // (32 // max(rows, 1)))
+    if pack == 2:
+        return kv_heads // 2
+    return kv_heads * -(-group // group_tile(heads, kv_heads, dim_qk, dim_v))
 
 
 def decode_workgroups(p, rows=1):
     """Decode workgroups per (request, split) of Problem `p` at `rows` query
     rows per request (mirrors decode_head_groups in decode_kernel.hip)."""
     gqa = uses_gqa_kernel(p, rows)
-    return workgroups_per_token(p.heads, p.kv_heads, p.dim_qk, p.dim_v, gqa, rows, gqa_pack(p, rows) if gqa else 1)
+    pack = gqa_pack(p, rows) if gqa else valu_pair(p)
+    return workgroups_per_token(p.heads, p.kv_heads, p.dim_qk, p.dim_v, gqa, rows, pack)
 
 
 def decode(p, out, splits=None):
