@@ -326,15 +326,15 @@ FA_DEV SplitItem split_item(const fa_attn_args& a, int rows, int span) {
 // past the real dims read the row's last real chunk (always in bounds), with
 // a zero query there, so they add nothing to Q.K; their V columns are never
 // stored.
-// PK = 2: two neighbouring KV heads whose rows sit next to each other in
-// every key row run in one workgroup as one row of 2 D elements, so each
-// 16-lane row reads 512-byte (or longer) runs instead of 256-byte ones.  A
-// lane's share of a head row is whole 16-byte pieces (piece j at byte
-// 256 j + 16 l), so in the paired row the first head's pieces come first and
-// the second head's follow, each in its own head's layout: query head g of
-// the workgroup (heads of the first KV head, then of the second) takes the
-// K and V words of its half only, and the arithmetic per byte is that of
-// one head.  GT counts the query heads of both halves.
+// PK = 2: two neighbouring KV heads, whose rows sit next to each other in
+// every key row, run in one workgroup: every lane loads its pieces of both
+// heads' rows (the second head's one head row further on), so a 16-lane
+// row's loads of one key cover both rows back to back, twice the run of one
+// head.  A lane's words hold the first head's pieces, then the second's,
+// each in its own head's layout: query head g of the workgroup (heads of
+// the first KV head, then of the second) takes the K and V words of its half
+// only, and the arithmetic per byte is that of one head.  GT counts the
+// query heads of both halves.
 template <typename CT, typename KT, typename VT, int D, int DV, int GT, bool CAP, int DT = D, int DVT = DV,
           bool ALIBI = false, int PK = 1>
 __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const fa_attn_args a, const int span) {
@@ -342,8 +342,7 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
   constexpr int LK = DT / EK, LV = DVT / EV;   // lanes of a 16-lane row holding real dims
   static_assert(DT % EK == 0 && DVT % EV == 0 && DT <= D && DVT <= DV, "true head dims fill whole lane chunks");
   constexpr int KB = EK * KT::bytes, VB = EV * VT::bytes;   // one head's bytes per lane
-  static_assert(PK == 1 || (PK == 2 && DT == D && DVT == DV && KB % 16 == 0 && VB % 16 == 0 && GT % 2 == 0),
-                "paired heads: unpadded rows of whole 16-byte lane pieces");
+  static_assert(PK == 1 || (PK == 2 && DT == D && DVT == DV && GT % 2 == 0), "paired heads: unpadded rows");
   constexpr int KBP = PK * KB, VBP = PK * VB;   // bytes per lane of the (paired) row
   constexpr int GH = GT / PK;                   // query heads per KV head of the workgroup
   constexpr int NT = DecodeRows<KBP, VBP>::value;
@@ -475,14 +474,16 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
   const uint32_t kpage_b = (uint32_t)(a.k_stride[0] * KT::bytes), vpage_b = (uint32_t)(a.v_stride[0] * VT::bytes);
   const uint32_t krow_b = (uint32_t)(a.k_stride[1] * KT::bytes), vrow_b = (uint32_t)(a.v_stride[1] * VT::bytes);
   const char* kbase = (const char*)a.k + (int64_t)(PK * kh) * a.k_stride[2] * KT::bytes;
-  uint32_t koff[piece_count(KBP)];
+  uint32_t koff[piece_count(KB)];
 #pragma unroll
-  for (int j = 0; j < piece_count(KBP); ++j) koff[j] = 16 * piece_start(KBP, j) + piece_bytes(KBP, j) * lq;
+  for (int j = 0; j < piece_count(KB); ++j) koff[j] = 16 * piece_start(KB, j) + piece_bytes(KB, j) * lq;
   const char* vbase = (const char*)a.v + (int64_t)(PK * kh) * a.v_stride[2] * VT::bytes;
   const int lv = min(l16, LV - 1);
-  uint32_t voff[piece_count(VBP)];
+  uint32_t voff[piece_count(VB)];
 #pragma unroll
-  for (int j = 0; j < piece_count(VBP); ++j) voff[j] = 16 * piece_start(VBP, j) + piece_bytes(VBP, j) * lv;
+  for (int j = 0; j < piece_count(VB); ++j) voff[j] = 16 * piece_start(VB, j) + piece_bytes(VB, j) * lv;
+  // Paired: the second head's row, one head stride further.
+  const uint32_t khead_b = (uint32_t)(a.k_stride[2] * KT::bytes), vhead_b = (uint32_t)(a.v_stride[2] * VT::bytes);
 
   // Address of the split's first key: the read target of rows with no valid position.
   const char* ksafe = kbase;
@@ -559,9 +560,15 @@ __global__ __launch_bounds__(DEC_THREADS, FA_DEC_MINB) void decode_kernel(const 
       }
     }
 #pragma unroll
-    for (int i = 0; i < NT; ++i) load_pieces_nt<KBP>(krow + ko[i], koff, kw[i]);
+    for (int i = 0; i < NT; ++i)
 #pragma unroll
-    for (int i = 0; i < NT; ++i) load_pieces_nt<VBP>(vrow + vo[i], voff, vw[i]);
+      for (int u = 0; u < PK; ++u)
+        load_pieces_nt<KB>(krow + ko[i] + u * khead_b, koff, *(uint32_t(*)[KB / 4])(kw[i] + u * (KB / 4)));
+#pragma unroll
+    for (int i = 0; i < NT; ++i)
+#pragma unroll
+      for (int u = 0; u < PK; ++u)
+        load_pieces_nt<VB>(vrow + vo[i] + u * vhead_b, voff, *(uint32_t(*)[VB / 4])(vw[i] + u * (VB / 4)));
     if (P) {
       inr += wrap;
       kin += (uint64_t)wrap * krow_b;
@@ -767,20 +774,18 @@ inline int64_t decode_tile_dim(int64_t d) {
   }
 }
 
-// Paired KV heads (PK = 2): 2 x the group's heads per workgroup; 4 only at
-// d128 and for E4M3 d256 (16-bit d256 rows hold twice the registers).
+// Paired KV heads (PK = 2), 2 x the group's heads per workgroup: E4M3 d128
+// (groups of 1-2) and 16-bit 192/128 (groups of 1), the layouts where
+// pairing measured faster (valu_pair in decode_kernel.hip).
 template <typename CT, typename KT, typename VT, bool CAP>
-DecodeKernel pick_pair(int64_t d, int gt) {
-  if (d == 128) {
-    if constexpr (KT::bytes == 2) {
+DecodeKernel pick_pair(int64_t d, int64_t dv, int gt) {
+  if constexpr (KT::bytes == 1) {
+    if (d == 128 && dv == 128) {
       if (gt == 2) return decode_kernel<CT, KT, VT, 128, 128, 2, CAP, 128, 128, false, 2>;
       if (gt == 4) return decode_kernel<CT, KT, VT, 128, 128, 4, CAP, 128, 128, false, 2>;
     }
-  } else if (d == 256) {
-    if (gt == 2) return decode_kernel<CT, KT, VT, 256, 256, 2, CAP, 256, 256, false, 2>;
-    if constexpr (KT::bytes == 1) {
-      if (gt == 4) return decode_kernel<CT, KT, VT, 256, 256, 4, CAP, 256, 256, false, 2>;
-    }
+  } else {
+    if (d == 192 && dv == 128 && gt == 2) return decode_kernel<CT, KT, VT, 192, 128, 2, CAP, 192, 128, false, 2>;
   }
   return nullptr;
 }
@@ -788,8 +793,8 @@ DecodeKernel pick_pair(int64_t d, int gt) {
 template <typename CT, typename KT, typename VT>
 DecodeKernel pick_dims(int64_t d, int64_t dv, int gt, bool cap, bool alibi, int pk) {
   if (pk == 2) {
-    if (alibi || d != dv) return nullptr;
-    return cap ? pick_pair<CT, KT, VT, true>(d, gt) : pick_pair<CT, KT, VT, false>(d, gt);
+    if (alibi) return nullptr;
+    return cap ? pick_pair<CT, KT, VT, true>(d, dv, gt) : pick_pair<CT, KT, VT, false>(d, dv, gt);
   }
   // ALiBi variants exist without softcap only (softcap + ALiBi: generic kernel).
   if (alibi) return cap ? nullptr : pick_dims_cap<CT, KT, VT, false, true>(d, dv, gt);

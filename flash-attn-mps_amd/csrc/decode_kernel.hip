@@ -149,24 +149,24 @@ int decode_group_tile(const fa_attn_args& a) {
 
 // KV heads per VALU-decode workgroup: 2 (decode_kernel PK = 2) when two
 // neighbouring heads' rows sit next to each other in every key row (head
-// stride = the head dim, rows of two heads or more), a lane's share of a
-// head row is whole 16-byte pieces (16-bit d128 / d256, E4M3 d256), no
-// ALiBi, the pair's 2 x group query heads fit one tile (groups of 1-2; 1
-// for 16-bit d256), and there are 8 KV heads or more (16 for 16-bit d256).
-// Each 16-lane row then reads 512-byte runs or longer.  Measured (64
-// requests of U[512, 32768] keys, one query row): 16-bit d128 16/16 6.26 ->
-// 6.66 TB/s, 32/32 6.43 -> 6.88, 16/8 6.03 -> 6.25, 8/8 6.11 -> 6.41, d256
-// 16/16 6.28 -> 6.68; config 4 (E4M3 d256, 16/8) 329 -> 325 us.  With fewer
-// KV heads pairing halves an already small grid: 16-bit d128 8/4 5.88 ->
-// 5.60, E4M3 d256 4/2 5.03 -> 4.52, 16-bit d256 8/8 6.32 -> 6.21.
+// stride = the head dim, rows of two heads or more), with 8 KV heads or
+// more and no ALiBi, for E4M3 d128 (groups of 1-2: 128-byte head rows, read
+// as 256-byte runs) and 16-bit 192/128 (groups of 1).  Measured in one
+// process against the unpaired kernel on the same caches, calls alternated
+// (64 requests of U[512, 32768] keys): E4M3 d128 16/8 5.34 -> 5.69 TB/s, 8/8
+// 5.43 -> 5.95, 16/16 5.63 -> 6.29; config 5 (192/128, 16/16, beside the
+// chunk prefill) 1743 -> 1694 us.  Rows of 256 bytes or more gain nothing
+// and lose a little: 16-bit d128 16/8 6.20 -> 6.04, 16/16 6.38 -> 6.42, d256
+// 16/16 6.36 -> 6.29, config 4 (E4M3 d256) 317 -> 325 us.
 int valu_pair(const fa_attn_args& a) {
-  const int64_t d = a.head_dim_qk, group = a.heads_q / a.heads_k;
-  if (a.alibi || a.head_dim_v != d || (d != 128 && d != 256) || (d * elem_size(a.k_dtype)) % 256) return 1;
-  if (a.heads_k % 2 || a.k_stride[2] != d || a.v_stride[2] != d || a.k_stride[1] < 2 * d || a.v_stride[1] < 2 * d)
+  const int64_t dq = a.head_dim_qk, dv = a.head_dim_v, group = a.heads_q / a.heads_k;
+  const bool e4m3_128 = a.k_dtype == FA_E4M3 && dq == 128 && dv == 128;
+  const bool diffkv = a.k_dtype != FA_E4M3 && dq == 192 && dv == 128;
+  if (a.alibi || !(e4m3_128 || diffkv)) return 1;
+  if (a.heads_k % 2 || a.k_stride[2] != dq || a.v_stride[2] != dv || a.k_stride[1] < 2 * dq || a.v_stride[1] < 2 * dv)
     return 1;
-  const bool wide16 = d == 256 && a.k_dtype != FA_E4M3;
-  if (a.heads_k < (wide16 ? 16 : 8)) return 1;
-  return group <= (wide16 ? 1 : 2) ? 2 : 1;
+  if (a.heads_k < 8) return 1;
+  return group <= (diffkv ? 1 : 2) ? 2 : 1;
 }
 
 bool chunk_aligned(const void* p, const int64_t* st, int nstrides, int esz, int bytes_per_lane) {

@@ -97,20 +97,18 @@ def gqa_pack(p, rows=1):
 def valu_pair(p):
     """KV heads per VALU-decode workgroup (mirrors valu_pair() in
     decode_kernel.hip): 2 when neighbouring heads' rows sit next to each other
-    in every key row, a lane's share of a head row is whole 16-byte pieces
-    (16-bit d128 / d256, E4M3 d256), there is no ALiBi, the group has 1-2
-    query heads per KV head (1 for 16-bit d256), and there are 8 or more KV
-    heads (16 for 16-bit d256); else 1."""
-    k, v, d = p.k, p.v, p.dim_qk
-    if p.alibi is not None or p.dim_v != d or d not in (128, 256) or (d * k.element_size()) % 256:
+    in every key row, there are 8 or more KV heads and no ALiBi, for E4M3
+    d128 caches (groups of 1-2) and 16-bit 192/128 (groups of 1); else 1."""
+    k, v, dq, dv = p.k, p.v, p.dim_qk, p.dim_v
+    fp8 = k.dtype == torch.float8_e4m3fn
+    e4m3_128 = fp8 and dq == 128 and dv == 128
+    diffkv = not fp8 and (dq, dv) == (192, 128)
+    if p.alibi is not None or not (e4m3_128 or diffkv):
         return 1
-    if (p.kv_heads % 2 or k.stride(-2) != d or v.stride(-2) != d or k.stride(-3) < 2 * d
-            or v.stride(-3) < 2 * d):
+    if (p.kv_heads % 2 or k.stride(-2) != dq or v.stride(-2) != dv or k.stride(-3) < 2 * dq
+            or v.stride(-3) < 2 * dv or p.kv_heads < 8):
         return 1
-    wide16 = d == 256 and k.dtype != torch.float8_e4m3fn
-    if p.kv_heads < (16 if wide16 else 8):
-        return 1
-    return 2 if p.heads // p.kv_heads <= (1 if wide16 else 2) else 1
+    return 2 if p.heads // p.kv_heads <= (1 if diffkv else 2) else 1
 
 
 def workgroups_per_token(heads, kv_heads, dim_qk, dim_v, gqa=False, rows=1, pack=1):

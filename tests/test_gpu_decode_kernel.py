@@ -330,17 +330,17 @@ def test_alibi_on_the_decode_kernel(device, heads, kv_heads, d, per_request, spl
     assert_parity(got, lse, ref, ref_lse)
 
 
-def _padded_pool(lengths, left, page, kv_heads, width, dtype, seed, scale_v=1.0):
-    """Paged K/V of a permuted pool with rows of `width` elements per head;
-    slot j of request b is real for left[b] <= j < left[b] + lengths[b] and
-    NaN elsewhere (left padding and tails)."""
+def _padded_pool(lengths, left, page, kv_heads, width_k, width_v, dtype, seed, scale_v=1.0):
+    """Paged K/V of a permuted pool with K / V rows of width_k / width_v
+    elements per head; slot j of request b is real for left[b] <= j <
+    left[b] + lengths[b] and NaN elsewhere (left padding and tails)."""
     g = torch.Generator().manual_seed(seed)
     stored = [n + p for n, p in zip(lengths, left)]
     cols = max(-(-n // page) for n in stored) + 1
     pool = len(lengths) * cols
     table = torch.randperm(pool, generator=g).int().reshape(len(lengths), cols)
-    kc = torch.randn(pool, page, kv_heads, width, generator=g)
-    vc = torch.randn(pool, page, kv_heads, width, generator=g) * scale_v
+    kc = torch.randn(pool, page, kv_heads, width_k, generator=g)
+    vc = torch.randn(pool, page, kv_heads, width_v, generator=g) * scale_v
     for b, n in enumerate(stored):
         for pos in list(range(0, left[b])) + list(range(n, cols * page)):
             kc[table[b, pos // page], pos % page] = float("nan")
@@ -348,54 +348,58 @@ def _padded_pool(lengths, left, page, kv_heads, width, dtype, seed, scale_v=1.0)
     return kc.to(dtype), vc.to(dtype), table, cols, g
 
 
-def _pair_case(device, kv_dtype, d, heads, kv_heads, splits, page, window, width, seed):
+def _pair_case(device, kv_dtype, dq, dv, heads, kv_heads, splits, page, window, stride_mult, seed):
+    """One decode call with sinks, softcap 30, per-(request, KV head) k/v
+    descales, NaN left padding and tails; heads sliced from rows
+    `stride_mult` times their width.  Returns (problem, got, reference)."""
     lengths, left = [1, 31, 300, 0, 2049, 77], [0, 3, 17, 0, 5, 16]
-    scale_v = 0.5 if kv_dtype != torch.float8_e4m3fn else 1.0
-    kc, vc, table, cols, g = _padded_pool(lengths, left, page, kv_heads, width, kv_dtype, seed, scale_v)
-    q_dtype = torch.float16 if kv_dtype == torch.float16 else torch.bfloat16
-    q = torch.randn(len(lengths), heads, d, generator=g).to(q_dtype)
     fp8 = kv_dtype == torch.float8_e4m3fn
+    kc, vc, table, cols, g = _padded_pool(lengths, left, page, kv_heads, stride_mult * dq, stride_mult * dv, kv_dtype,
+                                          seed, 1.0 if fp8 else 0.5)
+    q_dtype = torch.float16 if kv_dtype == torch.float16 else torch.bfloat16
+    q = torch.randn(len(lengths), heads, dq, generator=g).to(q_dtype)
     kd = torch.rand(len(lengths), kv_heads, generator=g) * (0.1 if fp8 else 0.5) + (0.05 if fp8 else 0.75)
     vd = torch.rand(len(lengths), kv_heads, generator=g) * 0.5 + 0.25
     sinks = torch.linspace(-2, 2, heads)
     cu_q, used, pads = (torch.arange(len(lengths) + 1, dtype=torch.int32), torch.tensor(lengths, dtype=torch.int32),
                         torch.tensor(left, dtype=torch.int32))
-    kg, vg = kc.to(device)[..., :d], vc.to(device)[..., :d]
+    kg, vg = kc.to(device)[..., :dq], vc.to(device)[..., :dv]
     kw = dict(cu_seqlens_q=cu_q.to(device), seqused_k=used.to(device), block_table=table.to(device),
               leftpad_k=pads.to(device), window_size=window, softcap=30.0, s_aux=sinks.to(device),
               k_descale=kd.to(device), v_descale=vd.to(device))
     p = problem(q.to(device), kg, vg, max_seqlen_q=1, max_seqlen_k=cols * page, **kw)
     got, lse = decode_attention(q.to(device), kg, vg, max_seqlen_k=cols * page, num_splits=splits, **kw)
-    ref, ref_lse = oracle_attention(q, kc[..., :d], vc[..., :d], cu_q, used_k=used, block_table=table, leftpad=left,
+    ref, ref_lse = oracle_attention(q, kc[..., :dq], vc[..., :dv], cu_q, used_k=used, block_table=table, leftpad=left,
                                     window=window, softcap=30.0, sinks=sinks, k_descale=kd, v_descale=vd)
     return p, (got, lse), (ref, ref_lse)
 
 
-@pytest.mark.parametrize("kv_dtype,d,heads,kv_heads", [
-    (torch.bfloat16, 128, 8, 8), (torch.bfloat16, 128, 16, 8), (torch.float16, 128, 32, 16),
-    (torch.bfloat16, 256, 16, 16), (torch.float8_e4m3fn, 256, 16, 8), (torch.float8_e4m3fn, 256, 8, 8)])
+@pytest.mark.parametrize("kv_dtype,dq,dv,heads,kv_heads", [
+    (torch.float8_e4m3fn, 128, 128, 8, 8), (torch.float8_e4m3fn, 128, 128, 16, 8),
+    (torch.float8_e4m3fn, 128, 128, 32, 16), (torch.bfloat16, 192, 128, 8, 8), (torch.float16, 192, 128, 16, 16)])
 @pytest.mark.parametrize("splits", [0, 3])
 @pytest.mark.parametrize("page,window", [(16, (-1, -1)), (8, (700, 0))])
-def test_paired_kv_heads(device, kv_dtype, d, heads, kv_heads, splits, page, window):
-    """Two neighbouring KV heads per workgroup, their rows read as one:
-    per-(request, KV head) k/v descales that differ between the heads of a
-    pair (a query head scaled with its neighbour's descale fails the bar),
-    sinks, softcap 30, a left window, NaN left padding and tails."""
-    p, (got, lse), (ref, ref_lse) = _pair_case(device, kv_dtype, d, heads, kv_heads, splits, page, window, d,
-                                               880 + d + heads + splits + page)
+def test_paired_kv_heads(device, kv_dtype, dq, dv, heads, kv_heads, splits, page, window):
+    """Two neighbouring KV heads per workgroup, each lane loading its pieces
+    of both heads' rows: per-(request, KV head) k/v descales that differ
+    between the heads of a pair (a query head scaled with its neighbour's
+    descale fails the bar), sinks, softcap 30, a left window, NaN left
+    padding and tails."""
+    p, (got, lse), (ref, ref_lse) = _pair_case(device, kv_dtype, dq, dv, heads, kv_heads, splits, page, window, 1,
+                                               880 + dq + heads + splits + page)
     assert not uses_gqa_kernel(p) and valu_pair(p) == 2
     assert_parity(got, lse, ref, ref_lse)
 
 
-@pytest.mark.parametrize("layout", ["strided", "few"])
-@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
-def test_unpaired_kv_head_layouts(device, layout, kv_dtype):
-    """Heads sliced from wider rows (head stride 2 d) and fewer than 8 KV
-    heads run one KV head per workgroup."""
-    d = 256 if kv_dtype == torch.float8_e4m3fn else 128
-    kv_heads = 8 if layout == "strided" else 4
-    width = 2 * d if layout == "strided" else d
-    p, (got, lse), (ref, ref_lse) = _pair_case(device, kv_dtype, d, 2 * kv_heads, kv_heads, 3, 16, (-1, -1), width,
-                                               890 + len(layout))
+@pytest.mark.parametrize("case", ["strided", "few", "wide_rows", "group"])
+def test_unpaired_kv_head_layouts(device, case):
+    """One KV head per workgroup: heads sliced from wider rows (head stride
+    2 d), fewer than 8 KV heads, 256-byte head rows (16-bit d128), and
+    192/128 groups of 2."""
+    kv_dtype, dq, dv, heads, kv_heads, mult = {
+        "strided": (torch.float8_e4m3fn, 128, 128, 16, 8, 2), "few": (torch.float8_e4m3fn, 128, 128, 8, 4, 1),
+        "wide_rows": (torch.bfloat16, 128, 128, 16, 8, 1), "group": (torch.bfloat16, 192, 128, 16, 8, 1)}[case]
+    p, (got, lse), (ref, ref_lse) = _pair_case(device, kv_dtype, dq, dv, heads, kv_heads, 3, 16, (-1, -1), mult,
+                                               890 + len(case))
     assert not uses_gqa_kernel(p) and valu_pair(p) == 1
     assert_parity(got, lse, ref, ref_lse)
