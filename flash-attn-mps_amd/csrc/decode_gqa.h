@@ -59,12 +59,14 @@ constexpr float GQA_RESCALE = 8.0f;  // log2 headroom before a column's running 
 constexpr bool GQA_NT = FA_GQA_NT;  // non-temporal K/V DMA
 
 // One 16-key slot: K then V, each D / 64 column groups of 16 rows x 128
-// bytes; slots per wave.
+// bytes (16-bit) or 16 raw rows of D bytes (E4M3); slots per wave: E4M3
+// rings hold two stages, except for paired heads, whose rows are twice as
+// long.  D is the row the slots hold (two heads' rows when paired).
 template <int D, bool FP8> constexpr int gqa_slot_bytes() { return FP8 ? 32 * D : 64 * D; }
-template <int D, bool FP8> constexpr int gqa_slots() { return FP8 ? 4 : 2; }
-template <int D, bool FP8> constexpr int gqa_lds_bytes() {
-  const int ring = 4 * gqa_slots<D, FP8>() * gqa_slot_bytes<D, FP8>();
-  const int combine = 4 * GQA_HEADS * (D + 4 + 2) * 4;
+template <int D, bool FP8, int PACK> constexpr int gqa_slots() { return FP8 && PACK == 1 ? 4 : 2; }
+template <int D, bool FP8, int PACK> constexpr int gqa_lds_bytes() {
+  const int ring = 4 * gqa_slots<D, FP8, PACK>() * gqa_slot_bytes<D, FP8>();
+  const int combine = 4 * GQA_HEADS * (D / PACK + 4 + 2) * 4;
   return ring > combine ? ring : combine;
 }
 
@@ -111,27 +113,35 @@ FA_DEV void wait_dma_groups(int n) {
 // rows (16 x D bytes, chunks XOR-swizzled): K operands widen in registers
 // after an 8-byte LDS read, V^T comes through ds_read_b64_tr_b8 and widens in
 // registers the same way, and the descales scale the scores and the output.
-// PACK = 2: two neighbouring KV heads of D / 2 = 64 dims, stored next to each
-// other in every key row, run as one virtual head of D = 128 dims, so each
-// DMA instruction reads rows of 2 x 64 dims (128 bytes of E4M3, 256 of
-// 16-bit) instead of 64-dim rows.  The virtual head's query heads are the
-// two heads' groups; a column's query holds its own head's half of the
-// virtual dims and zeros in the other, so S^T = K Q^T gives each column the
-// scores of its own KV head, and of O^T += V^T P^T each column keeps its own
-// half.  Descales are per column (its KV head).
+// PACK = 2: two neighbouring KV heads of DH = D / 2 dims, stored next to
+// each other in every key row, run in one workgroup whose slots hold both
+// heads' rows as one row of D elements, so each DMA instruction reads runs
+// of 2 x DH elements (64-dim heads: 128 bytes of E4M3 or 256 of 16-bit
+// instead of 64 / 128; 128-dim E4M3 heads: 256 bytes instead of 128).  The
+// workgroup's query heads are the two heads' groups.  S^T = K Q^T runs over
+// the whole row with each column's query entering only the k-steps of its
+// own head's half (zeros in the other's), so each column gets its own KV
+// head's scores; P.V runs over both halves of V into the same DH-dim O^T,
+// with each column's probabilities zeroed for the other head's half, so
+// every column accumulates only its own head's values.  Descales are per
+// column (its KV head).
 template <typename T, int D, bool CAP, typename KT = T, int PACK = 1>
 __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_attn_args a, const int span) {
-  static_assert(D == 64 || D == 128, "head dims 64 and 128");
-  static_assert(PACK == 1 || (PACK == 2 && D == 128), "two 64-dim heads per virtual 128-dim head");
+  static_assert(D == 64 || D == 128 || D == 256, "rows of 64, 128 or 256 elements");
+  static_assert((PACK == 1 && D <= 128) || (PACK == 2 && (D == 128 || (D == 256 && KT::id == FA_E4M3))),
+                "paired heads: 64-dim heads, or 128-dim E4M3 heads");
   constexpr int DH = D / PACK;            // the heads' own dims
   constexpr bool FP8 = KT::id == FA_E4M3;
   constexpr int EB = KT::bytes;           // bytes per K/V element
-  constexpr int KSTEPS = D / 16;          // k-steps of S^T = K Q^T
+  constexpr int KSTEPS = D / 16;          // k-steps of S^T = K Q^T over a slot row
+  constexpr int KPH = KSTEPS / PACK;      // k-steps per head
   constexpr int KG = D / 64;              // 64-dim column groups of a K slot
-  constexpr int DB = D / 32;              // 32-dim blocks of O^T
+  constexpr int DB = D / 32;              // 32-dim blocks of V^T in a slot row
+  constexpr int DBH = DH / 32;            // 32-dim blocks of O^T (one head)
   constexpr int KGROUP = 16 * 128;        // one column group: 16 rows x 128 bytes
-  constexpr int KBYTES = KG * KGROUP, SLOT = gqa_slot_bytes<D, FP8>(), NSLOT = gqa_slots<D, FP8>();
+  constexpr int KBYTES = KG * KGROUP, SLOT = gqa_slot_bytes<D, FP8>(), NSLOT = gqa_slots<D, FP8, PACK>();
   static_assert(NSLOT >= 2, "a stage's two slots");
+  constexpr bool RING2 = NSLOT == 4;      // slots hold two stages (E4M3, unpaired)
 
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
@@ -179,18 +189,15 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   }
   wait_lds();
 
-  // Q^T operands: k-step kk, lane (l32, hh) holds its column's query
-  // (token ctok, head h0 + chead), dims 16 kk + 8 hh .. +8 of the virtual
-  // head, i.e. of part kk / KPH (zeros for the other part, and for columns
-  // past the group or the request's tokens).
-  constexpr int KPH = KSTEPS / PACK;   // k-steps per part
-  u32x4 qop[KSTEPS];
+  // Q^T operands: k-step kk of a head, lane (l32, hh) holds its column's
+  // query (token ctok, head h0 + chead), dims 16 kk + 8 hh .. +8 (zeros for
+  // columns past the group or the request's tokens).
+  u32x4 qop[KPH];
   {
     const uint16_t* qp = (const uint16_t*)a.q + (int64_t)(r.q_begin + (col_ok ? ctok : 0)) * a.q_stride[0] +
                          (int64_t)(h0 + (col_ok ? chead : 0)) * a.q_stride[1] + 8 * hh;
 #pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk)
-      qop[kk] = col_ok && kk / KPH == cpart ? *(const u32x4*)(qp + 16 * (kk % KPH)) : u32x4{0u, 0u, 0u, 0u};
+    for (int kk = 0; kk < KPH; ++kk) qop[kk] = col_ok ? *(const u32x4*)(qp + 16 * kk) : u32x4{0u, 0u, 0u, 0u};
   }
 
   // Descales of this column's KV head (one per workgroup unless packed).
@@ -203,9 +210,9 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   const bool seed = a.sinks && split == 0 && wave == 0;
   float m_run = seed && col_ok ? a.sinks[(int64_t)(h0 + chead) * a.sink_stride] * LOG2E : -INFINITY;
   float l_run = seed && hh == 0 ? 1.0f : 0.0f;
-  f32x16 o[DB];
+  f32x16 o[DBH];
 #pragma unroll
-  for (int db = 0; db < DB; ++db)
+  for (int db = 0; db < DBH; ++db)
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
 
@@ -262,11 +269,11 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   // rows hold key sigma(row) and position q holds chunk q ^ swz8(row), which
   // spreads the 8-byte K operand reads of 16 rows over distinct bank slots.
   constexpr int NCH = D / 16;
-  auto swz8 = [](int row) { return D == 128 ? (row >> 1) & 7 : (row >> 2) & 3; };
+  auto swz8 = [](int row) { return D == 256 ? row & 15 : D == 128 ? (row >> 1) & 7 : (row >> 2) & 3; };
   // Raw E4M3 V rows: 16-byte chunk q at position q ^ vswz8(row), so the 16
   // lanes of one transposed read (8 rows x two 8-byte halves of one chunk)
   // fall on 16 distinct bank pairs.
-  auto vswz8 = [](int row) { return D == 128 ? row & 7 : (row >> 2) & 3; };
+  auto vswz8 = [](int row) { return D >= 128 ? row & 7 : (row >> 2) & 3; };
   int kdoff8[KG], vdoff8[KG];
 #pragma unroll
   for (int ib = 0; ib < KG; ++ib) {
@@ -333,7 +340,7 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   };
   // Slot of group c of stage i: 16-bit K and V of one stage (slots 0, 1);
   // E4M3 raw K and V rows of two stages (slots 2 (i % 2) + c).
-  auto slot_of = [&](int i, int c) -> char* { return ring + (FP8 ? 2 * (i & 1) + c : c) * SLOT; };
+  auto slot_of = [&](int i, int c) -> char* { return ring + (RING2 ? 2 * (i & 1) + c : c) * SLOT; };
   // DMA instructions per stage (two groups): 4 KG each for 16-bit K and V,
   // 2 KG each for E4M3 K and V.
   constexpr int KD = FP8 ? 2 * KG : 4 * KG, VD = KD;
@@ -409,12 +416,18 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
     char* const slot0 = slot_of(i, 0);
     char* const slot1 = slot_of(i, 1);
     // K(i) landed; newer: V(i), and for E4M3 also stage i + 1.
-    if (FP8 && more) wait_dma_older_than<2 * VD + KD>();
+    if (RING2 && more) wait_dma_older_than<2 * VD + KD>();
     else wait_dma_older_than<VD>();
     const char* const kb = l32 < 16 ? slot0 : slot1;
+    // Paired: a column's query enters only the k-steps of its own head's
+    // half of the slot rows (zeros in the other half's).
     f32x16 s;
 #pragma unroll
     for (int e = 0; e < 16; ++e) s[e] = 0.0f;
+    // All ones for the first head's columns; opaque per stage, so that the
+    // masked query copies are formed at their use, not kept for the loop.
+    uint32_t first = cpart == 0 ? ~0u : 0u;
+    asm volatile("" : "+v"(first));
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk) {
       u32x4 av;
@@ -425,10 +438,16 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
       } else {
         av = lds_read16(kb, krd[kk % 4] + (kk / 4) * KGROUP);
       }
-      s = mfma32<T>(av, qop[kk], s);
+      u32x4 qv = qop[kk % KPH];
+      if constexpr (PACK > 1) {
+        const uint32_t keep = kk < KPH ? first : ~first;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) qv[e] &= keep;
+      }
+      s = mfma32<T>(av, qv, s);
     }
     wait_lds();   // K reads of stage i done
-    if constexpr (FP8) {
+    if constexpr (RING2) {
       if (i + 2 < nst) dma_k_stage(i + 2);
     } else {
       if (more) dma_k_stage(i + 1);
@@ -459,7 +478,7 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
     l_run *= f;
     if (__builtin_expect(__any(f != 1.0f), 0)) {
 #pragma unroll
-      for (int db = 0; db < DB; ++db)
+      for (int db = 0; db < DBH; ++db)
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[db][e] *= f;
     }
@@ -471,13 +490,19 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
       psum += p;
     }
     l_run += psum;
-    u32x4 pop[2];
+    // P^T operands per head half: a column's probabilities for its own
+    // head's half of the V rows, zeros for the other half.
+    u32x4 pop[PACK][2];
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) pop[c][q] = pack2<T>(s[8 * c + 2 * q], s[8 * c + 2 * q + 1]);
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t w = pack2<T>(s[8 * c + 2 * q], s[8 * c + 2 * q + 1]);
+#pragma unroll
+        for (int u = 0; u < PACK; ++u) pop[u][c][q] = PACK == 1 || cpart == u ? w : 0u;
+      }
     // V(i) landed; newer: 16-bit K(i + 1); E4M3 stage i + 1 and K(i + 2).
-    if constexpr (FP8) {
+    if constexpr (RING2) {
       if (i + 2 < nst) wait_dma_older_than<2 * KD + VD>();
       else if (more) wait_dma_older_than<KD + VD>();
       else wait_dma_older_than<0>();
@@ -501,10 +526,10 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
           const u32x2 hi = lds_read_tr(vb, vrd + 4 * 128);
           av = u32x4{lo[0], lo[1], hi[0], hi[1]};
         }
-        o[db] = mfma32<T>(av, pop[c], o[db]);
+        o[db % DBH] = mfma32<T>(av, pop[db / DBH][c], o[db % DBH]);
       }
     wait_lds();   // V reads of stage i done
-    if constexpr (FP8) {
+    if constexpr (RING2) {
       if (i + 2 < nst) dma_v_stage(i + 2);
     } else {
       if (more) dma_v_stage(i + 1);
@@ -515,7 +540,7 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
     dma_k_stage(0);
     dma_v_stage(0);
   }
-  if (FP8 && nst > 1) {
+  if (RING2 && nst > 1) {
     dma_k_stage(1);
     dma_v_stage(1);
   }
@@ -527,9 +552,9 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   __syncthreads();
   float* const cm = (float*)smem;                      // [4][32]
   float* const cl = cm + 4 * GQA_HEADS;                // [4][32]
-  // [4][32][D + 4]: the 4-float pad puts the 32 head columns' 16-byte
+  // [4][32][DH + 4]: the 4-float pad puts the 32 head columns' 16-byte
   // stores of one instruction on distinct bank groups.
-  constexpr int CO_ROW = D + 4;
+  constexpr int CO_ROW = DH + 4;
   float* const co = cl + 4 * GQA_HEADS;
   if (hh == 0) {
     cm[wave * GQA_HEADS + l32] = m_run;
@@ -537,7 +562,7 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
   }
   // o[db][4 g + j] = O^T[dim 32 db + 8 g + 4 hh + j][head l32].
 #pragma unroll
-  for (int db = 0; db < DB; ++db)
+  for (int db = 0; db < DBH; ++db)
 #pragma unroll
     for (int g = 0; g < 4; ++g)
       *(float4*)(co + ((int64_t)wave * GQA_HEADS + l32) * CO_ROW + 32 * db + 8 * g + 4 * hh) =
@@ -573,10 +598,9 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
     const int hc = idx / DH, d = idx - hc * DH;   // column hc: head h0 + hc / ntok, token hc % ntok
     const int th = (int)(((uint64_t)hc * ntok_inv) >> 32), tt = hc - th * ntok;
     if (th >= nheads || tt >= r.q_len) continue;
-    const int dv = d + DH * part_of(th);   // the column's own half of the virtual dims
     float O = 0.0f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) O += co[((int64_t)w * GQA_HEADS + hc) * CO_ROW + dv] * cm[w * GQA_HEADS + hc];
+    for (int w = 0; w < 4; ++w) O += co[((int64_t)w * GQA_HEADS + hc) * CO_ROW + d] * cm[w * GQA_HEADS + hc];
     const int h = h0 + th;
     const int64_t tq = r.q_begin + tt;
     if (S == 1) {

@@ -29,7 +29,7 @@ GqaChoice choose(bool cap) {
   GqaChoice c;
   c.kern = cap ? fa_decode_gqa::decode_gqa_kernel<T, D, true, KT, PACK>
                : fa_decode_gqa::decode_gqa_kernel<T, D, false, KT, PACK>;
-  c.lds = fa_decode_gqa::gqa_lds_bytes<D, KT::id == FA_E4M3>();
+  c.lds = fa_decode_gqa::gqa_lds_bytes<D, KT::id == FA_E4M3, PACK>();
   c.pack = PACK;
   return c;
 }
@@ -48,15 +48,20 @@ GqaChoice choose(bool cap) {
 // kernel: E4M3 16/16 3.06 -> 5.64, 16/8 2.91 -> 4.92; 16-bit 16/16 5.94 ->
 // 6.29, 16/8 the same.
 bool packable(const fa_attn_args& a) {
-  const int64_t ntok = a.max_seqlen_q > 1 ? a.max_seqlen_q : 1;
-  return a.head_dim_qk == 64 && a.heads_k % 2 == 0 && a.k_stride[2] == 64 && a.v_stride[2] == 64 &&
-         a.k_stride[1] >= 128 && a.v_stride[1] >= 128 && 2 * (a.heads_q / a.heads_k) * ntok <= fa_decode_gqa::GQA_HEADS &&
-         (a.k_dtype == FA_E4M3 || a.heads_k >= 8);
+  const int64_t ntok = a.max_seqlen_q > 1 ? a.max_seqlen_q : 1, d = a.head_dim_qk;
+  const bool fp8 = a.k_dtype == FA_E4M3;
+  if (!(d == 64 || (d == 128 && fp8))) return false;
+  return a.heads_k % 2 == 0 && a.k_stride[2] == d && a.v_stride[2] == d && a.k_stride[1] >= 2 * d &&
+         a.v_stride[1] >= 2 * d && 2 * (a.heads_q / a.heads_k) * ntok <= fa_decode_gqa::GQA_HEADS &&
+         (fp8 || a.heads_k >= 8);
 }
 
 template <typename T, typename KT>
 GqaChoice choose_dim(const fa_attn_args& a, bool cap) {
   if (a.head_dim_qk == 64) return packable(a) ? choose<T, KT, 128, 2>(cap) : choose<T, KT, 64, 1>(cap);
+  if constexpr (KT::id == FA_E4M3) {
+    if (packable(a)) return choose<T, KT, 256, 2>(cap);
+  }
   return choose<T, KT, 128, 1>(cap);
 }
 
@@ -69,7 +74,8 @@ GqaChoice pick_decode_gqa(const fa_attn_args& a) {
   // VALU kernel is faster below); 2..DECODE_GQA_MAX_ROWS rows: any group
   // (nothing else runs a few rows per request as decode).
   if (a.max_seqlen_q > DECODE_GQA_MAX_ROWS) return none;
-  if (a.max_seqlen_q <= 1 && a.heads_q / a.heads_k < DECODE_GQA_MIN_GROUP && !packable(a)) return none;
+  if (a.max_seqlen_q <= 1 && a.heads_q / a.heads_k < DECODE_GQA_MIN_GROUP && !(a.head_dim_qk == 64 && packable(a)))
+    return none;
   if (a.q_dtype != FA_BF16 && a.q_dtype != FA_F16) return none;
   // P.V runs on probabilities rounded to the query's type: fp32 outputs
   // (held to fp32 accuracy) take the VALU kernel, which keeps P in fp32.

@@ -73,7 +73,8 @@ def uses_gqa_kernel(p, rows=None):
     changes the split plan's workgroup estimate)."""
     page = p.k.shape[1] if p.paged else 0
     rows = p.max_q if rows is None else rows
-    rows_ok = (p.heads // p.kv_heads >= _GQA_MIN_GROUP or gqa_pack(p, 1) == 2) if rows <= 1 else rows <= _GQA_MAX_ROWS
+    small = p.dim_qk == 64 and gqa_pack(p, 1) == 2   # paired 64-dim heads take groups of 1-2 too
+    rows_ok = (p.heads // p.kv_heads >= _GQA_MIN_GROUP or small) if rows <= 1 else rows <= _GQA_MAX_ROWS
     out_dtype = p.out.dtype if p.out is not None else p.output_dtype
     return (rows_ok and p.q.dtype in (torch.float16, torch.bfloat16) and out_dtype == p.q.dtype
             and p.k.dtype == p.v.dtype and p.k.dtype in (p.q.dtype, torch.float8_e4m3fn)
@@ -83,15 +84,17 @@ def uses_gqa_kernel(p, rows=None):
 
 def gqa_pack(p, rows=1):
     """KV heads per matrix-core decode workgroup at `rows` query rows per
-    request (mirrors packable() in decode_gqa.hip): 2 when 64-dim heads sit
-    next to each other in every key row (head stride 64 elements, rows of 128
-    or more), the KV heads pair up, both heads' query columns fit one
-    32-column tile, and the cache is E4M3 or has 8 or more KV heads; else 1."""
-    k, v = p.k, p.v
+    request (mirrors packable() in decode_gqa.hip): 2 when 64-dim heads (or
+    128-dim E4M3 heads) sit next to each other in every key row (head stride
+    = the head dim, rows of two heads or more), the KV heads pair up, both
+    heads' query columns fit one 32-column tile, and the cache is E4M3 or has
+    8 or more KV heads; else 1."""
+    k, v, d = p.k, p.v, p.dim_qk
+    fp8 = k.dtype == torch.float8_e4m3fn
     fits = 2 * (p.heads // p.kv_heads) * max(rows, 1) <= 32
-    return 2 if (p.dim_qk == 64 and p.kv_heads % 2 == 0 and k.stride(-2) == 64 and v.stride(-2) == 64
-                 and k.stride(-3) >= 128 and v.stride(-3) >= 128 and fits
-                 and (k.dtype == torch.float8_e4m3fn or p.kv_heads >= 8)) else 1
+    return 2 if ((d == 64 or (d == 128 and fp8)) and p.dim_v == d and p.kv_heads % 2 == 0 and k.stride(-2) == d
+                 and v.stride(-2) == d and k.stride(-3) >= 2 * d and v.stride(-3) >= 2 * d and fits
+                 and (fp8 or p.kv_heads >= 8)) else 1
 
 
 def valu_pair(p):

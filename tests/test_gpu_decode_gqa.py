@@ -67,7 +67,7 @@ def test_groups_dims_and_splits(device, heads, kv_heads, d, dtype, splits):
     kw = dict(cu_seqlens_q=cu_q, seqused_k=used, block_table=table, s_aux=sinks)
     p = problem(q, kc, vc, max_seqlen_q=1, max_seqlen_k=cols * page, **kw)
     # Groups of 1 and 2 take this kernel only with paired 64-dim heads.
-    assert uses_gqa_kernel(p) == (heads // kv_heads >= 3 or gqa_pack(p) == 2)
+    assert uses_gqa_kernel(p) == (heads // kv_heads >= 3 or (d == 64 and gqa_pack(p) == 2))
     assert gqa_pack(p) == (2 if d == 64 and (heads, kv_heads) in ((32, 8), (40, 8), (16, 16), (16, 8)) else 1)
     got, lse = decode_attention(q, kc, vc, max_seqlen_k=cols * page, num_splits=splits, out=buffer[:, :heads], **kw)
     ref, ref_lse = oracle_attention(q, kc, vc, cu_q, used_k=used, block_table=table, sinks=sinks)
@@ -150,8 +150,10 @@ def test_e4m3_caches_with_descales(device, heads, kv_heads, d, q_dtype, splits):
     kw = dict(cu_seqlens_q=cu_q.to(device), seqused_k=used.to(device), block_table=table.to(device),
               s_aux=sinks.to(device), softcap=30.0, k_descale=kd.to(device), v_descale=vd.to(device))
     p = problem(q.to(device), kc.to(device), vc.to(device), max_seqlen_q=1, max_seqlen_k=cols * page, **kw)
-    assert uses_gqa_kernel(p) == (heads // kv_heads >= 3 or gqa_pack(p) == 2)
-    assert gqa_pack(p) == (2 if d == 64 and (heads, kv_heads) in ((16, 2), (24, 8), (16, 16), (8, 4)) else 1)
+    # Groups of 1-2 take this kernel with paired 64-dim heads only (128-dim
+    # E4M3 pairs of such groups run on the VALU decode).
+    assert uses_gqa_kernel(p) == (heads // kv_heads >= 3 or (d == 64 and gqa_pack(p) == 2))
+    assert gqa_pack(p) == (2 if (heads, kv_heads) in ((16, 2), (24, 8), (16, 16), (8, 4)) else 1)
     got, lse = decode_attention(q.to(device), kc.to(device), vc.to(device), max_seqlen_k=cols * page,
                                 num_splits=splits, **kw)
     ref, ref_lse = oracle_attention(q, kc, vc, cu_q, used_k=used, block_table=table, sinks=sinks, softcap=30.0,
@@ -250,14 +252,14 @@ def test_rows_e4m3_cache(device, q_lens, q_dtype, heads, d):
 
 
 @pytest.mark.parametrize("layout", ["pairs", "strided", "odd"])
-@pytest.mark.parametrize("kind", [torch.bfloat16, torch.float8_e4m3fn])
-def test_head_pairs_and_unpaired_layouts(device, layout, kind):
-    """64-dim heads: neighbouring KV heads run in pairs; heads of a cache
-    sliced from wider rows (head stride 128) and an odd KV head count run one
-    KV head per workgroup.  Per-(request, KV head) descales differ between the
-    two heads of a pair, so a column scaled with its neighbour's descale
-    fails the bar."""
-    lengths, page, d = [1, 31, 33, 0, 300, 2049, 77], 16, 64
+@pytest.mark.parametrize("kind,d", [(torch.bfloat16, 64), (torch.float8_e4m3fn, 64), (torch.float8_e4m3fn, 128)])
+def test_head_pairs_and_unpaired_layouts(device, layout, kind, d):
+    """64-dim heads and 128-dim E4M3 heads: neighbouring KV heads run in
+    pairs; heads of a cache sliced from wider rows (head stride 2 d) and an
+    odd KV head count run one KV head per workgroup.  Per-(request, KV head)
+    descales differ between the two heads of a pair, so a column scaled with
+    its neighbour's descale fails the bar."""
+    lengths, page = [1, 31, 33, 0, 300, 2049, 77], 16
     kv_heads = 3 if layout == "odd" else 8
     heads = 6 * kv_heads
     g = torch.Generator().manual_seed(770 + len(layout))
