@@ -157,9 +157,13 @@ int decode_group_tile(const fa_attn_args& a) {
 // 5.43 -> 5.95, 16/16 5.63 -> 6.29; config 5 (192/128, 16/16, beside the
 // chunk prefill) 1743 -> 1694 us.  Rows of 256 bytes or more gain nothing
 // and lose a little: 16-bit d128 16/8 6.20 -> 6.04, 16/16 6.38 -> 6.42, d256
-// 16/16 6.36 -> 6.29, config 4 (E4M3 d256) 317 -> 325 us.
+// 16/16 6.36 -> 6.29, config 4 (E4M3 d256) 317 -> 325 us.  One split per
+// request (the fixed-order route) keeps one head per workgroup: there the
+// grid is one workgroup per request and head, and halving it made config
+// 5's fixed-order call slower (1738 -> 1784 us).
 int valu_pair(const fa_attn_args& a) {
   const int64_t dq = a.head_dim_qk, dv = a.head_dim_v, group = a.heads_q / a.heads_k;
+  if (a.num_splits == 1) return 1;
   const bool e4m3_128 = a.k_dtype == FA_E4M3 && dq == 128 && dv == 128;
   const bool diffkv = a.k_dtype != FA_E4M3 && dq == 192 && dv == 128;
   if (a.alibi || !(e4m3_128 || diffkv)) return 1;

@@ -101,8 +101,11 @@ def valu_pair(p):
     """KV heads per VALU-decode workgroup (mirrors valu_pair() in
     decode_kernel.hip): 2 when neighbouring heads' rows sit next to each other
     in every key row, there are 8 or more KV heads and no ALiBi, for E4M3
-    d128 caches (groups of 1-2) and 16-bit 192/128 (groups of 1); else 1."""
+    d128 caches (groups of 1-2) and 16-bit 192/128 (groups of 1), unless the
+    call runs one split per request; else 1."""
     k, v, dq, dv = p.k, p.v, p.dim_qk, p.dim_v
+    if p.splits == 1:
+        return 1
     fp8 = k.dtype == torch.float8_e4m3fn
     e4m3_128 = fp8 and dq == 128 and dv == 128
     diffkv = not fp8 and (dq, dv) == (192, 128)
