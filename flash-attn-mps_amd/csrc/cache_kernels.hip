@@ -105,8 +105,10 @@ __global__ __launch_bounds__(256) void store_kernel(const StoreParams p) {
 // the kernel, so no element does any division), the slot is read once per
 // token and split into page and row with a shift (power-of-two pages) or one
 // 32-bit division.  FP8: x / scale[h] (correctly rounded, by div_by_scale
-// with the scale's reciprocal) then the integer E4M3 encoder, VEC codes
-// stored as one 8- or 4-byte word.
+// with the scale's reciprocal) then the hardware E4M3 conversion (the
+// integer encoder's byte for every non-NaN input: checked on all 2^32 fp32
+// patterns; 2.4x fewer VALU instructions per element, the store 2-3%
+// faster), VEC codes stored as one 8- or 4-byte word.
 // Streaming (non-temporal) accesses: the token rows are read once and the
 // cache rows written once, so neither is kept in the caches (1.5% faster
 // than ordinary loads and stores on a 590K-token FP8 store).
@@ -176,6 +178,8 @@ __global__ __launch_bounds__(256) void store_rows_kernel(const StoreParams p, co
         } else {
           const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
           uint32_t packed[VEC / 4];
+          float qs[VEC];
+          bool anynan = false;
 #pragma unroll
           for (int j = 0; j < VEC; ++j) {
             float f;
@@ -187,8 +191,27 @@ __global__ __launch_bounds__(256) void store_rows_kernel(const StoreParams p, co
             float q;
             if constexpr (decltype(fast)::value) q = div_by_scale(f, scale[i], recip[i]);
             else q = f / scale[i];
-            const uint32_t code = e4m3_code(q) & 0xffu;
-            packed[j / 4] = (j & 3) == 0 ? code : packed[j / 4] | (code << (8 * (j & 3)));
+            qs[j] = q;
+            anynan |= q != q;
+          }
+          // Hardware conversion of |q| clamped to 448 (v_med3, then
+          // v_cvt_pk_fp8_f32, round to nearest even): the byte e4m3_code
+          // gives for every non-NaN fp32 value; NaN lanes take e4m3_code.
+#pragma unroll
+          for (int j = 0; j < VEC; j += 4) {
+            int v = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_fmed3f(qs[j], -448.0f, 448.0f),
+                                                    __builtin_amdgcn_fmed3f(qs[j + 1], -448.0f, 448.0f), 0, false);
+            v = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_fmed3f(qs[j + 2], -448.0f, 448.0f),
+                                                __builtin_amdgcn_fmed3f(qs[j + 3], -448.0f, 448.0f), v, true);
+            packed[j / 4] = (uint32_t)v;
+          }
+          if (__builtin_expect(anynan, 0)) {
+#pragma unroll
+            for (int j = 0; j < VEC; ++j)
+              if (qs[j] != qs[j]) {
+                const uint32_t code = e4m3_code(qs[j]) & 0xffu;
+                packed[j / 4] = (packed[j / 4] & ~(0xffu << (8 * (j & 3)))) | (code << (8 * (j & 3)));
+              }
           }
           uint8_t* out = (uint8_t*)d.cache + crow + dst[i];
           if constexpr (VEC == 8) store8_nt(out, make_uint2(packed[0], packed[1]));

@@ -78,6 +78,34 @@ def test_fp8_store_rounding_saturation_and_scales(device):
     assert torch.equal(expected, values.clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_fp8_row_store_codes_midpoints_and_every_bf16_pattern(device, dtype):
+    """The row kernel (contiguous [T, 8, 256] rows), whose E4M3 bytes come
+    from the hardware conversion: every code and every midpoint between
+    neighbours (ties to even) with their negatives, +-1000, +-inf and NaN,
+    under power-of-two per-head scales (exact quotients), then all 65536
+    bf16 bit patterns under scales 1, 2^-4 and 0.0173; bytes against the C
+    codec."""
+    heads, dim, page = 8, 256, 16
+    codes = torch.arange(127, dtype=torch.uint8).view(torch.float8_e4m3fn).float()
+    mids = (codes[:-1] + codes[1:]) / 2
+    table = torch.cat((codes, mids, -codes, -mids, torch.tensor([1000.0, -1000.0, INF, -INF, float("nan")])))
+    row = table.repeat(-(-heads * dim // len(table)))[: heads * dim].reshape(heads, dim)
+    scale = torch.tensor([0.5, 2.0, 1.0, 0.25, 4.0, 0.125, 8.0, 1.0])
+    rows = [row * scale[:, None]]
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).float()
+    x = torch.cat((torch.stack(rows), bits.reshape(-1, heads, dim))).to(dtype)
+    tokens = x.shape[0]
+    for s in (scale, torch.full((heads,), 2.0 ** -4), torch.full((heads,), 0.0173)):
+        pages = -(-tokens // page)
+        slots = torch.arange(tokens)
+        cache = torch.zeros(pages, page, heads, dim, dtype=torch.float8_e4m3fn, device=device)
+        store_kvcache(x.to(device), x.to(device), cache, cache, slots.to(device), k_scale=s.to(device),
+                      v_scale=s.to(device))
+        expected = ocache.store_kvcache(x, torch.zeros(pages, page, heads, dim, dtype=torch.float8_e4m3fn), slots, s)
+        assert torch.equal(_bytes(cache), _bytes(expected)), f"scale {s.tolist()}"
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("contiguous", [True, False])
 def test_fp8_store_of_random_rows_matches_the_c_codec(device, dtype, contiguous):
