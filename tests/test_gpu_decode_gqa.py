@@ -203,14 +203,16 @@ def test_rows_per_request(device, q_lens, heads, kv_heads, causal, splits):
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("splits", [0, 2])
 @pytest.mark.parametrize("heads,kv_heads", [(16, 4), (32, 8)])
-def test_rows_windows_softcap_leftpad(device, window, d, splits, heads, kv_heads):
+@pytest.mark.parametrize("kv_dtype", [torch.float16, torch.float8_e4m3fn])
+def test_rows_windows_softcap_leftpad(device, window, d, splits, heads, kv_heads, kv_dtype):
     """Multi-row decode with left/right windows (each row's own window),
-    softcap 30, descales of a 16-bit cache and NaN left padding (32 / 8
-    heads of 64 dims at 4 rows: paired KV heads filling one tile)."""
+    softcap 30, descales and NaN left padding, over 16-bit and E4M3 caches
+    (paired KV heads filling one tile: 32 / 8 heads of 64 dims at 4 rows,
+    and every E4M3 case here)."""
     q_lens, left = [3, 4, 1, 4, 2], [0, 5, 17, 3, 16]
     lengths = [3, 40, 777, 1500, 33]
     stored = [n + p for n, p in zip(lengths, left)]
-    kc, vc, table, cols = _pool(stored, 48, kv_heads, d, torch.float16, device, 750 + d + splits, left)
+    kc, vc, table, cols = _pool(stored, 48, kv_heads, d, kv_dtype, device, 750 + d + splits, left)
     g = torch.Generator().manual_seed(751 + d)
     q = torch.randn(sum(q_lens), heads, d, generator=g).to(torch.float16).to(device)
     kd = torch.rand(len(q_lens), kv_heads, generator=g) * 0.5 + 0.75
