@@ -19,7 +19,8 @@
 //   workgroups share a CU); each refill is issued as soon as the current
 //   stage has read its half (K after S^T, V after P.V), so a wave's loads
 //   overlap its own arithmetic.  E4M3 slots hold raw rows only, half the
-//   size, so they hold two stages.  Rings of 3-5 16-bit slots per wave (one
+//   size, so they hold two stages (paired 128-dim E4M3 heads, whose slot
+//   rows are two heads long, one).  Rings of 3-5 16-bit slots per wave (one
 //   workgroup per CU) measured 4-25% slower at d128 and up to 36% at d64:
 //   fewer waves per CU cost more than the prefetch gains.
 // * LDS layouts per 16-key slot: K as in the prefill kernel
@@ -37,8 +38,9 @@
 //   head dims 64 and 128 (Dqk = Dv), outputs of the query's type, packed or
 //   paged K/V (page size a multiple of 16), sinks, softcap, windows, 1-16
 //   query rows per request; the host keeps other combinations on the VALU
-//   kernel.  Neighbouring 64-dim KV heads can run in pairs as one 128-dim
-//   virtual head (PACK below), so that the DMA reads 128-dim row runs.
+//   kernel.  Neighbouring KV heads (64-dim, or 128-dim E4M3) can run in
+//   pairs whose rows the slots hold as one row (PACK below), so that each
+//   DMA instruction reads runs of two head rows.
 #ifndef FA_DECODE_GQA_H
 #define FA_DECODE_GQA_H
 
@@ -338,8 +340,9 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
                         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)gi);
     return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)gu, (short)0, bytes, 0x00020000);
   };
-  // Slot of group c of stage i: 16-bit K and V of one stage (slots 0, 1);
-  // E4M3 raw K and V rows of two stages (slots 2 (i % 2) + c).
+  // Slot of group c of stage i: 16-bit K and V, or paired E4M3 rows, of one
+  // stage (slots 0, 1); unpaired E4M3 raw K and V rows of two stages (slots
+  // 2 (i % 2) + c).
   auto slot_of = [&](int i, int c) -> char* { return ring + (RING2 ? 2 * (i & 1) + c : c) * SLOT; };
   // DMA instructions per stage (two groups): 4 KG each for 16-bit K and V,
   // 2 KG each for E4M3 K and V.
@@ -408,14 +411,14 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
 
   // Stage i.  K(i) landed (V(i) may still be in flight) -> S^T -> the next
   // K DMA into the K halves just read -> softmax -> V(i) landed -> P.V ->
-  // the next V DMA into the V halves just read.  16-bit slots hold one
-  // stage, so the refills are stage i + 1's; E4M3 slots hold two, so they
-  // are stage i + 2's while stage i + 1 is already in flight.  Each load
+  // the next V DMA into the V halves just read.  One-stage rings (16-bit,
+  // paired E4M3) refill with stage i + 1; two-stage rings (unpaired E4M3)
+  // with stage i + 2 while stage i + 1 is already in flight.  Each load
   // overlaps the wave's own arithmetic instead of following it.
   auto stage = [&](int i, bool more) {
     char* const slot0 = slot_of(i, 0);
     char* const slot1 = slot_of(i, 1);
-    // K(i) landed; newer: V(i), and for E4M3 also stage i + 1.
+    // K(i) landed; newer: V(i), and with two-stage rings also stage i + 1.
     if (RING2 && more) wait_dma_older_than<2 * VD + KD>();
     else wait_dma_older_than<VD>();
     const char* const kb = l32 < 16 ? slot0 : slot1;
@@ -501,7 +504,8 @@ __global__ __launch_bounds__(GQA_THREADS, 1) void decode_gqa_kernel(const fa_att
 #pragma unroll
         for (int u = 0; u < PACK; ++u) pop[u][c][q] = PACK == 1 || cpart == u ? w : 0u;
       }
-    // V(i) landed; newer: 16-bit K(i + 1); E4M3 stage i + 1 and K(i + 2).
+    // V(i) landed; newer: K(i + 1) with one-stage rings; stage i + 1 and
+    // K(i + 2) with two-stage rings.
     if constexpr (RING2) {
       if (i + 2 < nst) wait_dma_older_than<2 * KD + VD>();
       else if (more) wait_dma_older_than<KD + VD>();

@@ -1,7 +1,8 @@
 // Variants of the matrix-core GQA decode kernel (decode_gqa.h) and their
 // selection: 16-bit queries over K/V of the same type or E4M3, Dqk = Dv in
-// {64, 128}, with and without softcap; 64-dim heads stored next to each
-// other run two KV heads per workgroup (PACK = 2).
+// {64, 128}, with and without softcap; neighbouring 64-dim heads, and
+// 128-dim E4M3 heads, stored next to each other run two KV heads per
+// workgroup (PACK = 2).
 #include "decode_gqa.h"
 
 namespace fa_decode {
@@ -34,19 +35,22 @@ GqaChoice choose(bool cap) {
   return c;
 }
 
-// Two 64-dim KV heads per workgroup when every key row holds them next to
-// each other (head stride 64 elements, rows of at least 128), both heads'
-// query columns fit one 32-column tile (a second tile would read both heads'
-// rows again: 48/2 heads at 16 bits 4.82 -> 2.64 TB/s), and the cache is
-// E4M3 or has 8 KV heads or more.  Measured on 64 requests of U[512, 32768]
-// keys, one query row each: E4M3 32/8 2.95 -> 4.92 TB/s, 12/4 2.76 -> 4.01,
-// 6/2 2.40 -> 3.32 (64-byte rows are the worst case of the paged gather);
-// 16-bit 32/8 5.33 -> 5.65, 64/8 5.47 -> 5.81, but 12/4 5.58 -> 5.33 and 14/2
-// 5.01 -> 4.74 (with few KV heads a key row is 256-512 bytes that the heads'
-// workgroups already read side by side, and pairing halves the workgroups).
-// Paired heads also take groups of 1 and 2, which otherwise run on the VALU
-// kernel: E4M3 16/16 3.06 -> 5.64, 16/8 2.91 -> 4.92; 16-bit 16/16 5.94 ->
-// 6.29, 16/8 the same.
+// Two KV heads per workgroup (64-dim heads, or 128-dim E4M3 heads) when
+// every key row holds them next to each other (head stride = the head dim,
+// rows of two heads or more), both heads' query columns fit one 32-column
+// tile (a second tile would read both heads' rows again: 48/2 heads at 16
+// bits 4.82 -> 2.64 TB/s), and the cache is E4M3 or has 8 KV heads or more.
+// Measured in one process against the unpaired kernel on the same caches,
+// calls alternated (64 requests of U[512, 32768] keys, one query row): E4M3
+// d64 32/8 2.94 -> 5.18 TB/s, 16/8 2.97 -> 5.25 (64-byte rows are the worst
+// case of the paged gather); 16-bit d64 32/8 5.32 -> 5.68, 16/16 5.74 ->
+// 6.07; E4M3 d128 32/8 5.39 -> 5.70, 64/8 5.06 -> 5.37, 12/4 4.91 -> 4.88.
+// With few KV heads 16-bit pairing loses (separate processes: 12/4 5.58 ->
+// 5.33, 14/2 5.01 -> 4.74): a key row is then 256-512 bytes that the heads'
+// workgroups already read side by side, and pairing halves the workgroups.
+// Paired 64-dim heads also take groups of 1 and 2, which otherwise run on
+// the VALU kernel (separate processes: E4M3 16/16 3.06 -> 5.64, 16/8 2.91
+// -> 4.92; 16-bit 16/16 5.94 -> 6.29, 16/8 the same).
 bool packable(const fa_attn_args& a) {
   const int64_t ntok = a.max_seqlen_q > 1 ? a.max_seqlen_q : 1, d = a.head_dim_qk;
   const bool fp8 = a.k_dtype == FA_E4M3;

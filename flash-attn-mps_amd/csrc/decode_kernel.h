@@ -822,7 +822,7 @@ constexpr int DECODE_GQA_MAX_ROWS = 16;
 struct GqaChoice {
   DecodeKernel kern;
   size_t lds;
-  int pack;   // KV heads per workgroup (2: two 64-dim heads as one 128-dim virtual head)
+  int pack;   // KV heads per workgroup (2: neighbouring 64-dim or 128-dim E4M3 heads, PACK = 2)
 };
 GqaChoice pick_decode_gqa(const fa_attn_args& a);
 
