@@ -243,6 +243,7 @@ struct PrefillShape {
   int log2_page;   // paged K/V: page of position p = p >> log2_page, slot p & (2^log2_page - 1)
   int compact;     // 1: workgroups map onto the compact work list
   int hp;          // query heads per workgroup (1 or 2, dividing the GQA group): W / hp waves per head
+  int vparts;      // V column parts (1, or 2: each work item runs as two workgroups, one per DVT-column half)
 };
 
 // One workgroup's share of the compact work list.  With g = gcd(Hkv, 8),
@@ -353,8 +354,9 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // MFMAs (raw dot-product units); with softcap it follows the softcap.
   constexpr bool ALIBI_FOLD = ALIBI && !CAP, ALIBI_LATE = ALIBI && CAP;
   constexpr int KEB = KT::bytes;               // bytes per K/V element
-  static_assert(!FP8 || (DQT == DQ && DVT == DV && DQ == DV && (DQ == 64 || DQ == 128 || DQ == 256)),
-                "FP8 K/V tiles: 64/128/256-dim heads");
+  static_assert(!FP8 || (DQT == DQ && DVT == DV && ((DQ == DV && (DQ == 64 || DQ == 128 || DQ == 256)) ||
+                                                      (DQ == 256 && DV == 128 && !FQ))),
+                "FP8 K/V tiles: 64/128/256-dim heads (256-dim: also as 256/128 V halves)");
   static_assert(!FQ || FP8, "E4M3 queries: E4M3 K/V");
   constexpr int BM = 32 * NB * W;              // query rows per workgroup
   constexpr int KST = DQ / 16;                 // k-steps of the QK^T MFMA
@@ -392,8 +394,17 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // past a request's end.
   // With hp = 2 a workgroup holds BM / 2 rows of two query heads of one KV
   // head (waves 0 .. W/2-1 the first head), sharing every K/V tile.
+  // V column parts (shp.vparts = 2): the head's V and output columns are two
+  // halves of DVT, each a workgroup of its own that recomputes S (a 256-dim
+  // head then holds half of O^T, within the 256 registers of two waves per
+  // SIMD).  Blocks 16j..16j+7 take half 0 and 16j+8..16j+15 half 1 of work
+  // slots 8j..8j+7: both halves of an item run on one XCD, side by side,
+  // and their K reads meet in its L2.
+  const bool two_parts = shp.vparts == 2;
+  const int vpart = two_parts ? (int)(blockIdx.x >> 3) & 1 : 0;
+  const int bid = two_parts ? (int)((blockIdx.x >> 4) << 3 | (blockIdx.x & 7)) : (int)blockIdx.x;
   const int G = (int)(a.heads_q / a.heads_k) / shp.hp;
-  const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
+  const int xcd = bid % 8, slot = bid / 8;
   WorkItem wi;
   if (shp.compact) {
     bool found;
@@ -630,7 +641,10 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   const int kdoff = KEB * (int)(sigma(drow) * a.k_stride[1]) + (((lane & 7) ^ ((drow >> 1) & 7)) * 16);
   const int vdoff = 2 * (int)((lane >> 2) * a.v_stride[1]) + (lane & 3) * 16;
   const char* const khead = (const char*)a.k + KEB * (int64_t)kh * a.k_stride[2];
-  const char* const vhead = (const char*)a.v + KEB * (int64_t)kh * a.v_stride[2];
+  // (readfirstlane: the part's column offset stays a scalar, as the
+  // descriptors built from vhead must)
+  const char* const vhead = (const char*)a.v + KEB * (int64_t)kh * a.v_stride[2] +
+                            __builtin_amdgcn_readfirstlane(vpart * DVT * KEB);
   const uint32_t krow_b = (uint32_t)(KEB * a.k_stride[1]), vrow_b = (uint32_t)(KEB * a.v_stride[1]);
   const uint32_t kpage_b = (uint32_t)(KEB * a.k_stride[0]), vpage_b = (uint32_t)(KEB * a.v_stride[0]);
   const int32_t* const trow = paged ? a.block_table + b * a.bt_stride[0] : nullptr;
@@ -1261,7 +1275,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     if (row < r.q_len) {
       const float inv = lt > 0.0f ? vdsc / lt : 0.0f;
       const int64_t tq = (int64_t)r.q_begin + row;
-      uint16_t* op = (uint16_t*)a.out + tq * a.out_stride[0] + (int64_t)h * a.out_stride[1] + 4 * hh;
+      uint16_t* op = (uint16_t*)a.out + tq * a.out_stride[0] + (int64_t)h * a.out_stride[1] + vpart * DVT + 4 * hh;
 #pragma unroll
       for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -1272,7 +1286,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
           w.y = pack2<T>(o[nb][db][4 * g + 2] * inv, o[nb][db][4 * g + 3] * inv);
           *(uint2*)(op + 32 * db + 8 * g) = w;
         }
-      if (hh == 0)
+      if (hh == 0 && vpart == 0)
         a.lse[(int64_t)h * a.lse_stride[0] + tq * a.lse_stride[1]] = lt > 0.0f ? m_run[nb] * LN2 + logf(lt) : -INFINITY;
     }
   }
@@ -1297,7 +1311,11 @@ template <> struct PrefillTile<128, 128> {
 // second wave per SIMD, at every grid size (one workgroup per CU ran 7-48%
 // slower even on 128-workgroup launches).
 template <> struct PrefillTile<192, 128> { static constexpr int W = 4, NB = 1, MINB = 2, MINB_WIN = 2; };
+// 256/256 (E4M3 K/V, E4M3 queries): one wave per SIMD (128 KiB of LDS).
 template <> struct PrefillTile<256, 256> { static constexpr int W = 4, NB = 1, MINB = 1, MINB_WIN = 1; };
+// 256-dim 16-bit heads run as two 256/128 halves of V (vparts): eight
+// waves in 96 KiB of LDS, two per SIMD.
+template <> struct PrefillTile<256, 128> { static constexpr int W = 8, NB = 1, MINB = 1, MINB_WIN = 1; };
 
 template <int DQ, int DV>
 constexpr size_t lds_bytes() {
@@ -1310,6 +1328,7 @@ struct PrefillChoice {
   PrefillKernel kern;
   int bm, threads;
   size_t lds;
+  int vparts;   // workgroups per work item, one per DV-column part of the head (PrefillShape::vparts)
 };
 
 // score: 0 plain, 1 softcap, 2 ALiBi, 3 softcap then ALiBi; mk: vLLM
@@ -1334,7 +1353,8 @@ PrefillChoice pick_tile(int score, bool win, int mk) {
   } else if (score >= 2) {   // ALiBi (3: after a softcap)
     // With windows, softcap or E4M3 K/V: unpadded 64 / 128 / 256-dim heads
     // (E4M3 K/V: 64 / 128).
-    constexpr bool MORE = DQT == DQ && DVT == DV && DQ == DV && (DQ == 64 || DQ == 128 || DQ == 256) &&
+    constexpr bool MORE = DQT == DQ && DVT == DV &&
+                          ((DQ == DV && (DQ == 64 || DQ == 128 || DQ == 256)) || (DQ == 256 && DV == 128)) &&
                           !(KT::id == FA_E4M3 && DQ == 256);
     const bool capa = score == 3;
     if (!capa && !win && KT::id != FA_E4M3) {
@@ -1360,6 +1380,7 @@ PrefillChoice pick_tile(int score, bool win, int mk) {
   c.bm = 32 * S::NB * S::W;
   c.threads = 64 * S::W;
   c.lds = lds_bytes<DQ, DV>() + (KT::id == FA_E4M3 ? 64 * (size_t)(DQ + DV) : 0);   // + FP8 staging tile
+  c.vparts = 1;
   return c;
 }
 
@@ -1392,6 +1413,25 @@ PrefillChoice pick_dims_small(int64_t dq, int64_t dv, bool causal, int score, bo
   }
 }
 
+// 256-dim heads: two V-column halves per work item (PrefillShape::vparts),
+// each an eight-wave 256/128 tile at two waves per SIMD (the one-pass
+// 256/256 tile holds four waves, one per SIMD, and spills more).  The halves
+// recompute S, with every tanh of a softcap: 16-bit softcaps, and E4M3
+// softcaps with a window, keep the one-pass tile.  Measured on config 2's
+// lengths at 16/8 heads (TFLOP/s, one-pass -> halves): bf16 causal 456 ->
+// 597, non-causal 629 -> 716, ALiBi 404 -> 519, left window 1023 260 -> 292,
+// vLLM mm_prefix +36%, rswa +8%, softcap 50 560 -> 519, softcap + window
+// 346 -> 257; E4M3 K/V causal 299 -> 564, non-causal 342 -> 657, softcap
+// 339 -> 444, window 221 -> 255, softcap + window 285 -> 228.
+template <typename T, typename KT>
+PrefillChoice pick_256(bool causal, int score, bool win, int mk) {
+  const bool cap = score == 1 || score == 3;
+  if (cap && (KT::id != FA_E4M3 || win)) return pick<T, KT, 256, 256>(causal, score, win, mk);
+  PrefillChoice c = pick<T, KT, 256, 128>(causal, score, win, mk);
+  c.vparts = 2;
+  return c;
+}
+
 template <typename T>
 PrefillChoice pick_dims_large(int64_t dq, int64_t dv, bool causal, int score, bool win, bool fp8, int mk) {
   if (fp8) {
@@ -1399,12 +1439,12 @@ PrefillChoice pick_dims_large(int64_t dq, int64_t dv, bool causal, int score, bo
     switch (dq) {
       case 64: return pick<T, E4M3T, 64, 64>(causal, score, win, mk);
       case 128: return pick<T, E4M3T, 128, 128>(causal, score, win, mk);
-      case 256: return pick<T, E4M3T, 256, 256>(causal, score, win, mk);
+      case 256: return pick_256<T, E4M3T>(causal, score, win, mk);
       default: return PrefillChoice{nullptr, 0, 0, 0};
     }
   }
   if (dq == 192 && dv == 128) return pick<T, T, 192, 128>(causal, score, win, mk);
-  if (dq == 256 && dv == 256) return pick<T, T, 256, 256>(causal, score, win, mk);
+  if (dq == 256 && dv == 256) return pick_256<T, T>(causal, score, win, mk);
   return PrefillChoice{nullptr, 0, 0, 0};
 }
 
@@ -1426,6 +1466,7 @@ PrefillChoice pick_tile_fp8q(int score, bool win) {
   c.bm = 32 * S::NB * S::W;
   c.threads = 64 * S::W;
   c.lds = 2 * (size_t)((D + 127) / 128) * PF_GROUP_BYTES + 2 * (size_t)(D / 64) * PF_GROUP_BYTES + 2 * 64 * (size_t)D;
+  c.vparts = 1;
   return c;
 }
 

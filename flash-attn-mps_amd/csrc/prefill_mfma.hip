@@ -147,6 +147,10 @@ extern "C" int fa_prefill_fwd(const fa_attn_args* a, void* stream) {
       shp.compact = 1;
     }
   }
+  // V column parts: each work item runs as vparts workgroups (blocks is a
+  // multiple of 8, as the kernel's 16-block interleave of the parts needs).
+  shp.vparts = ch.vparts;
+  blocks *= ch.vparts;
   FA_REQUIRE(blocks <= 0x7fffffffll, "fa_prefill_fwd: grid too large");
   hipError_t err = hipFuncSetAttribute((const void*)ch.kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ch.lds);
   if (err != hipSuccess) {
