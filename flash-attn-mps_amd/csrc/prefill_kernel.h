@@ -1333,13 +1333,13 @@ struct PrefillChoice {
 
 // score: 0 plain, 1 softcap, 2 ALiBi, 3 softcap then ALiBi; mk: vLLM
 // mask kind (0 none; instantiated for unpadded head dims without ALiBi, not
-// for E4M3 K/V at d256, whose registers are already spilled).
+// for the one-pass E4M3 256/256 tile: E4M3 d256 masks run as V halves).
 template <typename T, int DQ, int DV, bool CAUSAL, typename S, int DQT, int DVT, typename KT>
 PrefillChoice pick_tile(int score, bool win, int mk) {
   PrefillChoice c;
   const bool cap = score == 1;
   if (mk != 0) {
-    if constexpr (CAUSAL || DQT != DQ || DVT != DV || (KT::id == FA_E4M3 && DQ == 256)) {
+    if constexpr (CAUSAL || DQT != DQ || DVT != DV || (KT::id == FA_E4M3 && DV == 256)) {
       return PrefillChoice{nullptr, 0, 0, 0};
     } else {
       if (score == 2) return PrefillChoice{nullptr, 0, 0, 0};

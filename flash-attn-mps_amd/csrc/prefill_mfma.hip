@@ -65,7 +65,6 @@ bool prefill_ok(const fa_attn_args& a) {
     if (a.mask_kind == 1 && !a.mask_ranges) return false;
     if (a.mask_kind == 2 && (!a.mask_prefix || !a.mask_window_len)) return false;
     if (!((dq == dv && (dq == 64 || dq == 128 || dq == 256)) || (dq == 192 && dv == 128))) return false;
-    if (fp8 && dq == 256) return false;
   }
   // ALiBi (per-head or per-request slopes): any 16-bit head dim alone; with
   // softcap, windows, per-request causality or E4M3 K/V, unpadded 64 / 128 /

@@ -138,12 +138,14 @@ def test_masks_over_pages_and_head_groups(device, mask_name, hq, hkv, page):
     _check(device, q, kc, vc, dtype, f"{mask_name} paged P={page} {hq}/{hkv}", **kw)
 
 
+@pytest.mark.parametrize("d,cap", [(128, 30.0), (256, 30.0), (256, 0.0)])
 @pytest.mark.parametrize("mask_name", ["prefix+window", "rolling window"])
-def test_masks_with_fp8_cache_and_softcap(device, mask_name):
-    """E4M3 K/V with per-(request, KV head) descales and softcap 30."""
-    dtype, d, fp8 = torch.bfloat16, 128, torch.float8_e4m3fn
+def test_masks_with_fp8_cache_and_softcap(device, mask_name, d, cap):
+    """E4M3 K/V with per-(request, KV head) descales, with and without
+    softcap 30 (256-dim heads: the V-half tile)."""
+    dtype, fp8 = torch.bfloat16, torch.float8_e4m3fn
     q_lens, k_lens = [100, 250], [400, 250]
-    q, k, v = _inputs(device, dtype, q_lens, k_lens, 8, 2, d, d, seed=41)
+    q, k, v = _inputs(device, dtype, q_lens, k_lens, 8, 2, d, d, seed=41 + d)
     k8, v8 = (k * 4).to(fp8), (v * 4).to(fp8)
     kd = torch.full((2, 2), 0.25, device=device)
     if mask_name == "rolling window":
@@ -153,9 +155,9 @@ def test_masks_with_fp8_cache_and_softcap(device, mask_name):
         mask = mm_prefix_mask(64)
         aux = [_image_ranges(q_lens, k_lens, [(320, 390), (20, 100)], device), offsets(q_lens, device)]
     kw = dict(_NONE, cu_seqlens_q=offsets(q_lens, device), cu_seqlens_k=offsets(k_lens, device),
-              max_seqlen_q=max(q_lens), max_seqlen_k=max(k_lens), mask_mod=mask, aux_tensors=aux, softcap=30.0,
+              max_seqlen_q=max(q_lens), max_seqlen_k=max(k_lens), mask_mod=mask, aux_tensors=aux, softcap=cap,
               k_descale=kd, v_descale=kd)
-    _check(device, q, k8, v8, dtype, f"{mask_name} E4M3 K/V", **kw)
+    _check(device, q, k8, v8, dtype, f"{mask_name} E4M3 K/V d={d} cap={cap}", **kw)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
