@@ -238,12 +238,15 @@ FA_DEV int64_t request_by_rank(const fa_attn_args& a, int64_t rank, int lane) {
   return (int64_t)__builtin_ctzll(hit);
 }
 
+// V column parts of a tile: 256-dim heads run in 256/128 tiles, each work
+// item as two workgroups, one per 128-column half of V and of the output.
+template <int DQ, int DV> constexpr int prefill_vparts() { return DQ == 256 && DV == 128 ? 2 : 1; }
+
 struct PrefillShape {
   int n_qblocks;
   int log2_page;   // paged K/V: page of position p = p >> log2_page, slot p & (2^log2_page - 1)
   int compact;     // 1: workgroups map onto the compact work list
   int hp;          // query heads per workgroup (1 or 2, dividing the GQA group): W / hp waves per head
-  int vparts;      // V column parts (1, or 2: each work item runs as two workgroups, one per DVT-column half)
 };
 
 // One workgroup's share of the compact work list.  With g = gcd(Hkv, 8),
@@ -394,15 +397,15 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // past a request's end.
   // With hp = 2 a workgroup holds BM / 2 rows of two query heads of one KV
   // head (waves 0 .. W/2-1 the first head), sharing every K/V tile.
-  // V column parts (shp.vparts = 2): the head's V and output columns are two
+  // V column parts (prefill_vparts = 2): the head's V and output columns are two
   // halves of DVT, each a workgroup of its own that recomputes S (a 256-dim
   // head then holds half of O^T, within the 256 registers of two waves per
   // SIMD).  Blocks 16j..16j+7 take half 0 and 16j+8..16j+15 half 1 of work
   // slots 8j..8j+7: both halves of an item run on one XCD, side by side,
   // and their K reads meet in its L2.
-  const bool two_parts = shp.vparts == 2;
-  const int vpart = two_parts ? (int)(blockIdx.x >> 3) & 1 : 0;
-  const int bid = two_parts ? (int)((blockIdx.x >> 4) << 3 | (blockIdx.x & 7)) : (int)blockIdx.x;
+  constexpr bool TWO_PARTS = prefill_vparts<DQ, DV>() == 2;
+  const int vpart = TWO_PARTS ? (int)(blockIdx.x >> 3) & 1 : 0;
+  const unsigned bid = TWO_PARTS ? (blockIdx.x >> 4) << 3 | (blockIdx.x & 7) : blockIdx.x;
   const int G = (int)(a.heads_q / a.heads_k) / shp.hp;
   const int xcd = bid % 8, slot = bid / 8;
   WorkItem wi;
@@ -643,8 +646,8 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   const char* const khead = (const char*)a.k + KEB * (int64_t)kh * a.k_stride[2];
   // (readfirstlane: the part's column offset stays a scalar, as the
   // descriptors built from vhead must)
-  const char* const vhead = (const char*)a.v + KEB * (int64_t)kh * a.v_stride[2] +
-                            __builtin_amdgcn_readfirstlane(vpart * DVT * KEB);
+  const char* vhead = (const char*)a.v + KEB * (int64_t)kh * a.v_stride[2];
+  if constexpr (TWO_PARTS) vhead += __builtin_amdgcn_readfirstlane(vpart * DVT * KEB);
   const uint32_t krow_b = (uint32_t)(KEB * a.k_stride[1]), vrow_b = (uint32_t)(KEB * a.v_stride[1]);
   const uint32_t kpage_b = (uint32_t)(KEB * a.k_stride[0]), vpage_b = (uint32_t)(KEB * a.v_stride[0]);
   const int32_t* const trow = paged ? a.block_table + b * a.bt_stride[0] : nullptr;
@@ -1275,7 +1278,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     if (row < r.q_len) {
       const float inv = lt > 0.0f ? vdsc / lt : 0.0f;
       const int64_t tq = (int64_t)r.q_begin + row;
-      uint16_t* op = (uint16_t*)a.out + tq * a.out_stride[0] + (int64_t)h * a.out_stride[1] + vpart * DVT + 4 * hh;
+      uint16_t* op = (uint16_t*)a.out + tq * a.out_stride[0] + (int64_t)h * a.out_stride[1] + (TWO_PARTS ? vpart * DVT : 0) + 4 * hh;
 #pragma unroll
       for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -1286,7 +1289,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
           w.y = pack2<T>(o[nb][db][4 * g + 2] * inv, o[nb][db][4 * g + 3] * inv);
           *(uint2*)(op + 32 * db + 8 * g) = w;
         }
-      if (hh == 0 && vpart == 0)
+      if (hh == 0 && (!TWO_PARTS || vpart == 0))
         a.lse[(int64_t)h * a.lse_stride[0] + tq * a.lse_stride[1]] = lt > 0.0f ? m_run[nb] * LN2 + logf(lt) : -INFINITY;
     }
   }
@@ -1313,7 +1316,7 @@ template <> struct PrefillTile<128, 128> {
 template <> struct PrefillTile<192, 128> { static constexpr int W = 4, NB = 1, MINB = 2, MINB_WIN = 2; };
 // 256/256 (E4M3 K/V, E4M3 queries): one wave per SIMD (128 KiB of LDS).
 template <> struct PrefillTile<256, 256> { static constexpr int W = 4, NB = 1, MINB = 1, MINB_WIN = 1; };
-// 256-dim 16-bit heads run as two 256/128 halves of V (vparts): eight
+// 256-dim 16-bit heads run as two 256/128 halves of V (prefill_vparts): eight
 // waves in 96 KiB of LDS, two per SIMD.
 template <> struct PrefillTile<256, 128> { static constexpr int W = 8, NB = 1, MINB = 1, MINB_WIN = 1; };
 
@@ -1328,7 +1331,7 @@ struct PrefillChoice {
   PrefillKernel kern;
   int bm, threads;
   size_t lds;
-  int vparts;   // workgroups per work item, one per DV-column part of the head (PrefillShape::vparts)
+  int vparts;   // workgroups per work item, one per DV-column part of the head (prefill_vparts)
 };
 
 // score: 0 plain, 1 softcap, 2 ALiBi, 3 softcap then ALiBi; mk: vLLM
@@ -1380,7 +1383,7 @@ PrefillChoice pick_tile(int score, bool win, int mk) {
   c.bm = 32 * S::NB * S::W;
   c.threads = 64 * S::W;
   c.lds = lds_bytes<DQ, DV>() + (KT::id == FA_E4M3 ? 64 * (size_t)(DQ + DV) : 0);   // + FP8 staging tile
-  c.vparts = 1;
+  c.vparts = prefill_vparts<DQ, DV>();
   return c;
 }
 
@@ -1413,7 +1416,7 @@ PrefillChoice pick_dims_small(int64_t dq, int64_t dv, bool causal, int score, bo
   }
 }
 
-// 256-dim heads: two V-column halves per work item (PrefillShape::vparts),
+// 256-dim heads: two V-column halves per work item (prefill_vparts),
 // each an eight-wave 256/128 tile at two waves per SIMD (the one-pass
 // 256/256 tile holds four waves, one per SIMD, and spills more).  The halves
 // recompute S, with every tanh of a softcap: 16-bit softcaps, and E4M3
@@ -1427,9 +1430,7 @@ template <typename T, typename KT>
 PrefillChoice pick_256(bool causal, int score, bool win, int mk) {
   const bool cap = score == 1 || score == 3;
   if (cap && (KT::id != FA_E4M3 || win)) return pick<T, KT, 256, 256>(causal, score, win, mk);
-  PrefillChoice c = pick<T, KT, 256, 128>(causal, score, win, mk);
-  c.vparts = 2;
-  return c;
+  return pick<T, KT, 256, 128>(causal, score, win, mk);
 }
 
 template <typename T>

@@ -118,6 +118,7 @@ extern "C" int fa_prefill_fwd(const fa_attn_args* a, void* stream) {
   if (a->total_q == 0) return FA_OK;
   FA_REQUIRE(a->max_seqlen_q >= 1, "fa_prefill_fwd: max_seqlen_q must be positive");
   PrefillChoice ch = select_prefill(*a);
+  FA_REQUIRE(ch.kern != nullptr && ch.vparts >= 1, "fa_prefill_fwd: no kernel instance for these arguments");
   PrefillShape shp;
   // Query heads per workgroup: two heads of a KV head share each workgroup's
   // K/V tiles when the GQA group is even.
@@ -148,7 +149,6 @@ extern "C" int fa_prefill_fwd(const fa_attn_args* a, void* stream) {
   }
   // V column parts: each work item runs as vparts workgroups (blocks is a
   // multiple of 8, as the kernel's 16-block interleave of the parts needs).
-  shp.vparts = ch.vparts;
   blocks *= ch.vparts;
   FA_REQUIRE(blocks <= 0x7fffffffll, "fa_prefill_fwd: grid too large");
   hipError_t err = hipFuncSetAttribute((const void*)ch.kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ch.lds);

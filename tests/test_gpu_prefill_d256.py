@@ -1,7 +1,7 @@
 """256-dim MFMA prefill run as two V-column halves vs the fp64 oracle.
 
 fa_prefill_fwd runs 256-dim heads as two workgroups per work item, one per
-128-column half of V and of the output (PrefillShape::vparts in
+128-column half of V and of the output (prefill_vparts in
 prefill_kernel.h; the one-pass 256/256 tile stays for 16-bit softcaps and for
 E4M3 softcaps with a window).  Both halves recompute S; only the first
 writes the LSE.  These cases pin the part decoding against both work-list
