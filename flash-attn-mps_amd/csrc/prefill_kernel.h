@@ -358,7 +358,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   constexpr bool ALIBI_FOLD = ALIBI && !CAP, ALIBI_LATE = ALIBI && CAP;
   constexpr int KEB = KT::bytes;               // bytes per K/V element
   static_assert(!FP8 || (DQT == DQ && DVT == DV && ((DQ == DV && (DQ == 64 || DQ == 128 || DQ == 256)) ||
-                                                      (DQ == 256 && DV == 128 && !FQ))),
+                                                      (DQ == 256 && DV == 128))),
                 "FP8 K/V tiles: 64/128/256-dim heads (256-dim: also as 256/128 V halves)");
   static_assert(!FQ || FP8, "E4M3 queries: E4M3 K/V");
   constexpr int BM = 32 * NB * W;              // query rows per workgroup
@@ -1314,7 +1314,7 @@ template <> struct PrefillTile<128, 128> {
 // second wave per SIMD, at every grid size (one workgroup per CU ran 7-48%
 // slower even on 128-workgroup launches).
 template <> struct PrefillTile<192, 128> { static constexpr int W = 4, NB = 1, MINB = 2, MINB_WIN = 2; };
-// 256/256 (E4M3 K/V, E4M3 queries): one wave per SIMD (128 KiB of LDS).
+// 256/256 (the softcap routes of pick_256): one wave per SIMD (128 KiB of LDS).
 template <> struct PrefillTile<256, 256> { static constexpr int W = 4, NB = 1, MINB = 1, MINB_WIN = 1; };
 // 256-dim 16-bit heads run as two 256/128 halves of V (prefill_vparts): eight
 // waves in 96 KiB of LDS, two per SIMD.
@@ -1450,33 +1450,39 @@ PrefillChoice pick_dims_large(int64_t dq, int64_t dv, bool causal, int score, bo
 }
 
 // E4M3 queries over E4M3 K/V (S on the FP8 MFMA), output type T; head dims
-// 64, 128 and 256.  K tiles hold raw bytes (ceil(DQ / 128) column groups), V
-// is staged twice (64 x DV bytes each) and widened into 16-bit tiles.
-template <typename T, int D, bool CAUSAL>
+// 64, 128 and 256 (256 as two 256/128 V-column halves, every variant: on
+// config 2's lengths at 16/8 heads, one pass -> halves, TFLOP/s: causal 617
+// -> 828, non-causal 715 -> 965, softcap 50 589 -> 655, left window 1023
+// 357 -> 618, softcap + window 415 -> 441).  K tiles hold raw bytes
+// (ceil(DQ / 128) column groups), V is staged twice (64 x DV bytes each) and
+// widened into 16-bit tiles.
+template <typename T, int DQ, int DV, bool CAUSAL>
 PrefillChoice pick_tile_fp8q(int score, bool win) {
-  using S = PrefillTile<D, D>;
+  using S = PrefillTile<DQ, DV>;
   if (score >= 2) return PrefillChoice{nullptr, 0, 0, 0};   // ALiBi with E4M3 queries: the generic kernel
   const bool cap = score == 1;
   PrefillChoice c;
   if (win)
-    c.kern = cap ? prefill_kernel<T, D, D, S::W, S::NB, S::MINB_WIN, CAUSAL, true, true, D, D, E4M3T, false, E4M3T>
-                 : prefill_kernel<T, D, D, S::W, S::NB, S::MINB_WIN, CAUSAL, false, true, D, D, E4M3T, false, E4M3T>;
+    c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB_WIN, CAUSAL, true, true, DQ, DV, E4M3T, false, E4M3T>
+                 : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB_WIN, CAUSAL, false, true, DQ, DV, E4M3T, false, E4M3T>;
   else
-    c.kern = cap ? prefill_kernel<T, D, D, S::W, S::NB, S::MINB, CAUSAL, true, false, D, D, E4M3T, false, E4M3T>
-                 : prefill_kernel<T, D, D, S::W, S::NB, S::MINB, CAUSAL, false, false, D, D, E4M3T, false, E4M3T>;
+    c.kern = cap ? prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, true, false, DQ, DV, E4M3T, false, E4M3T>
+                 : prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false, false, DQ, DV, E4M3T, false, E4M3T>;
   c.bm = 32 * S::NB * S::W;
   c.threads = 64 * S::W;
-  c.lds = 2 * (size_t)((D + 127) / 128) * PF_GROUP_BYTES + 2 * (size_t)(D / 64) * PF_GROUP_BYTES + 2 * 64 * (size_t)D;
-  c.vparts = 1;
+  c.lds = 2 * (size_t)((DQ + 127) / 128) * PF_GROUP_BYTES + 2 * (size_t)(DV / 64) * PF_GROUP_BYTES + 2 * 64 * (size_t)DV;
+  c.vparts = prefill_vparts<DQ, DV>();
   return c;
 }
 
 template <typename T>
 PrefillChoice pick_dims_fp8q(int64_t dq, int64_t dv, bool causal, int score, bool win) {
   if (dq != dv) return PrefillChoice{nullptr, 0, 0, 0};
-  if (dq == 64) return causal ? pick_tile_fp8q<T, 64, true>(score, win) : pick_tile_fp8q<T, 64, false>(score, win);
-  if (dq == 128) return causal ? pick_tile_fp8q<T, 128, true>(score, win) : pick_tile_fp8q<T, 128, false>(score, win);
-  if (dq == 256) return causal ? pick_tile_fp8q<T, 256, true>(score, win) : pick_tile_fp8q<T, 256, false>(score, win);
+  if (dq == 64) return causal ? pick_tile_fp8q<T, 64, 64, true>(score, win) : pick_tile_fp8q<T, 64, 64, false>(score, win);
+  if (dq == 128)
+    return causal ? pick_tile_fp8q<T, 128, 128, true>(score, win) : pick_tile_fp8q<T, 128, 128, false>(score, win);
+  if (dq == 256)
+    return causal ? pick_tile_fp8q<T, 256, 128, true>(score, win) : pick_tile_fp8q<T, 256, 128, false>(score, win);
   return PrefillChoice{nullptr, 0, 0, 0};
 }
 

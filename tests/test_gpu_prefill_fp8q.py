@@ -161,11 +161,13 @@ def test_fp8q_prefill_paged_poisoned_tail(device, page, d):
     assert_parity(out, lse, ref, ref_lse, torch.bfloat16)
 
 
+@pytest.mark.parametrize("d", [128, 256])
 @pytest.mark.parametrize("window", [(-1, -1), (127, 0), (40, -1)])
 @pytest.mark.parametrize("cap", [0.0, 30.0])
-def test_fp8q_prefill_softcap_window_sinks(device, window, cap):
+def test_fp8q_prefill_softcap_window_sinks(device, window, cap, d):
+    """Softcap, windows and sinks; 256-dim heads run as two V-column halves."""
     q_lens, k_lens = [3, 129, 300, 64], [40, 129, 300, 600]
-    q, k, v, qs, ks, vs, cuq, cuk = _packed(device, 128, 8, 2, q_lens, k_lens, seed=int(cap) + window[0] + 50,
+    q, k, v, qs, ks, vs, cuq, cuk = _packed(device, d, 8, 2, q_lens, k_lens, seed=int(cap) + window[0] + 50 + d,
                                             qscale=2.0)
     assert not torch.isnan(q.float()).any()
     sinks = torch.randn(8, generator=torch.Generator().manual_seed(3)).to(device)
@@ -173,7 +175,7 @@ def test_fp8q_prefill_softcap_window_sinks(device, window, cap):
               causal=True, window_size=window, softcap=cap, s_aux=sinks, q_descale=qs, k_descale=ks,
               v_descale=vs)
     assert _route_is_mfma(q, k, v, torch.bfloat16, **kw)
-    out = torch.empty(q.shape[0], 8, 128, dtype=torch.bfloat16, device=device)
+    out = torch.empty(q.shape[0], 8, d, dtype=torch.bfloat16, device=device)
     out, lse = attention(q, k, v, out=out, **kw)
     ref, ref_lse = oracle_attention(q, k, v, cuq, cuk, causal=True, window=window, softcap=cap,
                                     sinks=sinks.cpu(), q_descale=qs, k_descale=ks, v_descale=vs)
