@@ -49,7 +49,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=200)
     p.add_argument("--no-secondary", action="store_true", help="only the headline prefill config")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", default="", help="comma list of secondary configs to run (3,4,5,5_fixed_order,store4,prefill_fp8); config 2 always runs")
+    p.add_argument("--only", default="", help="comma list of secondary configs to run (3,4,5,5_fixed_order,store4,prefill_d256,prefill_fp8); "
+                        "config 2 always runs")
     p.add_argument("--copy-probe", action="store_true",
                    help="first run a known-size copy kernel (reads and writes 1 GiB) that calibrates "
                         "rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -205,6 +206,32 @@ def config2(device, steps, warmup, c=None):
     return dict(lengths=lengths, flops=flops, ms=ms, call_ms=call_ms, kernel_ms=kernel_ms,
                 tflops=flops / (ms * 1e-3) / 1e12, call_tflops=flops / (call_ms * 1e-3) / 1e12,
                 kernel_tflops=flops / (kernel_ms * 1e-3) / 1e12, tensors=(q, k, v, cu))
+
+
+def prefill_d256(device, steps, warmup, c=None):
+    """Config 2's lengths with 256-dim heads (Gemma-like, Hq/Hkv 16/8), bf16
+    0.5*N(0,1) Q/K/V, causal: the 256-dim MFMA prefill, which runs each work
+    item as two workgroups, one per 128-column half of V."""
+    import torch
+    import flash_attn_mps_amd as fa
+    c = c or config2_inputs(device)
+    lengths, cu = c["lengths"], c["cu"]
+    g = torch.Generator().manual_seed(123 + 256)
+    total, hq, hkv, d = sum(lengths), 16, 8, 256
+    q = (torch.randn(total, hq, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
+    k = (torch.randn(total, hkv, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
+    v = (torch.randn(total, hkv, d, generator=g) * 0.5).to(torch.bfloat16).to(device)
+    out = torch.empty_like(q)
+    maxlen = max(lengths)
+
+    def step():
+        fa.flash_attn_varlen_func(q, k, v, cu, cu, maxlen, maxlen, causal=True, out=out)
+
+    ms, call_ms, kernel_ms = time_calls(step, steps, warmup, kernel="fa_prefill_fwd")
+    flops = causal_pairs(lengths, lengths) * hq * 2 * (d + d)
+    return dict(ms=ms, call_ms=call_ms, kernel_ms=kernel_ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12,
+                what="config 2 lengths, Hq/Hkv 16/8, d256 bf16 causal (Gemma-like heads); "
+                     "two V-column halves per work item")
 
 
 def prefill_fp8(device, steps, warmup, c=None, defer=False):
@@ -464,7 +491,10 @@ def cpu_model():
 def secondary_entry(name, r, warmup):
     """The JSON object of one secondary line."""
     entry = {"ms_per_step": round(r["ms"], 4), "warmup": warmup}
-    if name == "prefill_fp8":
+    if name == "prefill_d256":
+        entry.update(TFLOPs=round(r["tflops"], 2), frac_of_bf16_peak=round(r["tflops"] / PEAK_BF16_TFLOPS, 4),
+                     kernel_event_ms=round(r["kernel_ms"], 4), flops=r["flops"], what=r["what"])
+    elif name == "prefill_fp8":
         entry.update(TFLOPs=round(r["tflops"], 2), frac_of_fp8_peak=round(r["tflops"] / PEAK_FP8_TFLOPS, 4),
                      frac_of_mixed_peak=round(r["tflops"] / PEAK_FP8_BF16_MIXED_TFLOPS, 4),
                      kernel_event_ms=round(r["kernel_ms"], 4), flops=r["flops"], what=r["what"])
@@ -515,6 +545,7 @@ def main():
     if not args.no_secondary:
         for name, fn in (("3", config3), ("4", config4), ("store4", store_fp8), ("5", config5),
                          ("5_fixed_order", lambda *x: config5(*x, splits=1)),
+                         ("prefill_d256", lambda *x: prefill_d256(*x, c=c2_inputs)),
                          ("prefill_fp8", lambda *x: prefill_fp8(*x, c=c2_inputs, defer=True))):
             if only and name not in only and not (name == "store4" and "4" in only):
                 continue

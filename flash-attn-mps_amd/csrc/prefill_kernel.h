@@ -401,8 +401,9 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // halves of DVT, each a workgroup of its own that recomputes S (a 256-dim
   // head then holds half of O^T, within the 256 registers of two waves per
   // SIMD).  Blocks 16j..16j+7 take half 0 and 16j+8..16j+15 half 1 of work
-  // slots 8j..8j+7: both halves of an item run on one XCD, side by side,
-  // and their K reads meet in its L2.
+  // slots 8j..8j+7: both halves of an item run on one XCD, next to each
+  // other in dispatch order (their Q and K reads still mostly come from HBM
+  // twice: 1.68x the algorithmic bytes on config 2's lengths at d256).
   constexpr bool TWO_PARTS = prefill_vparts<DQ, DV>() == 2;
   const int vpart = TWO_PARTS ? (int)(blockIdx.x >> 3) & 1 : 0;
   const unsigned bid = TWO_PARTS ? (blockIdx.x >> 4) << 3 | (blockIdx.x & 7) : blockIdx.x;
