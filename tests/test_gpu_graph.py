@@ -159,10 +159,12 @@ def test_graph_vllm_fp8_decode_into_caller_out(device):
         assert torch.equal(out, eager), f"replay {it}"
 
 
-def test_graph_varlen_prefill_with_lse(device):
-    gen = torch.Generator().manual_seed(73)
+@pytest.mark.parametrize("d", [128, 256])
+def test_graph_varlen_prefill_with_lse(device, d):
+    """d 256 runs as two V-column halves (twice the workgroups, one launch)."""
+    gen = torch.Generator().manual_seed(73 + d)
     lengths = [700, 1, 256, 1300, 64]
-    hq, hkv, d = 16, 8, 128
+    hq, hkv = 16, 8
     total = sum(lengths)
     q = torch.randn(total, hq, d, generator=gen).to(torch.bfloat16).to(device)
     k = torch.randn(total, hkv, d, generator=gen).to(torch.bfloat16).to(device)

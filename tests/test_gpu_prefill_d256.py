@@ -153,3 +153,29 @@ def test_d256_halves_paged_mixed_batch(device):
     ref, ref_lse = oracle_attention(q, kc, vc, cuq, used_k=used, block_table=table, causal=True)
     assert_parity(out, lse, ref, ref_lse, torch.bfloat16)
     assert_parity(out, lse, ref, ref_lse, torch.bfloat16, rows=_many_key_rows(q_lens, k_lens))
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, E4M3])
+def test_d256_halves_requests_alone_and_batched(device, kv_dtype):
+    """Each request's rows are bit-identical whether it runs alone or in a
+    batch (the work list and the halves change, a row's arithmetic does not).
+    Every request has two or more query rows: single-query requests take the
+    decode kernel, whose default split plan depends on the batch (its
+    fixed-order route is the batch-invariant one, tested elsewhere)."""
+    g = torch.Generator().manual_seed(2560)
+    q_lens, k_lens = [300, 2, 129, 700, 64], [300, 40, 129, 900, 64]
+    hq, hkv = 16, 8
+    q = (torch.randn(sum(q_lens), hq, 256, generator=g) * 0.5).to(torch.bfloat16).to(device)
+    k = (torch.randn(sum(k_lens), hkv, 256, generator=g) * 0.5).to(kv_dtype).to(device)
+    v = (torch.randn(sum(k_lens), hkv, 256, generator=g) * VALUE_SCALE).to(kv_dtype).to(device)
+    cuq, cuk = offsets(q_lens, device), offsets(k_lens, device)
+    out, lse = attention(q, k, v, cu_seqlens_q=cuq, cu_seqlens_k=cuk, max_seqlen_q=max(q_lens),
+                         max_seqlen_k=max(k_lens), causal=True)
+    qo, ko = 0, 0
+    for i, (n, m) in enumerate(zip(q_lens, k_lens)):
+        one_q, one_k = offsets([n], device), offsets([m], device)
+        o1, l1 = attention(q[qo:qo + n], k[ko:ko + m], v[ko:ko + m], cu_seqlens_q=one_q, cu_seqlens_k=one_k,
+                           max_seqlen_q=n, max_seqlen_k=m, causal=True)
+        assert torch.equal(o1, out[qo:qo + n]), f"request {i}: output"
+        assert torch.equal(l1, lse[:, qo:qo + n]), f"request {i}: LSE"
+        qo, ko = qo + n, ko + m
