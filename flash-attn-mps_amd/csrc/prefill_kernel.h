@@ -1356,10 +1356,10 @@ PrefillChoice pick_tile(int score, bool win, int mk) {
     }
   } else if (score >= 2) {   // ALiBi (3: after a softcap)
     // With windows, softcap or E4M3 K/V: unpadded 64 / 128 / 256-dim heads
-    // (E4M3 K/V: 64 / 128).
+    // (E4M3 K/V at d256 on the V-half tile only).
     constexpr bool MORE = DQT == DQ && DVT == DV &&
                           ((DQ == DV && (DQ == 64 || DQ == 128 || DQ == 256)) || (DQ == 256 && DV == 128)) &&
-                          !(KT::id == FA_E4M3 && DQ == 256);
+                          !(KT::id == FA_E4M3 && DV == 256);
     const bool capa = score == 3;
     if (!capa && !win && KT::id != FA_E4M3) {
       c.kern = prefill_kernel<T, DQ, DV, S::W, S::NB, S::MINB, CAUSAL, false, false, DQT, DVT, KT, true>;
@@ -1421,7 +1421,8 @@ PrefillChoice pick_dims_small(int64_t dq, int64_t dv, bool causal, int score, bo
 // each an eight-wave 256/128 tile at two waves per SIMD (the one-pass
 // 256/256 tile holds four waves, one per SIMD, and spills more).  The halves
 // recompute S, with every tanh of a softcap: 16-bit softcaps, and E4M3
-// softcaps with a window, keep the one-pass tile.  Measured on config 2's
+// softcaps with a window and no ALiBi, keep the one-pass tile (which has no
+// E4M3 ALiBi instance).  Measured on config 2's
 // lengths at 16/8 heads (TFLOP/s, one-pass -> halves): bf16 causal 456 ->
 // 597, non-causal 629 -> 716, ALiBi 404 -> 519, left window 1023 260 -> 292,
 // vLLM mm_prefix +36%, rswa +8%, softcap 50 560 -> 519, softcap + window
@@ -1430,7 +1431,7 @@ PrefillChoice pick_dims_small(int64_t dq, int64_t dv, bool causal, int score, bo
 template <typename T, typename KT>
 PrefillChoice pick_256(bool causal, int score, bool win, int mk) {
   const bool cap = score == 1 || score == 3;
-  if (cap && (KT::id != FA_E4M3 || win)) return pick<T, KT, 256, 256>(causal, score, win, mk);
+  if (cap && (KT::id != FA_E4M3 || (win && score == 1))) return pick<T, KT, 256, 256>(causal, score, win, mk);
   return pick<T, KT, 256, 128>(causal, score, win, mk);
 }
 

@@ -68,11 +68,10 @@ bool prefill_ok(const fa_attn_args& a) {
   }
   // ALiBi (per-head or per-request slopes): any 16-bit head dim alone; with
   // softcap, windows, per-request causality or E4M3 K/V, unpadded 64 / 128 /
-  // 256-dim heads (E4M3 K/V 64 / 128); not with E4M3 queries.
+  // 256-dim heads; not with E4M3 queries.
   if (a.alibi) {
     if (fp8q) return false;
-    if ((a.softcap > 0.0f || window_set(a) || fp8) &&
-        !(dq == dv && (dq == 64 || dq == 128 || (dq == 256 && !fp8))))
+    if ((a.softcap > 0.0f || window_set(a) || fp8) && !(dq == dv && (dq == 64 || dq == 128 || dq == 256)))
       return false;
   }
   const int kb = fp8 ? 1 : 2;   // K/V bytes per element

@@ -242,10 +242,12 @@ int fa_decode_fwd(const fa_attn_args* args, void* stream);
 #define FA_DECODE_SCRATCH_BYTES (32ll << 20)
 int fa_decode_fwd_noalloc(const fa_attn_args* args, void* stream);
 
-/* MFMA prefill (bf16/fp16 queries; bf16/fp16 or FP8 E4M3 K/V with
- * descales; causal, per-request causal, windows, softcap, sinks, and ALiBi
- * without softcap, windows, per-request causality or FP8; head dims 32-256
- * and 192/128).  fa_prefill_supported() says whether the argument
+/* MFMA prefill (bf16/fp16 queries over bf16/fp16 or FP8 E4M3 K/V with
+ * descales, or E4M3 queries over E4M3 K/V; causal, per-request causal,
+ * windows, softcap, sinks, vLLM mask kinds 1 and 2, and ALiBi, which
+ * combines with softcap, windows, per-request causality and E4M3 K/V at
+ * unpadded 64/128/256-dim heads; head dims 32-256 and 192/128).
+ * fa_prefill_supported() says whether the argument
  * combination is compiled in.  With FA_FLAG_SKIP_SINGLE_QUERY in
  * args->flags, requests with one query row are left untouched for
  * fa_decode_fwd (no reference counterpart: the reference runs such rows

@@ -6,7 +6,7 @@ oracle/attention.py:109-112 restates that).  Covered: causal and non-causal,
 per-head [Hq] and per-request [B, Hq] slopes, GQA with and without head
 packing, packed and paged K/V, q_len != k_len, sinks, BLOOM-sized slopes on
 long keys, ALiBi after a softcap, with windows, per-request causality and
-E4M3 K/V (64/128/256-dim heads; E4M3 64/128), negative and zero score
+E4M3 K/V (64/128/256-dim heads, E4M3 K/V too), negative and zero score
 scales, and that the MFMA kernel is the route taken (padded head dims keep
 the combinations on the generic kernel).  Tolerances: max-abs <= 2e-3 fp16,
 <= 1e-2 bf16, LSE <= 1e-4.
@@ -124,13 +124,13 @@ COMBOS = ["softcap", "window", "softcap+window", "per-request causal", "fp8", "f
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("d,extra", [(d, e) for d in (64, 128, 256) for e in COMBOS
-                                     if not (d == 256 and e.startswith("fp8"))])
+@pytest.mark.parametrize("d,extra", [(d, e) for d in (64, 128, 256) for e in COMBOS])
 def test_alibi_combinations_on_the_mfma_prefill(device, dtype, d, extra):
     """ALiBi after a softcap (softcap(score) - slope |diff|), with left / right
     windows, per-request causality and E4M3 K/V with descales
     (kernels/attention.metal:47-51, 84-87; the reference applies the bias in
-    every kernel).  E4M3 K/V take it at 64- and 128-dim heads."""
+    every kernel).  E4M3 K/V take it at every head dim (256: the V-half
+    tile, also with a softcap and a window)."""
     q_lens, k_lens = [70, 300, 1], [200, 300, 40]
     q, k, v, cuq, cuk = _case(device, dtype, d, 8, 2, q_lens, k_lens, seed=d + len(extra))
     v = v * 0.5
