@@ -116,6 +116,11 @@ template <> FA_DEV uint32_t widen_fp8_pair<F16T, false>(uint32_t w) {
 template <> FA_DEV uint32_t widen_fp8_pair<F16T, true>(uint32_t w) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true));
 }
+// w with its two 8-byte halves exchanged when `swap` (one select per dword).
+FA_DEV u32x4 halves_swapped_if(u32x4 w, int swap) {
+  return swap ? u32x4{w[2], w[3], w[0], w[1]} : w;
+}
+
 // 16 E4M3 codes -> 16 T values (dims 0..7 in lo, 8..15 in hi).
 template <typename T>
 FA_DEV void widen_fp8_16(u32x4 w, u32x4& lo, u32x4& hi) {
@@ -759,7 +764,9 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // distinct slots: K rows r and r + 1 share a swizzle, so odd keys write
   // their upper half first; V rows are 64 bytes, so the second block of the
   // pair writes its upper half first.  (A mapping by consecutive staging
-  // chunks conflicted 2-4 ways on K and 4-8 ways on V writes.)  The
+  // chunks conflicted 2-4 ways on K and 4-8 ways on V writes.)  The lane
+  // swaps the two 8-byte halves of its staging chunk before converting (4
+  // selects), rather than the two converted halves after it (8).  The
   // addresses derive from an opaque copy of t so that none of them is held
   // in registers across the main loop.
   static_assert(!FP8 || (DQ % (16 * W) == 0 && DV % (16 * W) == 0), "FP8 widening: whole groups per pass");
@@ -770,11 +777,12 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     for (int it = 0; it < DQ / (16 * W); ++it) {
       const int q = (it * GPI + (t >> 4)) / NG;
       const int r = 4 * q + (l16 >> 2), u = 4 * g + m, rho = sigma(r), sw = (rho >> 1) & 7, up = r & 1;
-      u32x4 lo, hi;
-      widen_fp8_16<T>(*(const u32x4*)(stk + r * DQ + 16 * (u ^ stage_rows<DQ>(r))), lo, hi);
+      u32x4 first, second;
+      widen_fp8_16<T>(halves_swapped_if(*(const u32x4*)(stk + r * DQ + 16 * (u ^ stage_rows<DQ>(r))), up), first,
+                      second);
       char* const row = kbuf0 + buf * KTILE + g * PF_GROUP_BYTES + rho * 128;
-      *(u32x4*)(row + ((2 * m + up) ^ sw) * 16) = up ? hi : lo;
-      *(u32x4*)(row + ((2 * m + 1 - up) ^ sw) * 16) = up ? lo : hi;
+      *(u32x4*)(row + ((2 * m + up) ^ sw) * 16) = first;
+      *(u32x4*)(row + ((2 * m + 1 - up) ^ sw) * 16) = second;
     }
   };
   auto widen_v_rows = [&](int t, const char* stage, int buf) {
@@ -784,11 +792,12 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
 #pragma unroll
     for (int it = 0; it < DV / (16 * W); ++it) {
       const int r = 4 * ((it * GPI + (t >> 4)) / NC) + (l16 >> 2);
-      u32x4 lo, hi;
-      widen_fp8_16<T>(*(const u32x4*)(stage + r * DV + 16 * (u ^ stage_rows<DV>(r))), lo, hi);
+      u32x4 first, second;
+      widen_fp8_16<T>(halves_swapped_if(*(const u32x4*)(stage + r * DV + 16 * (u ^ stage_rows<DV>(r))), up), first,
+                      second);
       char* const dst = vbuf0 + buf * VTILE + blk * PF_VBLOCK_BYTES + r * 64 + 32 * h;
-      *(u32x4*)(dst + 16 * up) = up ? hi : lo;
-      *(u32x4*)(dst + 16 * (1 - up)) = up ? lo : hi;
+      *(u32x4*)(dst + 16 * up) = first;
+      *(u32x4*)(dst + 16 * (1 - up)) = second;
     }
   };
   // E4M3 queries: staging slot -> V buffer buf.
