@@ -905,8 +905,14 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // With ALiBi the accumulators start at the key's bias, so the MFMAs add
   // the dot product onto it: -sl |x| with x = key - qa, which is sl x on
   // every key a causal row sees (keys past the row are masked later).
-  auto qk = [&](int st, f32x16 (&s)[NB]) {
-    const char* kl = kbuf0 + ((st >> 1) & 1) * KTILE + (st & 1) * 32 * 128;
+  // par: std::integral_constant<int, 2 p + e> when stage st is known to be
+  // half e of a tile in K/V buffer p (the LDS reads then take the stage's
+  // rows as immediate offsets), or <int, -1> (from st at run time).
+  auto qk = [&](int st, f32x16 (&s)[NB], auto par) {
+    constexpr int PAR = decltype(par)::value;
+    const char* kl;
+    if constexpr (PAR < 0) kl = kbuf0 + ((st >> 1) & 1) * KTILE + (st & 1) * 32 * 128;
+    else kl = kbuf0 + (PAR >> 1) * KTILE + (PAR & 1) * 32 * 128;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       if constexpr (ALIBI_FOLD) {
@@ -1023,8 +1029,11 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
       }
     }
   };
-  auto pv = [&](int st, const u32x4 (&pop)[NB][2]) {
-    const char* vl = vbuf0 + ((st >> 1) & 1) * VTILE + (st & 1) * 32 * 64;
+  auto pv = [&](int st, const u32x4 (&pop)[NB][2], auto par) {
+    constexpr int PAR = decltype(par)::value;
+    const char* vl;
+    if constexpr (PAR < 0) vl = vbuf0 + ((st >> 1) & 1) * VTILE + (st & 1) * 32 * 64;
+    else vl = vbuf0 + (PAR >> 1) * VTILE + (PAR & 1) * 32 * 64;
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -1037,6 +1046,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
         for (int nb = 0; nb < NB; ++nb) o[nb][db] = mfma32<T>(av, pop[nb][c], o[nb][db]);
       }
   };
+  const std::integral_constant<int, -1> at_run_time;
   auto rescale_o = [&](const float (&f)[NB]) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
@@ -1093,14 +1103,22 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
   // Steady state: stage st and st+1 both active, st+1 unmasked.  One
   // straight scheduling region: phase B(st) under the MFMAs of S(st+1),
   // phase A(st+1) under the MFMAs of P.V(st).
-  auto step_hot = [&](auto mode, int st, f32x16 (&sc)[NB], f32x16 (&sn)[NB], float (&f)[NB])
+  // par: stage st's parities, as for qk / pv.
+  auto step_hot = [&](auto mode, auto par, int st, f32x16 (&sc)[NB], f32x16 (&sn)[NB], float (&f)[NB])
                       __attribute__((always_inline)) {
     tile_start(mode, st);
     rescale_o(f);
     u32x4 pop[NB][2];
     phase_b(sc, pop);
-    qk(st + 1, sn);
-    pv(st, pop);
+    constexpr int PAR = decltype(par)::value;
+    if constexpr (PAR < 0) {
+      qk(st + 1, sn, at_run_time);
+    } else {
+      // stage st + 1: the other half, in the next buffer after a second half
+      constexpr int P = PAR >> 1, E = PAR & 1;
+      qk(st + 1, sn, std::integral_constant<int, 2 * (E ? P ^ 1 : P) + (E ^ 1)>());
+    }
+    pv(st, pop, par);
     if constexpr (!CAP) {
       // Phase A proper (the row max across the lane pair, the rescale factor,
       // the running max and sum) runs only when some lane holds a score past
@@ -1145,14 +1163,14 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
         rescale_o(f);
         phase_b(sc, pop);
       }
-      qk(st + 1, sn);
-      if (act) pv(st, pop);
+      qk(st + 1, sn, at_run_time);
+      if (act) pv(st, pop, at_run_time);
     } else {
       if (!act) return;
       rescale_o(f);
       phase_b(sc, pop);
-      qk(st + 1, sn);
-      pv(st, pop);
+      qk(st + 1, sn, at_run_time);
+      pv(st, pop, at_run_time);
     }
     if (needs_mask(st + 1)) phase_a(std::integral_constant<bool, true>(), st + 1, sn, act_n, f);
     else phase_a(std::integral_constant<bool, false>(), st + 1, sn, act_n, f);
@@ -1196,7 +1214,7 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) f[nb] = 1.0f;
     if (active(st0)) {
-      qk(st0, sa);
+      qk(st0, sa, at_run_time);
       phase_a(std::integral_constant<bool, true>(), st0, sa, true, f);
     }
     // Even stage st holds S in sa, odd in sb.  The unmasked two-stage loop
@@ -1206,9 +1224,10 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
     int st = st0;
     if constexpr (GEN) {
       auto run_hot = [&](auto mode) {
+        const std::integral_constant<int, -1> rt;
         for (; hot(st + 1) && hot(st + 2) && dma_full(st >> 1); st += 2) {
-          step_hot(mode, st, sa, sb, f);
-          step_hot(mode, st + 1, sb, sa, f);
+          step_hot(mode, rt, st, sa, sb, f);
+          step_hot(mode, rt, st + 1, sb, sa, f);
         }
       };
       while (st < n_stages) {
@@ -1231,10 +1250,38 @@ __global__ __launch_bounds__(64 * W, MINB) void prefill_kernel(const fa_attn_arg
       int hb = min(n_stages, r.k_len / 32);
       if constexpr (CAUSAL) hb = min(hb, max(wave_qabs_lo + 1, 0) / 32);
       const int lim = wave_rows ? min(hb - 2, 2 * jmax + 1) : INT_MIN;
+      // 64-dim 16-bit tiles: two tiles per iteration, so every stage's K/V
+      // buffer and half are constants (immediate LDS offsets instead of a
+      // VALU add per operand address): one loop per buffer of the first
+      // tile, then the last odd tile with run-time parities.  Same process
+      // on config 2's lengths at 32/8 heads: causal 770 -> 812 TFLOP/s.  The
+      // 128-dim tile ran 5.5-6.5% slower that way (config 2 948 -> 896,
+      // non-causal 1078 -> 1005, with 5 fewer VALU instructions per stage),
+      // so the other tiles keep one tile per iteration (E4M3 K/V also need
+      // their staging refill addresses scalar).
       auto run_hot = [&](auto mode) {
-        for (; st < lim; st += 2) {
-          step_hot(mode, st, sa, sb, f);
-          step_hot(mode, st + 1, sb, sa, f);
+        const std::integral_constant<int, -1> rt;
+        if constexpr (FP8 || DQ != 64) {
+          for (; st < lim; st += 2) {
+            step_hot(mode, rt, st, sa, sb, f);
+            step_hot(mode, rt, st + 1, sb, sa, f);
+          }
+        } else {
+          auto two_tiles = [&](auto p0, auto p1) {
+            for (; st + 2 < lim; st += 4) {
+              step_hot(mode, std::integral_constant<int, 2 * decltype(p0)::value>(), st, sa, sb, f);
+              step_hot(mode, std::integral_constant<int, 2 * decltype(p0)::value + 1>(), st + 1, sb, sa, f);
+              step_hot(mode, std::integral_constant<int, 2 * decltype(p1)::value>(), st + 2, sa, sb, f);
+              step_hot(mode, std::integral_constant<int, 2 * decltype(p1)::value + 1>(), st + 3, sb, sa, f);
+            }
+          };
+          if (((st >> 1) & 1) == 0) two_tiles(std::integral_constant<int, 0>(), std::integral_constant<int, 1>());
+          else two_tiles(std::integral_constant<int, 1>(), std::integral_constant<int, 0>());
+          if (st < lim) {
+            step_hot(mode, rt, st, sa, sb, f);
+            step_hot(mode, rt, st + 1, sb, sa, f);
+            st += 2;
+          }
         }
       };
       if (active(st)) {
